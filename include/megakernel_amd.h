@@ -1,0 +1,121 @@
+/*
+ * megakernel_amd.h -- C ABI of the MI355X (gfx950) batch-1 decode mega-kernel.
+ *
+ * Plain pointers and sizes only; no torch types. Every entry point returns a hipError_t and
+ * never throws. Device pointers refer to memory on the current HIP device.
+ *
+ * Reference interface this replaces: the extern "C" launcher of tejeshbhalla/mega-kernel,
+ * declared at /root/reference/pytorch_binding.cu:9-33 and defined at
+ * /root/reference/megakernel.cu:898-994, bound only by the pybind `decode` operator
+ * (/root/reference/pytorch_binding.cu:36-129).
+ */
+#ifndef MEGAKERNEL_AMD_H_
+#define MEGAKERNEL_AMD_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Per-layer weight table: 11 device pointers to bf16 tensors in the reference's order.
+ * Same layout as the reference's `LayerWeights` (/root/reference/config.cuh:77-89), filled from
+ * the flat 11-per-layer list built at /root/reference/model.py:30-44.
+ *   norm_weight [H], q_weight [16*128, H], k_weight [8*128, H], v_weight [8*128, H],
+ *   q_norm_weight [128], k_norm_weight [128], o_proj_weight [H, 16*128],
+ *   post_attn_norm_weight [H], gate_proj_weight [I, H], up_proj_weight [I, H],
+ *   down_proj_weight [H, I]
+ */
+typedef struct mk_layer_weights {
+  const void* norm_weight;
+  const void* q_weight;
+  const void* k_weight;
+  const void* v_weight;
+  const void* q_norm_weight;
+  const void* k_norm_weight;
+  const void* o_proj_weight;
+  const void* post_attn_norm_weight;
+  const void* gate_proj_weight;
+  const void* up_proj_weight;
+  const void* down_proj_weight;
+} mk_layer_weights;
+
+/* Model shape. Head geometry is fixed at 16 query heads, 8 K/V heads, head_dim 128 (Qwen3 0.6B
+ * and 1.7B). Supported (hidden, intermediate): (1024, 3072) and (2048, 6144). The reference
+ * fixes these as compile-time constants (/root/reference/config.cuh:9-18). */
+typedef struct mk_model_dims {
+  int32_t hidden;
+  int32_t intermediate;
+  int32_t num_layers;
+  int32_t vocab;
+} mk_model_dims;
+
+/*
+ * Drop-in for the reference launcher `launch_decode_kernel`
+ * (/root/reference/megakernel.cu:898-994; declaration /root/reference/pytorch_binding.cu:9-33).
+ * Same arguments, same meaning, Qwen3-0.6B shape (hidden 1024, intermediate 3072, 28 layers,
+ * vocab 151936) as in the reference:
+ *   layer_weights  device pointer to mk_layer_weights[28]
+ *   k_cache/v_cache [28, 8, max_seq_len, 128] bf16; the new K/V are written at `position`
+ *   cache_len      must equal position + 1 (the reference always passes that)
+ *   g_logits       fp32 [151936] output
+ * The remaining scratch pointers (hidden_buffer ... g_v) are accepted for ABI compatibility and
+ * not used: the kernel keeps its exchange buffers in a per-device workspace owned by the library
+ * and allocated on first use. Returns hipErrorInvalidValue for a null pointer, token/position out
+ * of range or cache_len != position + 1, otherwise the status of the cooperative launch.
+ */
+hipError_t launch_decode_kernel(int token_id, const void* embed_weight, const void* lm_head_weight,
+                                const void* final_norm_weight, const void* layer_weights,
+                                const void* cos_table, const void* sin_table, void* k_cache,
+                                void* v_cache, void* hidden_buffer, void* g_residual,
+                                void* g_activations, void* g_attn_output, void* g_normalized,
+                                void* g_mlp_intermediate, void* g_logits, void* g_q, void* g_k,
+                                void* g_v, int position, int cache_len, int max_seq_len,
+                                hipStream_t stream);
+
+/*
+ * Shape-general form of the same operation (same reference counterpart as above; the reference
+ * has one compile-time shape, this takes it at run time). Writes fp32 logits [vocab] and, when
+ * out_token is not NULL, the greedy token (argmax over bf16-rounded logits, lowest index on ties)
+ * as int32 to device memory, so a caller needs no separate argmax kernel.
+ * Argument errors return hipErrorInvalidValue before anything is launched.
+ */
+hipError_t mk_decode(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                     const void* lm_head_weight, const void* final_norm_weight,
+                     const void* layer_weights, const void* cos_table, const void* sin_table,
+                     void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
+                     int32_t* out_token, hipStream_t stream);
+
+/* Device status word of the current device's workspace (0 = healthy; bit 0 = a grid wait timed
+ * out, results of that launch are invalid). Synchronizes with the device. No reference
+ * counterpart: the reference surfaces errors only through the launch status. */
+hipError_t mk_status(uint32_t* status);
+
+/* Clears the status word and the workspace's barrier counters of the current device.
+ * Synchronizes with the device. No reference counterpart. */
+hipError_t mk_reset(void);
+
+/* Phase tracing (profiling builds and tools; no reference counterpart -- the reference has no
+ * in-kernel timers). With a non-NULL device buffer of at least mk_trace_bytes() bytes, every later
+ * launch on the current device writes, per workgroup, s_memrealtime stamps (100 MHz) at each
+ * phase start and barrier arrival: uint64 [grid][TRACE_N], TRACE_N = mk_trace_bytes() / 8 / grid,
+ * slot 10*layer + 2*phase (+1 for arrival) for phases A..E, tail slots 640.. for embedding, final
+ * norm, LM head and exit. NULL turns tracing off. */
+hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes);
+size_t mk_trace_bytes(void);
+
+/* Number of workgroups (one per CU) the cooperative launch uses on the current device, or a
+ * negative value if the device cannot run the kernel. No reference counterpart (the reference
+ * hard-codes 82 blocks, /root/reference/config.cuh:27). */
+int mk_grid_size(void);
+
+/* Library version string. */
+const char* mk_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGAKERNEL_AMD_H_ */

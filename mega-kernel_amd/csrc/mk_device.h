@@ -1,0 +1,134 @@
+// Device primitives for the gfx950 decode mega-kernel: bf16 unpacking, coherent (device-scope)
+// loads/stores for cross-workgroup exchange, wave64 reductions and bounded spin waits.
+//
+// Replaces the warp32 helpers of /root/reference/config.cuh:93-179 (shuffle trees, block sums,
+// silu). Everything here is written for CDNA4: 64-lane waves, DPP row operations for 16-lane
+// groups, ds_bpermute to cross rows, and the gfx950 cache-policy bits (sc1 = device
+// scope) for memory that other workgroups -- possibly on another XCD with its own L2 -- read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mk {
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (finite inputs; NaN keeps a quiet NaN pattern).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// dot of 8 bf16 weights (one 16-byte chunk) with 8 fp32 activations, accumulated into acc.
+__device__ __forceinline__ float dot8(uint4 w, const float* x, float acc) {
+  acc = fmaf(bf16_lo(w.x), x[0], acc);
+  acc = fmaf(bf16_hi(w.x), x[1], acc);
+  acc = fmaf(bf16_lo(w.y), x[2], acc);
+  acc = fmaf(bf16_hi(w.y), x[3], acc);
+  acc = fmaf(bf16_lo(w.z), x[4], acc);
+  acc = fmaf(bf16_hi(w.z), x[5], acc);
+  acc = fmaf(bf16_lo(w.w), x[6], acc);
+  acc = fmaf(bf16_hi(w.w), x[7], acc);
+  return acc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Memory access with explicit cache policy.
+//
+// On MI355X each XCD has its own L2. A plain store can sit dirty in the writer's L2; a plain
+// load can hit a stale line in the reader's L1/L2. Device-scope ("sc1") stores write through to
+// the memory side and device-scope loads never return a stale copy, so every buffer that one
+// workgroup writes and another reads within a launch goes through these helpers.
+// ---------------------------------------------------------------------------------------------
+constexpr int CPOL_SC1 = 16;  // gfx940+ cache-policy bit: device (agent) scope
+constexpr int CPOL_NT = 2;    // non-temporal (streaming) hint
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev_f32(const float* p) {
+  return __uint_as_float(ld_dev_u32(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ void st_dev_f32(float* p, float v) {
+  st_dev_u32(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+// 16-byte device-scope load/store; byte offset from a 16-byte aligned base.
+__device__ __forceinline__ float4 ld_dev_f32x4(const float* base, uint32_t byte_off) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 r = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(base), byte_off, 0, CPOL_SC1));
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+__device__ __forceinline__ void st_dev_f32x4(float* base, uint32_t byte_off, float4 v) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  u4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), byte_off, 0, CPOL_SC1);
+}
+
+// Weight stream: 16 bytes, non-temporal (each weight byte is read once per token).
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Wait until every outstanding vector-memory operation of this wave has completed (stores
+// acknowledged), so a following signal cannot overtake the data it announces.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------------------------------------
+// wave64 reductions (DPP inside 16-lane rows, ds_bpermute across rows)
+// ---------------------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum over each 16-lane row; every lane of the row receives the row total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+// Full wave sum / max; every lane receives the result.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ unsigned xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // HW_REG_XCC_ID[3:0]
+}
+
+}  // namespace mk

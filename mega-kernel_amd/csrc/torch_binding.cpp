@@ -1,0 +1,180 @@
+// PyTorch-ROCm operator for the decode mega-kernel: the drop-in for the reference's pybind
+// `decode` (/root/reference/pytorch_binding.cu:36-129, registered at :132-134).
+//
+// Same Python signature and meaning:
+//   decode(token_id, embed_weight, lm_head_weight, final_norm_weight, layer_weights,
+//          cos_table, sin_table, k_cache, v_cache, position, max_seq_len) -> fp32 logits [V]
+// writes the new K/V at `position`, attends over [0, position], returns fresh logits.
+//
+// Differences by design: every argument is validated before any HIP call (the reference checks
+// none); the per-layer weight table is built once per distinct set of weight tensors and kept on
+// the device (the reference mallocs, uploads and frees it on every token); the call is fully
+// asynchronous on the current stream (the reference's cudaFree synchronizes). `decode_greedy`
+// additionally returns the fused device argmax, and the model shape (0.6B or 1.7B) is taken
+// from the tensors instead of compile-time constants.
+#include <torch/extension.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/megakernel_amd.h"
+
+namespace {
+
+constexpr int kPerLayer = 11;
+constexpr int kHeadDim = 128, kQHeads = 16, kKVHeads = 8;
+
+#define MK_HIP_CHECK(expr)                                                                 \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    TORCH_CHECK(e_ == hipSuccess, "megakernel: ", #expr, " failed: ", hipGetErrorString(e_)); \
+  } while (0)
+
+// Device-resident LayerWeights table, rebuilt only when the weight tensors change. Holds
+// references to the tensors so the cached pointers cannot dangle.
+struct TableCache {
+  std::vector<torch::Tensor> held;
+  std::vector<const void*> ptrs;
+  torch::Tensor table;  // uint8 on device, num_layers * sizeof(mk_layer_weights)
+};
+std::mutex g_mu;
+std::vector<TableCache> g_tables(64);
+
+void check_bf16(const torch::Tensor& t, const char* name, at::IntArrayRef shape, const torch::Device& dev) {
+  TORCH_CHECK(t.defined(), "megakernel: ", name, " is undefined");
+  TORCH_CHECK(t.device() == dev, "megakernel: ", name, " must be on ", dev, ", got ", t.device());
+  TORCH_CHECK(t.scalar_type() == torch::kBFloat16, "megakernel: ", name, " must be bfloat16, got ", t.scalar_type());
+  TORCH_CHECK(t.is_contiguous(), "megakernel: ", name, " must be contiguous");
+  TORCH_CHECK(t.sizes() == shape, "megakernel: ", name, " must have shape ", shape, ", got ", t.sizes());
+}
+
+struct Checked {
+  mk_model_dims dims;
+  torch::Device dev{torch::kCPU};
+};
+
+Checked validate(int64_t token_id, const torch::Tensor& embed, const torch::Tensor& lm_head,
+                 const torch::Tensor& final_norm, const std::vector<torch::Tensor>& lw,
+                 const torch::Tensor& cos, const torch::Tensor& sin, const torch::Tensor& kc,
+                 const torch::Tensor& vc, int64_t position, int64_t max_seq_len) {
+  TORCH_CHECK(embed.defined() && embed.is_cuda(), "megakernel: embed_weight must be a GPU tensor");
+  TORCH_CHECK(embed.dim() == 2, "megakernel: embed_weight must be [vocab, hidden]");
+  const torch::Device dev = embed.device();
+  const int64_t V = embed.size(0), H = embed.size(1);
+  TORCH_CHECK(lw.size() % kPerLayer == 0 && !lw.empty(),
+              "megakernel: layer_weights must hold 11 tensors per layer, got ", lw.size());
+  const int64_t L = lw.size() / kPerLayer;
+  TORCH_CHECK(lw[8].dim() == 2, "megakernel: gate_proj weight must be 2-D");
+  const int64_t I = lw[8].size(0);
+  TORCH_CHECK((H == 1024 && I == 3072) || (H == 2048 && I == 6144),
+              "megakernel: supported (hidden, intermediate) are (1024, 3072) and (2048, 6144), got (", H, ", ", I, ")");
+  check_bf16(embed, "embed_weight", {V, H}, dev);
+  check_bf16(lm_head, "lm_head_weight", {V, H}, dev);
+  check_bf16(final_norm, "final_norm_weight", {H}, dev);
+  const int64_t Q = kQHeads * kHeadDim, KV = kKVHeads * kHeadDim;
+  for (int64_t l = 0; l < L; ++l) {
+    const torch::Tensor* t = &lw[l * kPerLayer];
+    check_bf16(t[0], "input_layernorm", {H}, dev);
+    check_bf16(t[1], "q_proj", {Q, H}, dev);
+    check_bf16(t[2], "k_proj", {KV, H}, dev);
+    check_bf16(t[3], "v_proj", {KV, H}, dev);
+    check_bf16(t[4], "q_norm", {kHeadDim}, dev);
+    check_bf16(t[5], "k_norm", {kHeadDim}, dev);
+    check_bf16(t[6], "o_proj", {H, Q}, dev);
+    check_bf16(t[7], "post_attention_layernorm", {H}, dev);
+    check_bf16(t[8], "gate_proj", {I, H}, dev);
+    check_bf16(t[9], "up_proj", {I, H}, dev);
+    check_bf16(t[10], "down_proj", {H, I}, dev);
+  }
+  TORCH_CHECK(max_seq_len >= 1, "megakernel: max_seq_len must be positive");
+  check_bf16(cos, "cos_table", {cos.size(0), kHeadDim}, dev);
+  check_bf16(sin, "sin_table", {sin.size(0), kHeadDim}, dev);
+  TORCH_CHECK(cos.size(0) >= max_seq_len && sin.size(0) >= max_seq_len,
+              "megakernel: cos/sin tables need at least max_seq_len rows");
+  check_bf16(kc, "k_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
+  check_bf16(vc, "v_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
+  TORCH_CHECK(kc.data_ptr() != vc.data_ptr(), "megakernel: k_cache and v_cache must be distinct");
+  TORCH_CHECK(position >= 0 && position < max_seq_len, "megakernel: position ", position,
+              " out of range [0, ", max_seq_len, ")");
+  TORCH_CHECK(token_id >= 0 && token_id < V, "megakernel: token_id ", token_id, " out of range [0, ", V, ")");
+  Checked c;
+  c.dims = {(int32_t)H, (int32_t)I, (int32_t)L, (int32_t)V};
+  c.dev = dev;
+  return c;
+}
+
+const void* device_table(const std::vector<torch::Tensor>& lw, const torch::Device& dev, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const int idx = dev.index() < 0 ? 0 : dev.index();
+  TORCH_CHECK(idx < (int)g_tables.size(), "megakernel: device index too large");
+  TableCache& tc = g_tables[idx];
+  std::vector<const void*> ptrs(lw.size());
+  for (size_t i = 0; i < lw.size(); ++i) ptrs[i] = lw[i].data_ptr();
+  if (tc.table.defined() && ptrs == tc.ptrs) return tc.table.data_ptr();
+  const int64_t L = lw.size() / kPerLayer;
+  auto host = torch::empty({L * (int64_t)sizeof(mk_layer_weights)}, torch::dtype(torch::kUInt8).pinned_memory(true));
+  auto* h = reinterpret_cast<mk_layer_weights*>(host.data_ptr());
+  for (int64_t l = 0; l < L; ++l) {
+    const void* const* p = &ptrs[l * kPerLayer];
+    h[l] = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10]};
+  }
+  auto table = torch::empty({host.numel()}, torch::dtype(torch::kUInt8).device(dev));
+  MK_HIP_CHECK(hipMemcpyAsync(table.data_ptr(), host.data_ptr(), host.numel(), hipMemcpyHostToDevice, stream));
+  MK_HIP_CHECK(hipStreamSynchronize(stream));  // once per new weight set; keeps `host` alive until copied
+  tc.held = lw;
+  tc.ptrs = std::move(ptrs);
+  tc.table = table;
+  return tc.table.data_ptr();
+}
+
+std::tuple<torch::Tensor, torch::Tensor> run(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
+                                             torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                             torch::Tensor cos, torch::Tensor sin, torch::Tensor kc,
+                                             torch::Tensor vc, int64_t position, int64_t max_seq_len,
+                                             bool want_token) {
+  Checked c = validate(token_id, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  const void* table = device_table(lw, c.dev, stream);
+  auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  torch::Tensor tok;
+  if (want_token) tok = torch::empty({1}, embed.options().dtype(torch::kInt32));
+  MK_HIP_CHECK(mk_decode(&c.dims, (int)token_id, embed.data_ptr(), lm_head.data_ptr(), final_norm.data_ptr(), table,
+                         cos.data_ptr(), sin.data_ptr(), kc.data_ptr(), vc.data_ptr(), (int)position,
+                         (int)max_seq_len, logits.data_ptr<float>(),
+                         want_token ? tok.data_ptr<int32_t>() : nullptr, stream));
+  return {logits, tok};
+}
+
+torch::Tensor decode(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head, torch::Tensor final_norm,
+                     std::vector<torch::Tensor> lw, torch::Tensor cos, torch::Tensor sin, torch::Tensor kc,
+                     torch::Tensor vc, int64_t position, int64_t max_seq_len) {
+  return std::get<0>(run(token_id, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len, false));
+}
+
+std::tuple<torch::Tensor, torch::Tensor> decode_greedy(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
+                                                       torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                       torch::Tensor cos, torch::Tensor sin, torch::Tensor kc,
+                                                       torch::Tensor vc, int64_t position, int64_t max_seq_len) {
+  return run(token_id, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len, true);
+}
+
+int64_t status() {
+  uint32_t s = 0;
+  MK_HIP_CHECK(mk_status(&s));
+  return s;
+}
+
+void reset() { MK_HIP_CHECK(mk_reset()); }
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("decode", &decode, "Qwen3 single-token decode (fp32 logits)");
+  m.def("decode_greedy", &decode_greedy, "Qwen3 single-token decode; returns (fp32 logits, int32 greedy token on device)");
+  m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
+  m.def("reset", &reset, "clear the decode workspace's status word and barrier counters; synchronizes");
+  m.def("version", []() { return std::string(mk_version()); });
+}
