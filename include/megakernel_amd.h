@@ -101,7 +101,8 @@ hipError_t mk_reset(void);
  * in-kernel timers). With a non-NULL device buffer of at least mk_trace_bytes() bytes, every later
  * launch on the current device writes, per workgroup, s_memrealtime stamps (100 MHz) at each
  * phase start and barrier arrival: uint64 [grid][TRACE_N], TRACE_N = mk_trace_bytes() / 8 / grid,
- * slot 10*layer + 2*phase (+1 for arrival) for phases A..E, tail slots 640.. for embedding, final
+ * slot 20*layer + 2*phase (+1 when published) for phases A..E, 20*layer + 10.. for the exchange
+ * waits, tail slots 1280.. for kernel start, final
  * norm, LM head and exit. NULL turns tracing off. */
 hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes);
 size_t mk_trace_bytes(void);

@@ -5,27 +5,33 @@
 // residual} -> final RMSNorm -> tied LM head -> greedy argmax. This is the work of the reference's
 // decode_kernel (/root/reference/megakernel.cu:744-893), re-planned for 256 CUs in 8 XCDs.
 //
-// Work placement (XCD-aware). The grid is one 512-thread workgroup per CU; workgroup b runs on
-// XCD x = b % 8 as "local" workgroup j = b / 8 (the dispatcher's round-robin placement, checked
-// by the host at initialisation; correctness does not depend on it). XCD x owns K/V head x: the
-// 512 Q/K/V rows of that group, its attention and its 256 columns of o_proj, plus a 1/8 slice of
-// the MLP intermediate. So per layer only two exchanges cross XCDs:
+// Placement. One 512-thread workgroup per CU. Workgroup b runs on XCD x = b % 8 as local
+// workgroup j = b / 8 (the dispatcher's round-robin placement; every workgroup checks its
+// HW_REG_XCC_ID and reports a mismatch in the status word). XCD x owns K/V head x -- the 512
+// Q/K/V rows of that group, its attention and its 256 columns of o_proj -- plus a 1/8 slice of
+// the MLP intermediate, so within a layer only two exchanges leave the XCD.
 //
-//   A  QKV rows of group x, 16 rows per WG            -> XCD barrier
-//   B  q/k norm + RoPE (redundant), K/V cache write,
-//      split-K attention over ctx/32 positions per WG -> XCD barrier
-//   C  merge 32 partials, o_proj partial over the
-//      group's 256 columns                            -> grid barrier
-//   D  residual += sum of 8 o_proj partials (every WG,
-//      same order), RMSNorm, gate/up rows of slice x  -> XCD barrier
-//   E  down_proj partial over slice x's columns       -> grid barrier
+// Roles. Wave 0 of every workgroup is the communication wave: it waits for other workgroups'
+// results, moves exchanged vectors, and does the vector work (RMSNorm, q/k norm + RoPE,
+// attention merges, SiLU). Waves 1-7 are math waves: they stream weights and K/V with 16-byte
+// loads issued about two phases ahead, and compute dot products from LDS inputs. Splitting the
+// roles keeps the math waves' prefetch queue from stalling the polling wave (vector-memory
+// completion is counted in order per wave).
 //
-// The residual stream is kept redundantly in every workgroup's LDS; every workgroup computes it
-// from the same inputs in the same order, so all copies are bitwise identical.
+// Exchanges (no atomics). A producer writes data, waits for its stores, then writes a flag word
+// holding the launch epoch; a consumer polls the flags with device-scope loads.
+//   * within an XCD (QKV -> attention, attention partials, SiLU(g)*u): plain stores land in the
+//     XCD's shared L2 and device-scope loads read them there;
+//   * across XCDs (o_proj and down_proj partial sums): workgroup j of XCD y writes its row block
+//     j through to memory (device scope); workgroup j of every XCD gathers block j from the 8
+//     XCDs, sums it in XCD order and republishes it into its own XCD's L2; then every workgroup
+//     reads the full vector from its L2. Two short hops, at most 8 pollers per cross-XCD line.
 //
 // Numerics follow the reference kernel's fp32 design: bf16 weights and cache, fp32 activations
 // and accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to bf16 as stored. Logits are
-// fp32; the greedy token is the argmax of the bf16-rounded logits, lowest index on ties.
+// fp32; the greedy token is the argmax of the bf16-rounded logits, lowest index on ties. The
+// residual stream is kept redundantly in every workgroup's LDS and updated from the same data
+// in the same order, so all copies are bitwise identical.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <mutex>
@@ -43,27 +49,45 @@ constexpr int NXCD = 8;       // XCDs on MI355X
 constexpr int WPX = 32;       // workgroups per XCD
 constexpr int NWG = NXCD * WPX;
 constexpr int NT = 512;       // threads per workgroup
-constexpr int NWAVE = NT / 64;
-constexpr int NGRP = NT / 16;  // 16-lane row groups per workgroup
-constexpr int QKV_ROWS_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
-constexpr int QKV_ROWS_WG = QKV_ROWS_X / WPX;  // 16
-constexpr int APS = 132;      // floats per attention partial: acc[128], m, l, pad
+constexpr int NMW = 7;        // math waves (1..7)
+constexpr int MG = NMW * 4;   // 16-lane math groups
+constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
+constexpr int QKV_WG = QKV_X / WPX;  // 16
+constexpr int APS = 132;      // floats per head in an attention partial: acc[128], m, l, pad
+constexpr int APF = 5;        // K/V positions per math wave loaded ahead of the attention phase
 constexpr float EPS = 1e-6f;
 constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
 constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr uint32_t ERR_TIMEOUT = 1u;
+constexpr uint32_t ERR_PLACEMENT = 2u;
+constexpr int MAX_LAYERS = 62;  // epoch = seq << 6 | layer; 63 marks the final exchange
 
-// Workspace layout. Floats first, then 256-byte counter lines.
-constexpr int MAX_H = 2048, MAX_I = 6144;
-constexpr size_t WS_QKV = 0;
-constexpr size_t WS_APART = WS_QKV + NXCD * QKV_ROWS_X;
-constexpr size_t WS_OPART = WS_APART + (size_t)NXCD * WPX * 2 * APS;
-constexpr size_t WS_MBUF = WS_OPART + (size_t)NXCD * MAX_H;
-constexpr size_t WS_DPART = WS_MBUF + MAX_I;
-constexpr size_t WS_FLOATS = WS_DPART + (size_t)NXCD * MAX_H;
-constexpr int CTR_LINE = 64;  // u32 per counter line (256 B)
-enum CtrLine { L_XL = 0, L_XG = 8, L_G = 16, L_XEXIT = 17, L_GEXIT = 25, L_STATUS = 26, L_AMAX = 27, N_LINES = 32 };
-constexpr size_t WS_BYTES = WS_FLOATS * 4 + (size_t)N_LINES * CTR_LINE * 4;
+// Workspace layout: float buffers, then 256-byte flag lines.
+constexpr int MAX_H = 2048, MAX_I = 6144, MAX_IX = MAX_I / NXCD, MAX_HPW = MAX_H / WPX;
+constexpr size_t W_QKV = 0;                                       // [8][512]
+constexpr size_t W_ATT = W_QKV + NXCD * QKV_X;                    // [8][32][2*APS]
+constexpr size_t W_M = W_ATT + (size_t)NXCD * WPX * 2 * APS;      // [8][MAX_IX]
+constexpr size_t W_LC = W_M + (size_t)NXCD * MAX_IX;              // [8][MAX_H]
+constexpr size_t W_LE = W_LC + (size_t)NXCD * MAX_H;              // [8][MAX_H]
+constexpr size_t W_GC = W_LE + (size_t)NXCD * MAX_H;              // [32][8][MAX_HPW]
+constexpr size_t W_GE = W_GC + (size_t)WPX * NXCD * MAX_HPW;      // [32][8][MAX_HPW]
+constexpr size_t WS_FLOATS = W_GE + (size_t)WPX * NXCD * MAX_HPW;
+// Flags, in u32 words after the float buffers. A local flag line (256 B) holds the 32 flags of
+// one XCD's workgroups -- all its writers share that XCD's L2. Every flag or value written across
+// XCDs gets a 128-byte slot of its own, so no cache line has writers on two XCDs.
+constexpr int LINE = 64;  // u32 per local flag line (256 B)
+constexpr int SLOT = 32;  // u32 per cross-XCD slot (128 B)
+enum LocalFlag { F_QKV = 0, F_ATT = 1, F_M = 2, F_LC = 3, F_LE = 4, N_LOCAL = 5 };
+constexpr size_t FL_LOCAL = 0;                                     // [type][x] lines
+constexpr size_t FL_CROSS = FL_LOCAL + (size_t)N_LOCAL * NXCD * LINE;  // [kind C/E][j][y] slots
+constexpr size_t FL_DONE = FL_CROSS + (size_t)2 * WPX * NXCD * SLOT;  // [wg] slots: flag, pad, key u64
+constexpr size_t FL_STATUS = FL_DONE + (size_t)NWG * SLOT;         // own line
+constexpr size_t FL_SEQ = FL_STATUS + LINE;                        // own line
+constexpr size_t FL_WORDS = FL_SEQ + LINE;
+__host__ __device__ constexpr size_t fl_local(int type, int x) { return FL_LOCAL + ((size_t)type * NXCD + x) * LINE; }
+__host__ __device__ constexpr size_t fl_cross(int kind, int j, int y) { return FL_CROSS + (((size_t)kind * WPX + j) * NXCD + y) * SLOT; }
+__host__ __device__ constexpr size_t fl_done(int wg) { return FL_DONE + (size_t)wg * SLOT; }
+constexpr size_t WS_BYTES = WS_FLOATS * 4 + FL_WORDS * 4;
 
 struct KArgs {
   const uint16_t* embed;
@@ -77,148 +101,139 @@ struct KArgs {
   float* logits;
   int32_t* out_token;
   float* ws;
-  uint32_t* ctr;
+  uint32_t* fl;     // flag lines
   uint64_t* trace;  // optional: per-workgroup phase timestamps (TRACE_N per workgroup)
   int token, position, max_seq, num_layers, vocab;
 };
 
-// Phase timestamps (s_memrealtime, 100 MHz): per layer and phase p in A..E, [10*layer + 2p] when the
-// phase starts (its barrier released) and [10*layer + 2p + 1] when the workgroup arrives at the
-// barrier that ends it; TRACE_TAIL slots for embedding, LM head and exit.
+// Phase timestamps (s_memrealtime, 100 MHz), TRACE_PER_LAYER slots per layer: for phase p in A..E,
+// [2p] when the phase's math starts and [2p + 1] when its outputs are published; [10 + k] when the
+// communication wave finishes its k-th wait of the layer (QKV, attention partials, cross o_proj,
+// local o_proj, MLP, cross down, local down). TRACE_TAIL slots after the layers: kernel start,
+// last exchange done, LM-head start and end.
 constexpr int TRACE_LAYERS = 64;
+constexpr int TRACE_PER_LAYER = 20;
 constexpr int TRACE_TAIL = 8;
-constexpr int TRACE_N = TRACE_LAYERS * 10 + TRACE_TAIL;
+constexpr int TRACE_N = TRACE_LAYERS * TRACE_PER_LAYER + TRACE_TAIL;
 __device__ __forceinline__ void mark(const KArgs& a, int idx) {
   if (a.trace != nullptr && threadIdx.x == 0 && idx >= 0 && idx < TRACE_N)
     a.trace[(size_t)blockIdx.x * TRACE_N + idx] = wall_clock64();
 }
 
 // ------------------------------------------------------------------------------------------
-// Grid synchronisation. Counters only grow during a launch; the last workgroup to leave resets
-// them, so every launch starts from zero. Every wait is bounded: on timeout the status word is
-// set and all later waits return at once, so a broken launch still drains.
+// Communication-wave helpers (called by wave 0 only; every lane participates)
 // ------------------------------------------------------------------------------------------
-struct Sync {
-  uint32_t* xl;     // this XCD's local-barrier counter
-  uint32_t* xg;     // this XCD's first-level grid-barrier counter
-  uint32_t* g;      // grid-barrier counter
+struct Comm {
   uint32_t* status;
-  uint32_t nl = 0, ng = 0;
   bool failed = false;
 };
 
-__device__ __forceinline__ bool wait_ge(const uint32_t* p, uint32_t target, uint32_t* status) {
+// Plain store: stays in this XCD's L2 until written back; visible to device-scope loads from the
+// same XCD.
+__device__ __forceinline__ void st_local_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void st_local_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// All earlier stores of this wave are complete before anything after this point is issued.
+__device__ __forceinline__ void store_fence() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  wait_vmem();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Wait until flags[0], flags[stride], ... flags[(n-1)*stride] all equal ep (n <= 64). Bounded;
+// on timeout sets the status word.
+__device__ __forceinline__ void poll_flags(Comm& c, const uint32_t* flags, int n, uint32_t ep, int stride = 1) {
+  if (c.failed) return;
+  const int lane = threadIdx.x & 63;
   for (uint32_t it = 0;; ++it) {
-    if ((int32_t)(ld_dev_u32(p) - target) >= 0) return true;
-    if ((it & 63u) == 63u && ld_dev_u32(status) != 0) return false;
+    const uint32_t v = lane < n ? ld_dev_u32(flags + lane * stride) : ep;
+    if (__ballot(v != ep) == 0) return;
+    if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) { c.failed = true; return; }
     if (it > SPIN_LIMIT) {
-      st_dev_u32(status, ERR_TIMEOUT);
-      return false;
+      if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT);
+      c.failed = true;
+      return;
     }
-    __builtin_amdgcn_s_sleep(1);
   }
 }
 
-__device__ __forceinline__ void xcd_barrier(Sync& s) {
-  wait_vmem();
-  __syncthreads();
-  s.nl++;
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(s.xl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (!s.failed && !wait_ge(s.xl, WPX * s.nl, s.status)) s.failed = true;
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ void grid_barrier(Sync& s) {
-  wait_vmem();
-  __syncthreads();
-  s.ng++;
-  if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_fetch_add(s.xg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old + 1 == WPX * s.ng) __hip_atomic_fetch_add(s.g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (!s.failed && !wait_ge(s.g, NXCD * s.ng, s.status)) s.failed = true;
-  }
-  __syncthreads();
-}
-
-// ------------------------------------------------------------------------------------------
-// Block helpers
-// ------------------------------------------------------------------------------------------
-__device__ __forceinline__ float block_sum(float v, float* s_red) {
-  v = wave_sum(v);
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) s_red[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int w = 0; w < NWAVE; ++w) t += s_red[w];
-  __syncthreads();
-  return t;
-}
-
-// RMSNorm in fp32, the reference's form x * w * rsqrt(mean(x^2) + eps)
-// (/root/reference/megakernel.cu:704-739 and :148-182).
+// s_res[i] += delta[i] (device-scope reads; delta may be null), then s_x = RMSNorm(s_res) * w in
+// fp32, the reference's form x * w * rsqrt(mean(x^2) + eps) (/root/reference/megakernel.cu:704-739).
+// Lane l owns the H/64 contiguous elements starting at l*H/64.
 template <int H>
-__device__ __forceinline__ void rms_norm(const float* s_in, const uint16_t* w, float* s_out, float* s_red) {
+__device__ __forceinline__ void comm_residual_norm(float* s_res, const float* delta, const uint16_t* w, float* s_x) {
+  constexpr int E = H / 64;
+  const int lane = threadIdx.x & 63;
+  float v[E];
   float ss = 0.f;
-  for (int i = threadIdx.x; i < H; i += NT) ss += s_in[i] * s_in[i];
-  ss = block_sum(ss, s_red);
-  const float r = rsqrtf(ss / (float)H + EPS);
-  for (int i = threadIdx.x; i < H; i += NT) s_out[i] = s_in[i] * bf16_to_f32(w[i]) * r;
-  __syncthreads();
-}
-
-// ------------------------------------------------------------------------------------------
-// GEMV engine. A workgroup's share of a phase is a list of (row, column-segment) tasks; each
-// 16-lane row group takes one task at a time, streams its weight chunks (16 B = 8 bf16 per lane
-// per step, 256 contiguous bytes per group per step) and reduces over the 16 lanes with DPP.
-// x is the fp32 input in LDS (C floats); emit(r, seg, value) receives each task's sum.
-// ------------------------------------------------------------------------------------------
-template <int C, int S, typename RowPtr, typename Emit>
-__device__ __forceinline__ void gemv(int R, RowPtr rowptr, const float* x, Emit emit) {
-  constexpr int CPS = C / 8 / S;  // 16-byte chunks per segment
-  constexpr int CPL = CPS / 16;   // chunks per lane per task
-  static_assert(CPS % 16 == 0, "segment must be a multiple of 16 chunks");
-  const int grp = threadIdx.x >> 4;
-  const int t = threadIdx.x & 15;
-  for (int task = grp; task < R * S; task += NGRP) {
-    const int r = task / S;
-    const int sg = task - r * S;
-    const uint4* w = reinterpret_cast<const uint4*>(rowptr(r)) + sg * CPS + t;
-    const float* xs = x + (sg * CPS + t) * 8;
-    uint4 wv[CPL];
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) wv[k] = ld_stream(w + 16 * k);
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) acc = dot8(wv[k], xs + 128 * k, acc);
-    acc = row16_sum(acc);
-    if (t == 0) emit(r, sg, acc);
-  }
-}
-
-// Read n floats published by other workgroups (device scope) into LDS.
-__device__ __forceinline__ void fetch_dev(const float* src, float* dst, int n) {
-  for (int i = threadIdx.x * 4; i < n; i += NT * 4) {
-    float4 v = ld_dev_f32x4(src, i * 4);
-    dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
-  }
-}
-
-// s_res[i] += sum over the 8 XCD partials part[x][i], x ascending (identical order everywhere).
-template <int H>
-__device__ __forceinline__ void add_partials(float* s_res, const float* part) {
-  for (int i = threadIdx.x * 4; i < H; i += NT * 4) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int x = 0; x < NXCD; ++x) {
-      float4 v = ld_dev_f32x4(part, (x * H + i) * 4);
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  for (int k = 0; k < E; k += 4) {
+    float4 r = *reinterpret_cast<const float4*>(s_res + lane * E + k);
+    if (delta != nullptr) {
+      const float4 d = ld_dev_f32x4(delta, (lane * E + k) * 4);
+      r.x += d.x; r.y += d.y; r.z += d.z; r.w += d.w;
+      *reinterpret_cast<float4*>(s_res + lane * E + k) = r;
     }
-    s_res[i] += acc.x; s_res[i + 1] += acc.y; s_res[i + 2] += acc.z; s_res[i + 3] += acc.w;
+    v[k] = r.x; v[k + 1] = r.y; v[k + 2] = r.z; v[k + 3] = r.w;
   }
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < E; ++k) ss += v[k] * v[k];
+  ss = wave_sum(ss);
+  const float rs = rsqrtf(ss / (float)H + EPS);
+  const uint4* wp = reinterpret_cast<const uint4*>(w + lane * E);
+#pragma unroll
+  for (int k = 0; k < E; k += 8) {
+    const uint4 ww = ld_global16(wp + k / 8);
+    const float wv[8] = {bf16_lo(ww.x), bf16_hi(ww.x), bf16_lo(ww.y), bf16_hi(ww.y),
+                         bf16_lo(ww.z), bf16_hi(ww.z), bf16_lo(ww.w), bf16_hi(ww.w)};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s_x[lane * E + k + q] = v[k + q] * wv[q] * rs;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Math-wave helpers. A phase's weight tile is cut into units of 16 chunks (256 contiguous
+// bytes of one row); math group g (16 lanes) owns units g, g+28, g+56, ...; lane t of the group
+// loads chunk t of each unit. Unit u covers row u / UPR, column block u % UPR (128 elements).
+// ------------------------------------------------------------------------------------------
+// Loads are unconditional (a lane past the tile re-reads the tile's last unit): a conditional
+// load becomes a branch whose join forces the wave to wait for every outstanding load, which
+// would serialize the phase and drain the prefetch of later phases.
+template <int NU, int UPR, typename Ptr>
+__device__ __forceinline__ void load_units(uint4 (&w)[NU], int k0, int U, int g, int t, Ptr ptr) {
+#pragma unroll
+  for (int k = 0; k < NU; ++k) {
+    int u = g + MG * (k0 + k);
+    u = u < U ? u : U - 1;
+    w[k] = ld_stream(ptr(u / UPR, u % UPR) + t);
+  }
+}
+
+template <int NU, int UPR>
+__device__ __forceinline__ void dot_units(const uint4 (&w)[NU], int k0, int U, int g, int t, const float* x, float* s_up) {
+#pragma unroll
+  for (int k = 0; k < NU; ++k) {
+    const int u = g + MG * (k0 + k);
+    const int uc = u < U ? u : U - 1;
+    float acc = dot8(w[k], x + (uc % UPR) * 128 + t * 8, 0.f);
+    acc = row16_sum(acc);
+    if (t == 0 && u < U) s_up[u] = acc;
+  }
+}
+
+// A GEMV phase whose first PFN units per lane were loaded ahead (pf); the rest stream here.
+template <int NU, int PFN, int UPR, typename Ptr>
+__device__ __forceinline__ void gemv_phase(const uint4 (&pf)[PFN], int U, int g, int t, Ptr ptr, const float* x, float* s_up) {
+  dot_units<PFN, UPR>(pf, 0, U, g, t, x, s_up);
+#pragma unroll
+  for (int k0 = PFN; k0 < NU; k0 += PFN) {
+    uint4 w[PFN];
+    load_units<PFN, UPR>(w, k0, U, g, t, ptr);
+    dot_units<PFN, UPR>(w, k0, U, g, t, x, s_up);
+  }
 }
 
 __device__ __forceinline__ unsigned long long argmax_key(float logit, int idx) {
@@ -229,132 +244,228 @@ __device__ __forceinline__ unsigned long long argmax_key(float logit, int idx) {
   return ((unsigned long long)u << 32) | (0xffffffffu - (uint32_t)idx);
 }
 
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+// Returns v unchanged but hides its origin from the optimizer, so per-unit indices derived from it
+// are recomputed inside each phase instead of being hoisted out of the layer loop and held in
+// registers for the whole kernel.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // ------------------------------------------------------------------------------------------
 // The kernel
 // ------------------------------------------------------------------------------------------
 template <int H, int I>
 __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
-  constexpr int IX = I / NXCD;      // MLP intermediate slice per XCD
-  constexpr int IPW = IX / WPX;     // gate (and up) rows per workgroup
-  constexpr int HPW = H / WPX;      // o_proj / down_proj rows per workgroup
-  // column segments for gate/up: the smallest S with a whole number of task rounds
-  constexpr int GU_S = (2 * IPW) % NGRP == 0 ? 1 : (4 * IPW) % NGRP == 0 ? 2 : 4;
+  constexpr int IX = I / NXCD;     // MLP intermediate slice per XCD
+  constexpr int IPW = IX / WPX;    // gate (and up) rows per workgroup
+  constexpr int HPW = H / WPX;     // o_proj / down_proj rows per workgroup
+  constexpr int UPR_H = H / 128, UPR_C = 2 * D / 128, UPR_E = IX / 128;
+  constexpr int U_A = QKV_WG * UPR_H, U_C = HPW * UPR_C, U_D = 2 * IPW * UPR_H, U_E = HPW * UPR_E;
+  constexpr int NU_A = (U_A + MG - 1) / MG, NU_C = (U_C + MG - 1) / MG;
+  constexpr int NU_D = (U_D + MG - 1) / MG, NU_E = (U_E + MG - 1) / MG;
+  constexpr int PF = H <= 1024 ? 8 : 4;  // max 16-byte chunks per lane loaded ahead of a GEMV phase
+  constexpr int PA = NU_A < PF ? NU_A : PF, PC = NU_C < PF ? NU_C : PF;
+  constexpr int PD = NU_D < PF ? NU_D : PF, PE = NU_E < PF ? NU_E : PF;
   constexpr int XN = (H > IX ? H : IX);
+  constexpr int UMAX = (U_D > U_A ? U_D : U_A) > U_E ? (U_D > U_A ? U_D : U_A) : U_E;
   static_assert(HPW * WPX == H && IPW * WPX == IX && IX * NXCD == I, "shape must split evenly");
-  static_assert((2 * IPW * GU_S) % NGRP == 0 && (H / 8 / GU_S) % 16 == 0, "gate/up tasks must tile the groups");
+  static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64, "unsupported shape");
 
   __shared__ __attribute__((aligned(16))) float s_res[H];
   __shared__ __attribute__((aligned(16))) float s_x[XN];
-  __shared__ __attribute__((aligned(16))) float s_part[128];
-  __shared__ float s_red[NWAVE];
+  __shared__ __attribute__((aligned(16))) float s_up[UMAX];
   __shared__ __attribute__((aligned(16))) float s_q[2][D];
   __shared__ __attribute__((aligned(16))) float s_k[D];
   __shared__ __attribute__((aligned(16))) float s_v[D];
-  __shared__ __attribute__((aligned(16))) float s_wpart[NWAVE][2][D + 2];
-  __shared__ float s_mw[WPX][2][2];
+  __shared__ __attribute__((aligned(16))) float s_wp[NMW][2][D + 2];
+  __shared__ unsigned long long s_best[NMW];
 
   const int xcd = blockIdx.x % NXCD;
   const int j = blockIdx.x / NXCD;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const bool comm = wave == 0;
+  const int g = comm ? 0 : (wave - 1) * 4 + (lane >> 4);  // math group
+  const int t = lane & 15;
 
   float* ws = a.ws;
-  float* qkv_x = ws + WS_QKV + xcd * QKV_ROWS_X;
-  float* apart_x = ws + WS_APART + (size_t)xcd * WPX * 2 * APS;
-  float* opart = ws + WS_OPART;
-  float* mbuf_x = ws + WS_MBUF + xcd * IX;
-  float* dpart = ws + WS_DPART;
-
-  Sync sync;
-  sync.xl = a.ctr + (L_XL + xcd) * CTR_LINE;
-  sync.xg = a.ctr + (L_XG + xcd) * CTR_LINE;
-  sync.g = a.ctr + L_G * CTR_LINE;
-  sync.status = a.ctr + L_STATUS * CTR_LINE;
-
+  uint32_t* fl = a.fl;
+  Comm c;
+  c.status = fl + FL_STATUS;
   const int position = a.position;
   const int ctx = position + 1;
+  const int L = a.num_layers;
 
-  const int tb = TRACE_LAYERS * 10;
-  mark(a, tb + 0);
-  // Embedding row -> fp32 residual (every workgroup keeps its own copy).
-  {
-    const uint16_t* row = a.embed + (size_t)a.token * H;
-    for (int i = threadIdx.x; i < H; i += NT) s_res[i] = bf16_to_f32(row[i]);
-    __syncthreads();
-  }
+  // Split-K attention: the context is cut into S = min(32, ceil(ctx / 32)) splits handled by local
+  // workgroups 0..S-1; math wave w of a split takes positions p0 + w, p0 + w + 7, ...
+  const int S = ctx >= WPX * 32 ? WPX : (ctx + 31) / 32;
+  const int p0 = j < S ? (int)(((long long)ctx * j) / S) : 0;
+  const int p1 = j < S ? (int)(((long long)ctx * (j + 1)) / S) : 0;
+  const int mw = wave - 1;
+  const int np_w = (!comm && p1 - p0 > mw) ? (p1 - p0 - mw + NMW - 1) / NMW : 0;
 
-  for (int layer = 0; layer < a.num_layers; ++layer) {
-    const mk_layer_weights lw = a.layers[layer];
-    const int tl = layer < TRACE_LAYERS ? layer * 10 : -1000000;
-    mark(a, tl + 0);
-    if (layer > 0) add_partials<H>(s_res, dpart);
+  // ---- per-phase weight tiles (unit (r, b) starts at chunk 16*b of tile row r) -------------
+  auto ptr_A = [&](const mk_layer_weights& lw) {
+    const uint16_t* base;
+    int row0;
+    if (j < 16) { base = (const uint16_t*)lw.q_weight; row0 = 2 * D * xcd + QKV_WG * j; }
+    else if (j < 24) { base = (const uint16_t*)lw.k_weight; row0 = D * xcd + QKV_WG * (j - 16); }
+    else { base = (const uint16_t*)lw.v_weight; row0 = D * xcd + QKV_WG * (j - 24); }
+    return [=](int r, int b) { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * H) + 16 * b; };
+  };
+  auto ptr_C = [&](const mk_layer_weights& lw) {
+    const uint16_t* wo = (const uint16_t*)lw.o_proj_weight;
+    const int row0 = HPW * j;
+    return [=](int r, int b) {
+      return reinterpret_cast<const uint4*>(wo + (size_t)(row0 + r) * (HQ * D) + 2 * D * xcd) + 16 * b;
+    };
+  };
+  auto ptr_D = [&](const mk_layer_weights& lw) {
+    const uint16_t* wg = (const uint16_t*)lw.gate_proj_weight;
+    const uint16_t* wu = (const uint16_t*)lw.up_proj_weight;
+    const int row0 = IX * xcd + IPW * j;
+    return [=](int r, int b) {
+      const uint16_t* row = r < IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - IPW) * H;
+      return reinterpret_cast<const uint4*>(row) + 16 * b;
+    };
+  };
+  auto ptr_E = [&](const mk_layer_weights& lw) {
+    const uint16_t* wd = (const uint16_t*)lw.down_proj_weight;
+    const int row0 = HPW * j;
+    return [=](int r, int b) { return reinterpret_cast<const uint4*>(wd + (size_t)(row0 + r) * I + IX * xcd) + 16 * b; };
+  };
 
-    // ---- A: input RMSNorm, QKV rows of this XCD's K/V group --------------------------------
-    rms_norm<H>(s_res, (const uint16_t*)lw.norm_weight, s_x, s_red);
-    {
-      // local rows [16j, 16j+16) of the XCD's 512: q heads 2x,2x+1 (256), k head x, v head x
-      const uint16_t* base;
-      int row0;
-      if (j < 16) { base = (const uint16_t*)lw.q_weight; row0 = 2 * D * xcd + QKV_ROWS_WG * j; }
-      else if (j < 24) { base = (const uint16_t*)lw.k_weight; row0 = D * xcd + QKV_ROWS_WG * (j - 16); }
-      else { base = (const uint16_t*)lw.v_weight; row0 = D * xcd + QKV_ROWS_WG * (j - 24); }
-      gemv<H, 2>(QKV_ROWS_WG, [&](int r) { return base + (size_t)(row0 + r) * H; }, s_x,
-                 [&](int r, int sg, float v) { s_part[r * 2 + sg] = v; });
-      __syncthreads();
-      if (threadIdx.x < QKV_ROWS_WG)
-        st_dev_f32(qkv_x + QKV_ROWS_WG * j + threadIdx.x, s_part[threadIdx.x * 2] + s_part[threadIdx.x * 2 + 1]);
+  // K/V of the first APF positions of this math wave, loaded ahead of the attention phase
+  uint32_t kv_k[APF], kv_v[APF];
+  auto load_kv = [&](int layer) {
+    const size_t hb = ((size_t)layer * HKV + xcd) * a.max_seq * D;
+    const uint32_t* kc = reinterpret_cast<const uint32_t*>(a.k_cache + hb);
+    const uint32_t* vc = reinterpret_cast<const uint32_t*>(a.v_cache + hb);
+#pragma unroll
+    for (int i = 0; i < APF; ++i) {
+      // unconditional (see load_units); positions outside [p0, p1) or the new one are not used
+      int p = p0 + mw + NMW * i;
+      p = (i < np_w && p != position) ? p : 0;
+      kv_k[i] = gp(kc)[(size_t)p * (D / 2) + lane];
+      kv_v[i] = gp(vc)[(size_t)p * (D / 2) + lane];
     }
-    mark(a, tl + 1);
-    xcd_barrier(sync);
-    mark(a, tl + 2);
+  };
 
-    // ---- B: per-head q/k RMSNorm + RoPE, cache write, split-K attention ------------------------
-    {
-      fetch_dev(qkv_x, s_x, QKV_ROWS_X);  // s_x[0:256) q (2 heads), [256:384) k, [384:512) v
-      __syncthreads();
-      const uint16_t* cr = a.cos_tab + (size_t)position * D;
-      const uint16_t* sr = a.sin_tab + (size_t)position * D;
-      if (wave < 3) {
-        // wave 0,1: q heads; wave 2: k head. Lane l handles dims l and l+64.
-        const float* src = s_x + (wave < 2 ? wave * D : 2 * D);
-        const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-        const float t0 = src[lane], t1 = src[lane + 64];
-        const float ss = wave_sum(t0 * t0 + t1 * t1);
-        const float rs = rsqrtf(ss / (float)D + EPS);
-        const float u0 = t0 * rs * bf16_to_f32(nw[lane]);
-        const float u1 = t1 * rs * bf16_to_f32(nw[lane + 64]);
-        const float o0 = u0 * bf16_to_f32(cr[lane]) - u1 * bf16_to_f32(sr[lane]);
-        const float o1 = u1 * bf16_to_f32(cr[lane + 64]) + u0 * bf16_to_f32(sr[lane + 64]);
-        if (wave < 2) { s_q[wave][lane] = o0; s_q[wave][lane + 64] = o1; }
+  uint4 wA[PA], wC[PC], wD[PD], wE[PE];
+  uint32_t seq = 0;
+  float cs_c0 = 0.f, cs_c1 = 0.f, cs_s0 = 0.f, cs_s1 = 0.f;  // comm: cos/sin at dims lane, lane+64
+
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 0);
+  if (comm) {
+    seq = ld_dev_u32(fl + FL_SEQ);
+    if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, ERR_PLACEMENT);
+    const uint16_t* row = a.embed + (size_t)a.token * H;
+    for (int i = lane; i < H; i += 64) s_res[i] = bf16_to_f32(gp(row)[i]);
+    const uint16_t* cr = a.cos_tab + (size_t)position * D;
+    const uint16_t* sr = a.sin_tab + (size_t)position * D;
+    cs_c0 = bf16_to_f32(gp(cr)[lane]); cs_c1 = bf16_to_f32(gp(cr)[lane + 64]);
+    cs_s0 = bf16_to_f32(gp(sr)[lane]); cs_s1 = bf16_to_f32(gp(sr)[lane + 64]);
+    comm_residual_norm<H>(s_res, nullptr, (const uint16_t*)a.layers[0].norm_weight, s_x);
+  } else {
+    const mk_layer_weights lw0 = a.layers[0];
+    load_units<PA, UPR_H>(wA, 0, U_A, g, t, ptr_A(lw0));
+  }
+  __syncthreads();
+
+  for (int layer = 0; layer < L; ++layer) {
+    const mk_layer_weights lw = a.layers[layer];
+    const uint32_t ep = (seq << 6) | (uint32_t)layer;
+    const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
+    float* qkv_x = ws + W_QKV + xcd * QKV_X;
+    float* att_x = ws + W_ATT + (size_t)xcd * WPX * 2 * APS;
+    float* m_x = ws + W_M + xcd * IX;
+    float* lc_x = ws + W_LC + xcd * H;
+    float* le_x = ws + W_LE + xcd * H;
+
+    // ---- A: QKV rows of this XCD's group -------------------------------------------------
+    mark(a, tl + 0);
+    if (!comm) {
+      const int gq = opaque(g), tq = opaque(t);
+      load_units<PC, UPR_C>(wC, 0, U_C, gq, tq, ptr_C(lw));
+      load_kv(layer);
+      gemv_phase<NU_A, PA, UPR_H>(wA, U_A, gq, tq, ptr_A(lw), s_x, s_up);
+    }
+    __syncthreads();
+    if (comm) {
+      if (lane < QKV_WG) {
+        float s = 0.f;
+#pragma unroll
+        for (int b = 0; b < UPR_H; ++b) s += s_up[lane * UPR_H + b];
+        st_local_f32(qkv_x + QKV_WG * j + lane, s);
+      }
+      store_fence();
+      mark(a, tl + 1);
+      if (lane == 0) st_local_u32(fl + fl_local(F_QKV, xcd) + j, ep);
+      poll_flags(c, fl + fl_local(F_QKV, xcd), WPX, ep);
+      mark(a, tl + 10);
+      // q heads 2x, 2x+1 at [0, 256), k head x at [256, 384), v head x at [384, 512)
+      float t0[3], t1[3];
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        t0[h] = ld_dev_f32(qkv_x + h * D + lane);
+        t1[h] = ld_dev_f32(qkv_x + h * D + lane + 64);
+      }
+      const float v0 = ld_dev_f32(qkv_x + 3 * D + lane), v1 = ld_dev_f32(qkv_x + 3 * D + lane + 64);
+      const uint16_t* qn = (const uint16_t*)lw.q_norm_weight;
+      const uint16_t* kn = (const uint16_t*)lw.k_norm_weight;
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        // per-head RMSNorm then rotate-half RoPE (/root/reference/megakernel.cu:490-630)
+        const uint16_t* nw = h < 2 ? qn : kn;
+        const float rs = rsqrtf(wave_sum(t0[h] * t0[h] + t1[h] * t1[h]) / (float)D + EPS);
+        const float u0 = t0[h] * rs * bf16_to_f32(gp(nw)[lane]);
+        const float u1 = t1[h] * rs * bf16_to_f32(gp(nw)[lane + 64]);
+        const float o0 = u0 * cs_c0 - u1 * cs_s0;
+        const float o1 = u1 * cs_c1 + u0 * cs_s1;
+        if (h < 2) { s_q[h][lane] = o0; s_q[h][lane + 64] = o1; }
         else { s_k[lane] = round_bf16(o0); s_k[lane + 64] = round_bf16(o1); }
-      } else if (wave == 3) {
-        s_v[lane] = round_bf16(s_x[3 * D + lane]);
-        s_v[lane + 64] = round_bf16(s_x[3 * D + lane + 64]);
       }
-      __syncthreads();
-      const size_t head_base = ((size_t)layer * HKV + xcd) * a.max_seq * D;
-      if (j == 0 && threadIdx.x < D) {
-        a.k_cache[head_base + (size_t)position * D + threadIdx.x] = f32_to_bf16(s_k[threadIdx.x]);
-        a.v_cache[head_base + (size_t)position * D + threadIdx.x] = f32_to_bf16(s_v[threadIdx.x]);
+      s_v[lane] = round_bf16(v0);
+      s_v[lane + 64] = round_bf16(v1);
+      if (j == 0) {
+        const size_t slot = (((size_t)layer * HKV + xcd) * a.max_seq + position) * D;
+        gpw(a.k_cache)[slot + lane] = f32_to_bf16(s_k[lane]);
+        gpw(a.k_cache)[slot + lane + 64] = f32_to_bf16(s_k[lane + 64]);
+        gpw(a.v_cache)[slot + lane] = f32_to_bf16(v0);
+        gpw(a.v_cache)[slot + lane + 64] = f32_to_bf16(v1);
       }
-      // positions [p0, p1) of this workgroup; wave w takes p0+w, p0+w+8, ...
-      const int p0 = (int)(((long long)ctx * j) / WPX);
-      const int p1 = (int)(((long long)ctx * (j + 1)) / WPX);
+    }
+    __syncthreads();
+
+    // ---- B: split-K attention over this workgroup's positions ----------------------------
+    mark(a, tl + 2);
+    if (!comm) {
+      load_units<PD, UPR_H>(wD, 0, U_D, opaque(g), opaque(t), ptr_D(lw));
       const float q00 = s_q[0][2 * lane], q01 = s_q[0][2 * lane + 1];
       const float q10 = s_q[1][2 * lane], q11 = s_q[1][2 * lane + 1];
       float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
-      const uint32_t* kc = reinterpret_cast<const uint32_t*>(a.k_cache + head_base);
-      const uint32_t* vc = reinterpret_cast<const uint32_t*>(a.v_cache + head_base);
-      for (int p = p0 + wave; p < p1; p += NWAVE) {
-        float k0, k1, v0, v1;
+      const size_t hb = ((size_t)layer * HKV + xcd) * a.max_seq * D;
+      const uint32_t* kc = reinterpret_cast<const uint32_t*>(a.k_cache + hb);
+      const uint32_t* vc = reinterpret_cast<const uint32_t*>(a.v_cache + hb);
+      for (int i = 0; i < np_w; ++i) {
+        const int p = p0 + mw + NMW * i;
+        uint32_t kw, vw;
         if (p == position) {
-          k0 = s_k[2 * lane]; k1 = s_k[2 * lane + 1]; v0 = s_v[2 * lane]; v1 = s_v[2 * lane + 1];
+          kw = (uint32_t)f32_to_bf16(s_k[2 * lane]) | ((uint32_t)f32_to_bf16(s_k[2 * lane + 1]) << 16);
+          vw = (uint32_t)f32_to_bf16(s_v[2 * lane]) | ((uint32_t)f32_to_bf16(s_v[2 * lane + 1]) << 16);
+        } else if (i < APF) {
+          kw = kv_k[0]; vw = kv_v[0];
+#pragma unroll
+          for (int q = 1; q < APF; ++q) if (i == q) { kw = kv_k[q]; vw = kv_v[q]; }
         } else {
-          const uint32_t kw = kc[(size_t)p * (D / 2) + lane];
-          const uint32_t vw = vc[(size_t)p * (D / 2) + lane];
-          k0 = bf16_lo(kw); k1 = bf16_hi(kw); v0 = bf16_lo(vw); v1 = bf16_hi(vw);
+          kw = gp(kc)[(size_t)p * (D / 2) + lane];
+          vw = gp(vc)[(size_t)p * (D / 2) + lane];
         }
+        const float k0 = bf16_lo(kw), k1 = bf16_hi(kw), v0 = bf16_lo(vw), v1 = bf16_hi(vw);
         const float s0 = wave_sum(q00 * k0 + q01 * k1) * ATT_SCALE;
         const float s1 = wave_sum(q10 * k0 + q11 * k1) * ATT_SCALE;
         const float n0 = fmaxf(m0, s0), n1 = fmaxf(m1, s1);
@@ -365,157 +476,258 @@ __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
         a10 = a10 * c1 + e1 * v0; a11 = a11 * c1 + e1 * v1;
         m0 = n0; m1 = n1;
       }
-      // merge the 8 waves' partials in LDS, then publish this workgroup's partial
-      s_wpart[wave][0][2 * lane] = a00; s_wpart[wave][0][2 * lane + 1] = a01;
-      s_wpart[wave][1][2 * lane] = a10; s_wpart[wave][1][2 * lane + 1] = a11;
-      if (lane == 0) { s_wpart[wave][0][D] = m0; s_wpart[wave][0][D + 1] = l0; s_wpart[wave][1][D] = m1; s_wpart[wave][1][D + 1] = l1; }
-      __syncthreads();
-      if (threadIdx.x < 2 * D) {
-        const int h = threadIdx.x / D, d = threadIdx.x % D;
-        float M = -INFINITY;
+      s_wp[mw][0][2 * lane] = a00; s_wp[mw][0][2 * lane + 1] = a01;
+      s_wp[mw][1][2 * lane] = a10; s_wp[mw][1][2 * lane + 1] = a11;
+      if (lane == 0) { s_wp[mw][0][D] = m0; s_wp[mw][0][D + 1] = l0; s_wp[mw][1][D] = m1; s_wp[mw][1][D + 1] = l1; }
+    }
+    __syncthreads();
+    if (comm) {
+      // merge the 7 waves' partials: lane -> head h = lane / 32, dims 4*(lane % 32) .. +3
+      const int h = lane >> 5, d0 = (lane & 31) * 4;
+      float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, s_wpart[w][h][D]);
-        float acc = 0.f, L = 0.f;
-        if (M != -INFINITY) {
+      for (int w = 0; w < NMW; ++w) M = fmaxf(M, s_wp[w][h][D]);
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      float Lsum = 0.f;
+      if (M != -INFINITY) {
 #pragma unroll
-          for (int w = 0; w < NWAVE; ++w) {
-            const float mw = s_wpart[w][h][D];
-            if (mw != -INFINITY) {
-              const float f = expf(mw - M);
-              acc += s_wpart[w][h][d] * f;
-              L += s_wpart[w][h][D + 1] * f;
-            }
+        for (int w = 0; w < NMW; ++w) {
+          const float mw_ = s_wp[w][h][D];
+          if (mw_ != -INFINITY) {
+            const float f = expf(mw_ - M);
+            acc.x += s_wp[w][h][d0] * f; acc.y += s_wp[w][h][d0 + 1] * f;
+            acc.z += s_wp[w][h][d0 + 2] * f; acc.w += s_wp[w][h][d0 + 3] * f;
+            Lsum += s_wp[w][h][D + 1] * f;
           }
         }
-        float* dst = apart_x + ((size_t)j * 2 + h) * APS;
-        st_dev_f32(dst + d, acc);
-        if (d == 0) { st_dev_f32(dst + D, M); st_dev_f32(dst + D + 1, L); }
       }
+      float* dst = att_x + ((size_t)j * 2 + h) * APS;
+      if (j < S) {
+        st_local_f32(dst + d0, acc.x); st_local_f32(dst + d0 + 1, acc.y);
+        st_local_f32(dst + d0 + 2, acc.z); st_local_f32(dst + d0 + 3, acc.w);
+        if ((lane & 31) == 0) { st_local_f32(dst + D, M); st_local_f32(dst + D + 1, Lsum); }
+      }
+      store_fence();
+      mark(a, tl + 3);
+      if (lane == 0) st_local_u32(fl + fl_local(F_ATT, xcd) + j, ep);
+      poll_flags(c, fl + fl_local(F_ATT, xcd), S, ep);
+      mark(a, tl + 11);
+      // merge the S split partials of this XCD's two heads -> s_x[0, 256): lane jj < S reads
+      // split jj's (m, l) for both heads, the wave reduces them, then every lane accumulates its
+      // 4 dims of one head over the splits with the loads of a batch in flight together
+      float mj[2], lj[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float* src = att_x + ((size_t)(lane < S ? lane : 0) * 2 + hh) * APS;
+        mj[hh] = ld_dev_f32(src + D);
+        lj[hh] = ld_dev_f32(src + D + 1);
+        if (lane >= S) { mj[hh] = -INFINITY; lj[hh] = 0.f; }
+      }
+      float Mh[2], Lh[2], fh[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        Mh[hh] = wave_max(mj[hh]);
+        fh[hh] = mj[hh] == -INFINITY ? 0.f : expf(mj[hh] - Mh[hh]);
+        Lh[hh] = wave_sum(lj[hh] * fh[hh]);
+      }
+      float* s_f = &s_wp[0][0][0];  // merge weights [2][32], reusing the wave-partial buffer
+      if (lane < WPX) { s_f[lane] = fh[0]; s_f[WPX + lane] = fh[1]; }
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j0 = 0; j0 < S; j0 += 8) {
+        float4 aj[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int jj = j0 + q < S ? j0 + q : j0;
+          aj[q] = ld_dev_f32x4(att_x + ((size_t)jj * 2 + h) * APS, d0 * 4);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (j0 + q < S) {
+            const float f = s_f[h * WPX + j0 + q];
+            o.x += aj[q].x * f; o.y += aj[q].y * f; o.z += aj[q].z * f; o.w += aj[q].w * f;
+          }
+        }
+      }
+      const float inv = 1.f / Lh[h];
+      s_x[h * D + d0] = o.x * inv; s_x[h * D + d0 + 1] = o.y * inv;
+      s_x[h * D + d0 + 2] = o.z * inv; s_x[h * D + d0 + 3] = o.w * inv;
     }
-    mark(a, tl + 3);
-    xcd_barrier(sync);
+    __syncthreads();
+
+    // ---- C: o_proj partial over this group's 256 columns --------------------------------------
     mark(a, tl + 4);
-
-    // ---- C: merge 32 attention partials, o_proj partial over this group's 256 columns ----------
-    {
-      if (threadIdx.x < WPX * 2) {
-        const int jj = threadIdx.x >> 1, h = threadIdx.x & 1;
-        const float* src = apart_x + ((size_t)jj * 2 + h) * APS;
-        s_mw[jj][h][0] = ld_dev_f32(src + D);
-        s_mw[jj][h][1] = ld_dev_f32(src + D + 1);
-      }
-      __syncthreads();
-      if (threadIdx.x < 2 * D) {
-        const int h = threadIdx.x / D, d = threadIdx.x % D;
-        float M = -INFINITY;
-        for (int jj = 0; jj < WPX; ++jj) M = fmaxf(M, s_mw[jj][h][0]);
-        float acc = 0.f, L = 0.f;
-        for (int jj = 0; jj < WPX; ++jj) {
-          const float mj = s_mw[jj][h][0];
-          if (mj != -INFINITY) {
-            const float f = expf(mj - M);
-            acc += ld_dev_f32(apart_x + ((size_t)jj * 2 + h) * APS + d) * f;
-            L += s_mw[jj][h][1] * f;
-          }
-        }
-        s_x[h * D + d] = acc / L;
-      }
-      __syncthreads();
-      const uint16_t* wo = (const uint16_t*)lw.o_proj_weight;
-      const int row0 = HPW * j;
-      gemv<2 * D, 1>(HPW, [&](int r) { return wo + (size_t)(row0 + r) * (HQ * D) + 2 * D * xcd; }, s_x,
-                     [&](int r, int, float v) { st_dev_f32(opart + (size_t)xcd * H + row0 + r, v); });
+    if (!comm) {
+      const int gq = opaque(g), tq = opaque(t);
+      load_units<PE, UPR_E>(wE, 0, U_E, gq, tq, ptr_E(lw));
+      gemv_phase<NU_C, PC, UPR_C>(wC, U_C, gq, tq, ptr_C(lw), s_x, s_up);
     }
-    mark(a, tl + 5);
-    grid_barrier(sync);
-    mark(a, tl + 6);
-
-    // ---- D: residual += o_proj, post-attention RMSNorm, gate/up rows of slice x ---------------
-    add_partials<H>(s_res, opart);
-    rms_norm<H>(s_res, (const uint16_t*)lw.post_attn_norm_weight, s_x, s_red);
-    {
-      const uint16_t* wg = (const uint16_t*)lw.gate_proj_weight;
-      const uint16_t* wu = (const uint16_t*)lw.up_proj_weight;
-      const int row0 = IX * xcd + IPW * j;
-      gemv<H, GU_S>(2 * IPW,
-                    [&](int r) { return (r < IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - IPW) * H); },
-                    s_x, [&](int r, int sg, float v) { s_part[r * GU_S + sg] = v; });
-      __syncthreads();
-      if (threadIdx.x < IPW) {
-        float g = 0.f, u = 0.f;
+    __syncthreads();
+    if (comm) {
+      float* gc = ws + W_GC + (size_t)j * NXCD * MAX_HPW;  // [8][MAX_HPW] for row block j
+      if (lane < HPW) st_dev_f32(gc + xcd * MAX_HPW + lane, s_up[lane * UPR_C] + s_up[lane * UPR_C + 1]);
+      store_fence();
+      mark(a, tl + 5);
+      if (lane == 0) st_dev_u32(fl + fl_cross(0, j, xcd), ep);
+      poll_flags(c, fl + fl_cross(0, j, 0), NXCD, ep, SLOT);
+      mark(a, tl + 12);
+      if (lane < HPW) {
+        float s = 0.f;
 #pragma unroll
-        for (int sg = 0; sg < GU_S; ++sg) { g += s_part[threadIdx.x * GU_S + sg]; u += s_part[(threadIdx.x + IPW) * GU_S + sg]; }
-        const float m = g / (1.f + expf(-g)) * u;  // silu(g) * u, /root/reference/config.cuh:177-179
-        st_dev_f32(mbuf_x + IPW * j + threadIdx.x, m);
+        for (int y = 0; y < NXCD; ++y) s += ld_dev_f32(gc + y * MAX_HPW + lane);
+        st_local_f32(lc_x + HPW * j + lane, s);
+      }
+      store_fence();
+      if (lane == 0) st_local_u32(fl + fl_local(F_LC, xcd) + j, ep);
+      poll_flags(c, fl + fl_local(F_LC, xcd), WPX, ep);
+      mark(a, tl + 13);
+      comm_residual_norm<H>(s_res, lc_x, (const uint16_t*)lw.post_attn_norm_weight, s_x);
+    }
+    __syncthreads();
+
+    // ---- D: gate/up rows of MLP slice x ------------------------------------------------------
+    mark(a, tl + 6);
+    if (!comm) {
+      const int gq = opaque(g), tq = opaque(t);
+      if (layer + 1 < L) load_units<PA, UPR_H>(wA, 0, U_A, gq, tq, ptr_A(a.layers[layer + 1]));
+      gemv_phase<NU_D, PD, UPR_H>(wD, U_D, gq, tq, ptr_D(lw), s_x, s_up);
+    }
+    __syncthreads();
+    if (comm) {
+      if (lane < IPW) {
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int b = 0; b < UPR_H; ++b) { gs += s_up[lane * UPR_H + b]; us += s_up[(lane + IPW) * UPR_H + b]; }
+        st_local_f32(m_x + IPW * j + lane, gs / (1.f + expf(-gs)) * us);  // silu(g) * u
+      }
+      store_fence();
+      mark(a, tl + 7);
+      if (lane == 0) st_local_u32(fl + fl_local(F_M, xcd) + j, ep);
+      poll_flags(c, fl + fl_local(F_M, xcd), WPX, ep);
+      mark(a, tl + 14);
+      for (int i = lane * 4; i < IX; i += 256) {
+        const float4 v = ld_dev_f32x4(m_x, i * 4);
+        *reinterpret_cast<float4*>(s_x + i) = v;
       }
     }
-    mark(a, tl + 7);
-    xcd_barrier(sync);
-    mark(a, tl + 8);
+    __syncthreads();
 
-    // ---- E: down_proj partial over slice x's columns ------------------------------------------
-    {
-      fetch_dev(mbuf_x, s_x, IX);
-      __syncthreads();
-      const uint16_t* wd = (const uint16_t*)lw.down_proj_weight;
-      const int row0 = HPW * j;
-      gemv<IX, 1>(HPW, [&](int r) { return wd + (size_t)(row0 + r) * I + IX * xcd; }, s_x,
-                  [&](int r, int, float v) { st_dev_f32(dpart + (size_t)xcd * H + row0 + r, v); });
+    // ---- E: down_proj partial over slice x's columns -----------------------------------------
+    mark(a, tl + 8);
+    if (!comm) gemv_phase<NU_E, PE, UPR_E>(wE, U_E, opaque(g), opaque(t), ptr_E(lw), s_x, s_up);
+    __syncthreads();
+    if (comm) {
+      float* ge = ws + W_GE + (size_t)j * NXCD * MAX_HPW;
+      if (lane < HPW) {
+        float s = 0.f;
+#pragma unroll
+        for (int b = 0; b < UPR_E; ++b) s += s_up[lane * UPR_E + b];
+        st_dev_f32(ge + xcd * MAX_HPW + lane, s);
+      }
+      store_fence();
+      mark(a, tl + 9);
+      if (lane == 0) st_dev_u32(fl + fl_cross(1, j, xcd), ep);
+      poll_flags(c, fl + fl_cross(1, j, 0), NXCD, ep, SLOT);
+      mark(a, tl + 15);
+      if (lane < HPW) {
+        float s = 0.f;
+#pragma unroll
+        for (int y = 0; y < NXCD; ++y) s += ld_dev_f32(ge + y * MAX_HPW + lane);
+        st_local_f32(le_x + HPW * j + lane, s);
+      }
+      store_fence();
+      if (lane == 0) st_local_u32(fl + fl_local(F_LE, xcd) + j, ep);
+      poll_flags(c, fl + fl_local(F_LE, xcd), WPX, ep);
+      mark(a, tl + 16);
+      const uint16_t* nw = layer + 1 < L ? (const uint16_t*)a.layers[layer + 1].norm_weight : a.final_norm;
+      comm_residual_norm<H>(s_res, le_x, nw, s_x);
     }
-    mark(a, tl + 9);
-    grid_barrier(sync);
+    __syncthreads();
   }
 
-  // ---- final RMSNorm, tied LM head, argmax ------------------------------------------------------
-  mark(a, tb + 1);
-  add_partials<H>(s_res, dpart);
-  rms_norm<H>(s_res, a.final_norm, s_x, s_red);
-  mark(a, tb + 2);
+  // ---- tied LM head over rows [r0, r1), greedy argmax ------------------------------------------
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 1);
   {
     const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
     const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
-    unsigned long long best = 0;
-    gemv<H, 1>(r1 - r0, [&](int r) { return a.lm_head + (size_t)(r0 + r) * H; }, s_x, [&](int r, int, float v) {
-      a.logits[r0 + r] = v;
-      const unsigned long long k = argmax_key(v, r0 + r);
-      best = k > best ? k : best;
-    });
-    // workgroup max of the per-thread keys (only group leaders hold non-zero keys)
-    unsigned long long* s_best = reinterpret_cast<unsigned long long*>(s_wpart);
-    for (int off = 32; off >= 1; off >>= 1) {
-      const unsigned long long o = __shfl_xor(best, off);
-      best = o > best ? o : best;
-    }
-    if (lane == 0) s_best[wave] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned long long b = 0;
-      for (int w = 0; w < NWAVE; ++w) b = s_best[w] > b ? s_best[w] : b;
-      __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(a.ctr + L_AMAX * CTR_LINE), b,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-
-  mark(a, tb + 3);
-  // ---- exit: the last workgroup out publishes the token and resets the counters ---------------
-  wait_vmem();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_fetch_add(a.ctr + (L_XEXIT + xcd) * CTR_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == WPX - 1) {
-      old = __hip_atomic_fetch_add(a.ctr + L_GEXIT * CTR_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == NXCD - 1) {
-        unsigned long long* amax = reinterpret_cast<unsigned long long*>(a.ctr + L_AMAX * CTR_LINE);
-        const unsigned long long b = __hip_atomic_load(amax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (a.out_token) *a.out_token = b ? (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu)) : -1;
-        __hip_atomic_store(amax, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int x = 0; x < NXCD; ++x) {
-          st_dev_u32(a.ctr + (L_XL + x) * CTR_LINE, 0u);
-          st_dev_u32(a.ctr + (L_XG + x) * CTR_LINE, 0u);
-          st_dev_u32(a.ctr + (L_XEXIT + x) * CTR_LINE, 0u);
+    mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 2);
+    if (!comm) {
+      unsigned long long best = 0;
+      // each group takes whole rows r0+g, r0+g+28, ...; a row is SEG segments of 8 chunks per lane;
+      // the next segment's loads are issued before the current one is consumed
+      constexpr int SEG = UPR_H / 8;
+      const int gq = opaque(g), tq = opaque(t);
+      int r = r0 + gq;
+      int sg = 0;
+      uint4 cur[8], nxt[8];
+      auto seg_ptr = [&](int row, int seg) {
+        return reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + 128 * seg + tq;
+      };
+      {
+        const int rl = r < r1 ? r : r0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) cur[b] = ld_stream(seg_ptr(rl, 0) + 16 * b);
+      }
+      float acc = 0.f;
+      while (r < r1) {
+        const int sn = sg + 1 == SEG ? 0 : sg + 1;
+        const int rn = sg + 1 == SEG ? r + MG : r;
+        {
+          const int rl = rn < r1 ? rn : r;  // past the end: re-read the current segment, unused
+          const int sl = rn < r1 ? sn : sg;
+#pragma unroll
+          for (int b = 0; b < 8; ++b) nxt[b] = ld_stream(seg_ptr(rl, sl) + 16 * b);
         }
-        st_dev_u32(a.ctr + L_G * CTR_LINE, 0u);
-        st_dev_u32(a.ctr + L_GEXIT * CTR_LINE, 0u);
+        const float* xs = s_x + 1024 * sg + tq * 8;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc = dot8(cur[b], xs + 128 * b, acc);
+        if (sg + 1 == SEG) {
+          const float v = row16_sum(acc);
+          if (tq == 0) {
+            gpw(a.logits)[r] = v;
+            best = umax64(best, argmax_key(v, r));
+          }
+          acc = 0.f;
+        }
+#pragma unroll
+        for (int b = 0; b < 8; ++b) cur[b] = nxt[b];
+        r = rn;
+        sg = sn;
+      }
+      for (int off = 32; off >= 1; off >>= 1) best = umax64(best, __shfl_xor(best, off));
+      if (lane == 0) s_best[mw] = best;
+    }
+    __syncthreads();
+    mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 3);
+    if (comm) {
+      const uint32_t ep_end = (seq << 6) | 63u;
+      unsigned long long b = 0;
+#pragma unroll
+      for (int w = 0; w < NMW; ++w) b = umax64(b, s_best[w]);
+      // this workgroup's best key and done flag, in its own slot: key first, flag after it
+      uint32_t* mine = fl + fl_done(blockIdx.x);
+      if (lane == 0) __hip_atomic_store(reinterpret_cast<unsigned long long*>(mine + 2), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store_fence();
+      if (lane == 0) st_dev_u32(mine, ep_end);
+      if (blockIdx.x == 0) {
+        // the grid's greedy token: poll all 256 done flags (4 per lane), then reduce the keys
+        for (uint32_t it = 0; !c.failed; ++it) {
+          bool ok = true;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ok &= ld_dev_u32(fl + fl_done(lane * 4 + q)) == ep_end;
+          if (__ballot(!ok) == 0) break;
+          if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) c.failed = true;
+          if (it > SPIN_LIMIT) { if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT); c.failed = true; }
+        }
+        unsigned long long m = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          m = umax64(m, __hip_atomic_load(reinterpret_cast<unsigned long long*>(fl + fl_done(lane * 4 + q) + 2),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        for (int off = 32; off >= 1; off >>= 1) m = umax64(m, __shfl_xor(m, off));
+        if (lane == 0) {
+          if (a.out_token) *gpw(a.out_token) = m ? (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu)) : -1;
+          st_dev_u32(fl + FL_SEQ, seq + 1);  // every workgroup read seq at its start
+        }
       }
     }
   }
@@ -542,6 +754,17 @@ static hipError_t check_kernel_fits() {
   return blocks >= 1 ? hipSuccess : hipErrorCooperativeLaunchTooLarge;
 }
 
+// Zero every flag and start the launch sequence at 1 (flag value 0 never matches an epoch).
+static hipError_t clear_flags(void* ws) {
+  char* fl = (char*)ws + WS_FLOATS * 4;
+  hipError_t e = hipMemset(fl, 0, FL_WORDS * 4);
+  if (e != hipSuccess) return e;
+  const uint32_t one = 1;
+  e = hipMemcpy(fl + FL_SEQ * 4, &one, 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return e;
+  return hipDeviceSynchronize();
+}
+
 static hipError_t device_state(DeviceState** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -559,7 +782,7 @@ static hipError_t device_state(DeviceState** out) {
     if ((e = check_kernel_fits<2048, 6144>()) != hipSuccess) return e;
     if ((e = hipMalloc(&s.ws, WS_BYTES)) != hipSuccess) return e;
     if ((e = hipMemset(s.ws, 0, WS_BYTES)) != hipSuccess) return e;
-    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    if ((e = clear_flags(s.ws)) != hipSuccess) return e;
     s.ok = true;
   }
   if (!s.ok) return hipErrorNotSupported;
@@ -587,7 +810,7 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
     return hipErrorInvalidValue;
   const bool s06 = dims->hidden == 1024 && dims->intermediate == 3072;
   const bool s17 = dims->hidden == 2048 && dims->intermediate == 6144;
-  if (!(s06 || s17) || dims->num_layers < 1 || dims->vocab < NWG) return hipErrorInvalidValue;
+  if (!(s06 || s17) || dims->num_layers < 1 || dims->num_layers > MAX_LAYERS || dims->vocab < NWG) return hipErrorInvalidValue;
   if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
   if (max_seq_len < 1 || position < 0 || position >= max_seq_len) return hipErrorInvalidValue;
   DeviceState* st = nullptr;
@@ -605,7 +828,7 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.logits = logits;
   k.out_token = out_token;
   k.ws = (float*)st->ws;
-  k.ctr = (uint32_t*)((char*)st->ws + WS_FLOATS * 4);
+  k.fl = (uint32_t*)((char*)st->ws + WS_FLOATS * 4);
   k.trace = st->trace;
   k.token = token_id;
   k.position = position;
@@ -637,7 +860,7 @@ extern "C" hipError_t mk_status(uint32_t* status) {
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  return hipMemcpy(status, (char*)st->ws + WS_FLOATS * 4 + (size_t)L_STATUS * CTR_LINE * 4, 4, hipMemcpyDeviceToHost);
+  return hipMemcpy(status, (char*)st->ws + WS_FLOATS * 4 + FL_STATUS * 4, 4, hipMemcpyDeviceToHost);
 }
 
 extern "C" hipError_t mk_reset(void) {
@@ -645,8 +868,7 @@ extern "C" hipError_t mk_reset(void) {
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  if ((e = hipMemset((char*)st->ws + WS_FLOATS * 4, 0, (size_t)N_LINES * CTR_LINE * 4)) != hipSuccess) return e;
-  return hipDeviceSynchronize();
+  return clear_flags(st->ws);
 }
 
 extern "C" hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes) {
@@ -665,4 +887,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.1 (gfx950, xcd-aware v1)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.2 (gfx950; comm/math waves, flag exchanges)"; }

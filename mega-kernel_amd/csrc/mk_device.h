@@ -80,10 +80,30 @@ __device__ __forceinline__ void st_dev_f32x4(float* base, uint32_t byte_off, flo
   __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), byte_off, 0, CPOL_SC1);
 }
 
+// Global-address-space views. Pointers that come out of memory (the layer table) or through
+// lambdas are generic to the compiler, and generic accesses become FLAT instructions, which count
+// against the LDS counter as well as the vector-memory counter: every LDS wait would then also
+// wait for all outstanding weight loads. These casts keep such accesses global.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gp(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gpw(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
+// 16-byte global load (cached).
+__device__ __forceinline__ uint4 ld_global16(const uint4* p) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  u4 v = *(const __attribute__((address_space(1))) u4*)p;
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // Weight stream: 16 bytes, non-temporal (each weight byte is read once per token).
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
-  u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  u4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u4*)p);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
