@@ -177,5 +177,19 @@ def main():
     return 0
 
 
+def release_device():
+    """Free the cached device memory and drain the GPU before interpreter exit, so that an
+    attached profiler (rocprofv3) finalizes its output before the runtime tears down."""
+    torch = sys.modules.get("torch")
+    if torch is not None and torch.cuda.is_initialized():
+        import gc
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
 if __name__ == "__main__":
-    sys.exit(main())
+    rc = main()
+    release_device()
+    if rc:
+        sys.exit(rc)
