@@ -58,8 +58,9 @@ struct Checked {
 Checked validate(int64_t token_id, const torch::Tensor& embed, const torch::Tensor& lm_head,
                  const torch::Tensor& final_norm, const std::vector<torch::Tensor>& lw,
                  const torch::Tensor& cos, const torch::Tensor& sin, const torch::Tensor& kc,
-                 const torch::Tensor& vc, int64_t position, int64_t max_seq_len) {
-  TORCH_CHECK(embed.defined() && embed.is_cuda(), "megakernel: embed_weight must be a GPU tensor");
+                 const torch::Tensor& vc, int64_t position, int64_t max_seq_len, bool require_gpu = true) {
+  TORCH_CHECK(embed.defined(), "megakernel: embed_weight is undefined");
+  TORCH_CHECK(!require_gpu || embed.is_cuda(), "megakernel: embed_weight must be a GPU tensor");
   TORCH_CHECK(embed.dim() == 2, "megakernel: embed_weight must be [vocab, hidden]");
   const torch::Device dev = embed.device();
   const int64_t V = embed.size(0), H = embed.size(1);
@@ -169,6 +170,16 @@ int64_t status() {
 
 void reset() { MK_HIP_CHECK(mk_reset()); }
 
+// Runs decode's argument validation only (tensors may live on any one device, nothing is
+// launched) and returns (hidden, intermediate, num_layers, vocab). For host-side tests.
+std::tuple<int64_t, int64_t, int64_t, int64_t> check_args(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
+                                                           torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                           torch::Tensor cos, torch::Tensor sin, torch::Tensor kc,
+                                                           torch::Tensor vc, int64_t position, int64_t max_seq_len) {
+  Checked c = validate(token_id, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len, false);
+  return {c.dims.hidden, c.dims.intermediate, c.dims.num_layers, c.dims.vocab};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -176,5 +187,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_greedy", &decode_greedy, "Qwen3 single-token decode; returns (fp32 logits, int32 greedy token on device)");
   m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
   m.def("reset", &reset, "clear the decode workspace's status word and barrier counters; synchronizes");
+  m.def("check_args", &check_args, "validate decode's arguments without launching; returns (hidden, intermediate, layers, vocab)");
   m.def("version", []() { return std::string(mk_version()); });
 }

@@ -124,3 +124,35 @@ def greedy_reference(model, ids, steps):
 def cpu_threads():
     """Threads the CPU baseline uses: every core this process may run on."""
     return len(os.sched_getaffinity(0))
+
+
+def float64_decode_step(model, k_cache, v_cache, token, position, cos, sin):
+    """Transformers' own decode step run in float64, with the kernel's inputs: the bf16 cache
+    ``[L, Hkv, max_seq, D]`` (positions ``[0, position)``), the bf16 RoPE tables ``cos``/``sin``
+    ``[max_seq, D]`` and the new K/V rounded to bf16 as the kernel stores them before attending
+    (the reference kernel writes K/V to the cache and attention reads them back,
+    ``/root/reference/megakernel.cu:613-619``, ``:270-309``). Returns float64 logits [V].
+
+    This is the independent pin of the float32 restatement (``restate.decode_step(...,
+    numerics="fp32")``): same inputs, Transformers' code (``modeling_qwen3.py:241-323``, eager
+    attention with a float32 softmax) at higher precision, so the two may differ only by float32
+    rounding. Does not modify ``model`` or the caches."""
+    import copy
+
+    from transformers import DynamicCache
+
+    m = copy.deepcopy(model).double()
+    m.config._attn_implementation = "eager"
+    m.model.rotary_emb.forward = lambda x, pos: (cos[pos].double(), sin[pos].double())
+    cache = DynamicCache()
+    for layer in range(k_cache.shape[0]):
+        cache.update(k_cache[layer:layer + 1, :, :position].double(), v_cache[layer:layer + 1, :, :position].double(),
+                     layer)
+    for cl in cache.layers:
+        upd = cl.update
+        cl.update = (lambda k, v, *a, upd=upd, **kw:
+                     upd(k.to(torch.bfloat16).double(), v.to(torch.bfloat16).double(), *a, **kw))
+    with torch.inference_mode():
+        out = m(torch.tensor([[int(token)]]), past_key_values=cache, use_cache=True,
+                position_ids=torch.tensor([[int(position)]]))
+    return out.logits[0, -1].clone()

@@ -240,3 +240,27 @@ def argmax_bf16(logits):
     """Greedy token over bf16-rounded logits, lowest index on ties (what ``torch.argmax`` returns
     for the bf16 logits Transformers emits)."""
     return int(torch.argmax(bf16(logits)))
+
+
+def attention_split(q, k, v, scale, splits):
+    """Split-K ("flash-decoding") form of ``attention_fp32``: the keys are cut into ``splits``
+    contiguous ranges, each range yields a partial (running max m, sum l, unnormalised acc), and the
+    partials are merged with weights ``exp(m_s - max_s m_s)``; empty ranges contribute nothing.
+    This is the decomposition the HIP kernel uses across workgroups; softmax is invariant to it, so
+    it must equal ``attention_fp32`` up to float32 rounding for every split count."""
+    rep = q.shape[0] // k.shape[0]
+    kr, vr = k.repeat_interleave(rep, 0), v.repeat_interleave(rep, 0)
+    L = k.shape[1]
+    parts = []
+    for sidx in range(splits):
+        a, b = (L * sidx) // splits, (L * (sidx + 1)) // splits
+        if a == b:
+            continue
+        s = torch.einsum("hd,hld->hl", q, kr[:, a:b]) * scale
+        m = s.amax(-1, keepdim=True)
+        e = torch.exp(s - m)
+        parts.append((m, e.sum(-1, keepdim=True), torch.einsum("hl,hld->hd", e, vr[:, a:b])))
+    M = torch.stack([p[0] for p in parts]).amax(0)
+    lsum = sum(p[1] * torch.exp(p[0] - M) for p in parts)
+    acc = sum(p[2] * torch.exp(p[0] - M) for p in parts)
+    return acc / lsum

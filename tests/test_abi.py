@@ -1,0 +1,145 @@
+"""Host-side tests of the drop-in boundary: the C-ABI library and the PyTorch operator load, export
+what ``include/megakernel_amd.h`` declares, and reject bad arguments before anything is launched
+(the reference validates nothing, /root/reference/pytorch_binding.cu:36-129; its errors surface only
+from CUDA calls). No GPU is used: every call here returns before the first HIP runtime call."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from megakernel import build as mkbuild
+
+HEADER = os.path.join(mkbuild.INCLUDE, "megakernel_amd.h")
+HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(mk_\w+|launch_decode_kernel)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert os.path.exists(mkbuild.LIB), "libmegakernel_amd.so is not built (run __graft_entry__.build())"
+    return ctypes.CDLL(mkbuild.LIB)
+
+
+def test_header_declares_the_reference_launcher_and_the_library_exports_everything(lib):
+    names = declared_functions()
+    assert "launch_decode_kernel" in names and "mk_decode" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in megakernel_amd.h but not exported"
+
+
+def test_version(lib):
+    lib.mk_version.restype = ctypes.c_char_p
+    assert lib.mk_version().decode().startswith("megakernel_amd")
+
+
+def test_trace_bytes(lib):
+    lib.mk_trace_bytes.restype = ctypes.c_size_t
+    n = lib.mk_trace_bytes()
+    assert n > 0 and n % 8 == 0
+
+
+def test_c_abi_rejects_bad_arguments_before_launch(lib):
+    """hipErrorInvalidValue for a null shape, an unsupported shape, a token or position out of range
+    and (reference launcher) cache_len != position + 1 -- no device is touched."""
+    f = lib.mk_decode
+    f.restype = ctypes.c_int
+    vp = ctypes.c_void_p
+    f.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    dummy = vp(16)
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                    ("num_layers", ctypes.c_int32), ("vocab", ctypes.c_int32)]
+
+    def call(dims, token=1, position=3, max_seq=512, logits=dummy):
+        d = ctypes.byref(dims) if dims is not None else None
+        return f(d, token, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, position, max_seq, logits, None, None)
+
+    good = Dims(1024, 3072, 28, 151936)
+    assert call(None) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 4096, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 0, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(good, token=-1) == HIP_ERROR_INVALID_VALUE
+    assert call(good, token=151936) == HIP_ERROR_INVALID_VALUE
+    assert call(good, position=512) == HIP_ERROR_INVALID_VALUE
+    assert call(good, position=-1) == HIP_ERROR_INVALID_VALUE
+    assert call(good, logits=None) == HIP_ERROR_INVALID_VALUE
+
+    g = lib.launch_decode_kernel
+    g.restype = ctypes.c_int
+    g.argtypes = [ctypes.c_int] + [vp] * 18 + [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+    assert g(1, *([dummy] * 18), 10, 10, 512, None) == HIP_ERROR_INVALID_VALUE  # cache_len must be position + 1
+
+
+# ---------------------------------------------------------------------------------------------
+# the PyTorch operator (reference name and signature)
+# ---------------------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def ext():
+    import megakernel
+    return megakernel.load()
+
+
+def _args(L=2, V=300, max_seq=16, dtype=torch.bfloat16):
+    """A well-formed argument list on the CPU: the 0.6B layer shapes (hidden 1024, intermediate
+    3072, 16 q / 8 kv heads of 128) with few layers, a small vocabulary and a short cache."""
+    H, I = 1024, 3072
+    mk = lambda *s: torch.zeros(*s, dtype=dtype)
+    lw = []
+    for _ in range(L):
+        lw += [mk(H), mk(2048, H), mk(1024, H), mk(1024, H), mk(128), mk(128), mk(H, 2048), mk(H), mk(I, H),
+               mk(I, H), mk(H, I)]
+    embed = mk(V, H)
+    return [5, embed, embed, mk(H), lw, mk(max_seq, 128), mk(max_seq, 128), mk(L, 8, max_seq, 128),
+            mk(L, 8, max_seq, 128), 3, max_seq]
+
+
+def test_operator_exports_reference_entry_point(ext):
+    assert callable(ext.decode) and callable(ext.decode_greedy)
+    assert ext.version().startswith("megakernel_amd")
+
+
+def test_operator_requires_gpu_tensors(ext):
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        ext.decode(*_args())
+
+
+def test_check_args_accepts_well_formed_input(ext):
+    assert ext.check_args(*_args()) == (1024, 3072, 2, 300)
+
+
+@pytest.mark.parametrize("mutate, message", [
+    (lambda a: a.__setitem__(0, 300), "token_id"),
+    (lambda a: a.__setitem__(0, -1), "token_id"),
+    (lambda a: a.__setitem__(9, 16), "position"),
+    (lambda a: a.__setitem__(9, -1), "position"),
+    (lambda a: a.__setitem__(4, a[4][:-1]), "11 tensors per layer"),
+    (lambda a: a.__setitem__(1, a[1].float()), "bfloat16"),
+    (lambda a: a.__setitem__(7, a[7].transpose(2, 3).contiguous().transpose(2, 3)), "contiguous"),
+    (lambda a: a.__setitem__(7, a[7][:, :, :8].contiguous()), "k_cache"),
+    (lambda a: a.__setitem__(8, a[7]), "distinct"),
+    (lambda a: a.__setitem__(5, a[5][:8].contiguous()), "cos/sin"),
+    (lambda a: a[4].__setitem__(1, torch.zeros(2048, 512, dtype=torch.bfloat16)), "q_proj"),
+    (lambda a: a.__setitem__(3, torch.zeros(1023, dtype=torch.bfloat16)), "final_norm"),
+])
+def test_check_args_rejects(ext, mutate, message):
+    a = _args()
+    mutate(a)
+    with pytest.raises(RuntimeError, match=message):
+        ext.check_args(*a)
+
+
+def test_unsupported_shape_is_rejected(ext):
+    a = _args()
+    for i in range(len(a[4])):
+        if a[4][i].dim() == 2 and a[4][i].shape[0] == 3072:
+            a[4][i] = torch.zeros(4096, 1024, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="supported"):
+        ext.check_args(*a)

@@ -1,0 +1,235 @@
+"""CPU tests that pin the oracle (``oracle/``) before anything is checked against it.
+
+The reference ships no tests or known-answer vectors for its decode path (its arithmetic is
+Transformers', driven from /root/reference/model.py:72-73, :159-172), so the oracle is pinned by:
+  * golden vectors written by Transformers itself (``tests/golden/make_golden.py``): the bf16
+    restatement must reproduce them bit for bit;
+  * Transformers' own code run in float64 on the kernel's inputs (``oracle.hf.float64_decode_step``):
+    the float32 restatement -- the numerics the HIP kernel implements -- must agree to float32
+    rounding;
+  * closed forms and invariants on small inputs, brute-forced in float64 with plain loops: RMSNorm,
+    RoPE as a rotation, GQA head mapping, softmax attention, split-K merge invariance, SDPA
+    behaviour of torch's CPU flash kernel, fexp_u20 error, the argmax tie rule, the cache slot.
+"""
+import math
+import os
+
+import pytest
+import torch
+from safetensors.torch import load_file
+
+from oracle import hf, restate
+from oracle.spec import LAYER_WEIGHT_ORDER, SHAPES
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_decode.safetensors")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    g = load_file(GOLDEN)
+    s = SHAPES["tiny"]
+    lw = [g[f"layer_weights.{i:03d}"] for i in range(len(LAYER_WEIGHT_ORDER) * s.layers)]
+    g["W"] = restate.Weights(g["embed"], lw, g["final_norm"], s)
+    g["P"] = int(g["prompt_ids"].numel())
+    return g
+
+
+def _lanes():
+    cap = torch.backends.cpu.get_cpu_capability()
+    return 16 if "512" in cap else 8
+
+
+def test_golden_fixture_shapes(golden):
+    s = SHAPES["tiny"]
+    assert golden["k_cache"].shape == (s.layers, s.kv_heads, 32, s.head_dim)
+    assert golden["k_cache"].dtype == torch.bfloat16
+    assert golden["logits"].shape == (golden["tokens"].numel(), s.vocab)
+    P = golden["P"]
+    assert golden["k_cache"][:, :, P:].abs().sum() == 0  # only the prompt is cached
+    # the fed tokens are Transformers' own greedy chain (first index on ties, model.py:97)
+    assert int(golden["tokens"][0]) == int(golden["prefill_logits"].float().argmax())
+    for t in range(1, golden["tokens"].numel()):
+        assert int(golden["tokens"][t]) == int(golden["logits"][t - 1].float().argmax())
+
+
+def test_bf16_restatement_reproduces_transformers_bit_exact(golden):
+    """The bf16-rounding restatement equals Transformers' CPU decode logits exactly, every step."""
+    kc, vc = golden["k_cache"].clone(), golden["v_cache"].clone()
+    for t in range(golden["tokens"].numel()):
+        tok, pos = int(golden["tokens"][t]), golden["P"] + t
+        got, _ = restate.decode_step(golden["W"], kc, vc, tok, pos, golden["cos"], golden["sin"], numerics="hf",
+                                     lanes=_lanes())
+        want = golden["logits"][t].float()
+        assert torch.equal(restate.bf16(got), want), f"step {t}: max|d| {(restate.bf16(got) - want).abs().max()}"
+
+
+def test_fp32_restatement_matches_transformers_float64(golden):
+    """The float32 restatement (the kernel's numerics) against Transformers' own forward in float64
+    on the same inputs: they may differ only by float32 rounding."""
+    model = hf.build_model("tiny", max_positions=32)
+    # the rebuilt model is the one the fixture was written from
+    assert torch.equal(model.model.embed_tokens.weight.detach(), golden["embed"])
+    kc, vc = golden["k_cache"].clone(), golden["v_cache"].clone()
+    for t in range(3):
+        tok, pos = int(golden["tokens"][t]), golden["P"] + t
+        ref = hf.float64_decode_step(model, kc, vc, tok, pos, golden["cos"], golden["sin"])
+        got, _ = restate.decode_step(golden["W"], kc, vc, tok, pos, golden["cos"], golden["sin"], numerics="fp32")
+        err = (got.double() - ref).abs().max().item()
+        assert err < 2e-6, f"step {t}: {err}"
+
+
+def test_fp32_restatement_within_bf16_noise_of_golden(golden):
+    kc, vc = golden["k_cache"].clone(), golden["v_cache"].clone()
+    for t in range(golden["tokens"].numel()):
+        tok, pos = int(golden["tokens"][t]), golden["P"] + t
+        got, _ = restate.decode_step(golden["W"], kc, vc, tok, pos, golden["cos"], golden["sin"], numerics="fp32")
+        want = golden["logits"][t].float()
+        assert (got - want).abs().max().item() < 8e-3
+        assert restate.argmax_bf16(got) == int(want.argmax())
+
+
+@pytest.mark.slow
+def test_mini_fp32_restatement_matches_transformers_float64():
+    """Same pin at the kernel's head geometry (16 q / 8 kv heads of 128, hidden 1024)."""
+    model = hf.build_model("mini", max_positions=128)
+    s = SHAPES["mini"]
+    ids = hf.prompt_ids(24, s.vocab)
+    last, cache = hf.prefill(model, ids)
+    kc, vc = hf.cache_to_kernel_layout(cache, s.layers, s.kv_heads, 64, s.head_dim)
+    cos, sin = hf.rope_tables(model, 64)
+    tok = int(last.float().argmax())
+    ref = hf.float64_decode_step(model, kc, vc, tok, 24, cos, sin)
+    got, _ = restate.decode_step(restate.Weights.from_model(model, s), kc, vc, tok, 24, cos, sin, numerics="fp32")
+    assert (got.double() - ref).abs().max().item() < 1e-5
+
+
+# ---------------------------------------------------------------------------------------------
+# closed forms and invariants
+# ---------------------------------------------------------------------------------------------
+def test_rms_norm_closed_form():
+    g = torch.Generator().manual_seed(3)
+    x = restate.bf16(torch.randn(64, generator=g))
+    w = restate.bf16(torch.rand(64, generator=g) + 0.5)
+    got = restate.rms_norm_hf(x, w, 1e-6)
+    for i in range(64):
+        ms = sum(float(v) ** 2 for v in x) / 64
+        exact = float(w[i]) * float(x[i]) / math.sqrt(ms + 1e-6)
+        assert abs(float(got[i]) - exact) <= 2 * 2.0 ** -8 * abs(exact) + 1e-30
+
+
+def test_rope_is_a_rotation_by_position_angle():
+    """rotate-half RoPE: dims (i, i + D/2) rotate by angle p * theta**(-2i/D)."""
+    D, p, theta = 16, 5, 1e6
+    g = torch.Generator().manual_seed(4)
+    x = restate.bf16(torch.randn(D, generator=g))
+    ang = torch.tensor([p * theta ** (-2 * (i % (D // 2)) / D) for i in range(D)], dtype=torch.float64)
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    got = restate.rope_hf(x, cos, sin)
+    for i in range(D // 2):
+        a, b = float(x[i]), float(x[i + D // 2])
+        c, s = math.cos(float(ang[i])), math.sin(float(ang[i]))
+        assert abs(float(got[i]) - (a * c - b * s)) < 2e-2 * (abs(a) + abs(b)) + 1e-6
+        assert abs(float(got[i + D // 2]) - (b * c + a * s)) < 2e-2 * (abs(a) + abs(b)) + 1e-6
+    # position 0 is the identity
+    assert torch.equal(restate.rope_hf(x, torch.ones(D), torch.zeros(D)), x)
+
+
+def _attention_loops(q, k, v, scale):
+    """Brute-force float64 attention with GQA mapping kv = h // (Hq / Hkv)."""
+    hq, d = q.shape
+    hkv, L, _ = k.shape
+    out = torch.zeros(hq, d, dtype=torch.float64)
+    for h in range(hq):
+        kvh = h // (hq // hkv)
+        s = [sum(float(q[h, i]) * float(k[kvh, j, i]) for i in range(d)) * scale for j in range(L)]
+        m = max(s)
+        e = [math.exp(x - m) for x in s]
+        z = sum(e)
+        for i in range(d):
+            out[h, i] = sum(e[j] * float(v[kvh, j, i]) for j in range(L)) / z
+    return out
+
+
+def test_attention_fp32_brute_force_with_gqa():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(4, 8, generator=g)
+    k = torch.randn(2, 7, 8, generator=g)
+    v = torch.randn(2, 7, 8, generator=g)
+    ref = _attention_loops(q, k, v, 8 ** -0.5)
+    assert (restate.attention_fp32(q, k, v, 8 ** -0.5).double() - ref).abs().max() < 1e-5
+    # the mapping is h // 2, not h % 2: swapping the kv heads must change heads 0 and 1
+    assert (restate.attention_fp32(q, k.flip(0), v.flip(0), 8 ** -0.5)[:2].double() - ref[:2]).abs().max() > 1e-2
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 32, 40])
+def test_split_k_merge_is_invariant(splits):
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(4, 16, generator=g) * 3
+    k = torch.randn(2, 33, 16, generator=g)
+    v = torch.randn(2, 33, 16, generator=g)
+    ref = restate.attention_fp32(q, k, v, 0.25)
+    assert (restate.attention_split(q, k, v, 0.25, splits) - ref).abs().max() < 1e-5
+
+
+def test_flash_restatement_matches_torch_cpu_sdpa():
+    """``attention_flash`` restates torch's CPU flash SDPA for one bf16 query (the path Transformers'
+    sdpa attention takes for q_len 1): nearly all outputs bit-identical, the rest one bf16 ulp."""
+    g = torch.Generator().manual_seed(7)
+    for L in (33, 512, 700):
+        q = torch.randn(16, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(8, L, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(8, L, 128, generator=g).to(torch.bfloat16)
+        ref = torch.nn.functional.scaled_dot_product_attention(q[None, :, None], k[None], v[None], enable_gqa=True)[0, :, 0]
+        got = restate.attention_flash(q.float(), k.float(), v.float(), 128 ** -0.5, lanes=_lanes())
+        same = (got == ref.float()).float().mean().item()
+        assert same >= 0.99, (L, same)
+        assert (got - ref.float()).abs().max() <= 2 ** -7 * ref.float().abs().max()
+
+
+def test_fexp_u20_error_bound():
+    x = torch.linspace(-80, 0, 20001)
+    got = restate.fexp_u20(x).double()
+    ref = torch.exp(x.double())
+    rel = ((got - ref).abs() / ref).max().item()
+    assert rel < 2e-4
+    assert float(restate.fexp_u20(torch.tensor([-200.0]))) == 0.0
+
+
+def test_argmax_bf16_prefers_lowest_index_on_ties():
+    x = torch.zeros(10)
+    x[3] = 1.0
+    x[7] = 1.0 + 2 ** -12  # same bf16 value as 1.0
+    assert restate.argmax_bf16(x) == 3
+    x[7] = 1.0 + 2 ** -7    # one bf16 ulp above
+    assert restate.argmax_bf16(x) == 7
+
+
+def test_decode_step_writes_only_its_cache_slot(golden):
+    kc, vc = golden["k_cache"].clone(), golden["v_cache"].clone()
+    k0, v0 = kc.clone(), vc.clone()
+    pos = golden["P"]
+    restate.decode_step(golden["W"], kc, vc, int(golden["tokens"][0]), pos, golden["cos"], golden["sin"],
+                        numerics="fp32")
+    changed = (kc != k0).any(-1) | (vc != v0).any(-1)
+    assert changed[:, :, pos].all()
+    changed[:, :, pos] = False
+    assert not changed.any()
+
+
+# ---------------------------------------------------------------------------------------------
+# byte accounting used by the roofline
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name, expected", [("qwen3-0.6b", 1_192_101_888), ("qwen3-1.7b", 3_441_154_048)])
+def test_weight_bytes_per_token(name, expected):
+    """W = every layer weight + full tied LM head + one embedding row + final norm (bf16), counted
+    from the Transformers model's own parameters (built on the meta device)."""
+    s = SHAPES[name]
+    assert s.weight_bytes_per_token() == expected
+    from transformers import Qwen3ForCausalLM
+    with torch.device("meta"):
+        m = Qwen3ForCausalLM(hf.make_config(name))
+    layer_params = sum(p.numel() for p in m.model.layers.parameters())
+    counted = 2 * (layer_params + s.vocab * s.hidden + s.hidden + s.hidden)
+    assert counted == expected
+    assert s.kv_bytes_per_position() == 114_688
+    assert s.bytes_per_token(288) == expected + 114_688 * 289 + 512
