@@ -7,40 +7,47 @@
 //
 // Placement. One 512-thread workgroup per CU. Workgroup b runs on XCD x = b % 8 as local
 // workgroup j = b / 8 (the dispatcher's round-robin placement; every workgroup checks its
-// HW_REG_XCC_ID and reports a mismatch in the status word). XCD x owns K/V head x -- the 512
-// Q/K/V rows of that group, its attention and its 256 columns of o_proj -- plus a 1/8 slice of
-// the MLP intermediate, so within a layer only two exchanges leave the XCD.
+// HW_REG_XCC_ID). XCD x owns K/V head x -- the 512 Q/K/V rows of that group, its attention and its
+// 256 columns of o_proj -- plus a 1/8 slice of the MLP intermediate, so within a layer only two
+// exchanges (the o_proj and down_proj partial sums) leave the XCD.
 //
-// Roles. Wave 0 of every workgroup is the communication wave: it waits for other workgroups'
-// results, moves exchanged vectors, and does the vector work (RMSNorm, q/k norm + RoPE,
-// attention merges, SiLU). Waves 1-7 are math waves: they stream weights and K/V with 16-byte
-// loads issued about two phases ahead, and compute dot products from LDS inputs. Splitting the
-// roles keeps the math waves' prefetch queue from stalling the polling wave (vector-memory
-// completion is counted in order per wave).
+// Roles. Wave 0 of every workgroup is the communication wave: it publishes this workgroup's
+// results, polls for other workgroups' results and does the vector work (residual, RMSNorm, q/k
+// norm + RoPE, attention merges, SiLU). Waves 1-7 are math waves. Each math lane holds the weights
+// of every phase of the NEXT layer in registers: a phase's weights are consumed from registers and
+// the same registers are immediately reloaded with the next layer's weights, so weight traffic runs
+// a full layer ahead of the dependency chain and never waits on it. Because vector-memory
+// completions are counted in issue order per wave, the math waves never poll; the comm wave never
+// prefetches.
 //
-// Exchanges (no atomics). A producer writes data, waits for its stores, then writes a flag word
-// holding the launch epoch; a consumer polls the flags with device-scope loads.
-//   * within an XCD (QKV -> attention, attention partials, SiLU(g)*u): plain stores land in the
-//     XCD's shared L2 and device-scope loads read them there;
-//   * across XCDs (o_proj and down_proj partial sums): workgroup j of XCD y writes its row block
-//     j through to memory (device scope); workgroup j of every XCD gathers block j from the 8
-//     XCDs, sums it in XCD order and republishes it into its own XCD's L2; then every workgroup
-//     reads the full vector from its L2. Two short hops, at most 8 pollers per cross-XCD line.
+// Exchanges are "LL" words: 64-bit stores of (value bits | epoch << 32), epoch = launch sequence
+// << 6 | layer. A reader polls the words themselves until every epoch matches, so one store and
+// one load carry both data and readiness (no flag, no store-acknowledge wait). Within an XCD the
+// words live in that XCD's L2 (plain stores, device-scope loads); across XCDs they are written
+// through to memory (device-scope stores). Cross-XCD partial sums go in two hops: workgroup j of
+// each XCD gathers row block j from the 8 XCDs, sums it in XCD order and republishes it inside its
+// own XCD; then every workgroup reads the whole vector from its L2. Every buffer is written once
+// per layer and read before any writer can reach the next layer's write, and epochs differ per
+// layer and launch, so no buffer needs clearing.
 //
-// Numerics follow the reference kernel's fp32 design: bf16 weights and cache, fp32 activations
-// and accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to bf16 as stored. Logits are
-// fp32; the greedy token is the argmax of the bf16-rounded logits, lowest index on ties. The
-// residual stream is kept redundantly in every workgroup's LDS and updated from the same data
-// in the same order, so all copies are bitwise identical.
+// Numerics follow the reference kernel's fp32 design: bf16 weights and cache, fp32 activations and
+// accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to bf16 as stored. Logits are fp32;
+// the greedy token is the argmax of the bf16-rounded logits, lowest index on ties. Every
+// workgroup keeps its own copy of the residual stream in the comm wave's registers and updates it
+// from the same data in the same order, so all copies are bitwise identical.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <mutex>
+#include <type_traits>
 #include <string.h>
 
 #include "mk_device.h"
 #include "../../include/megakernel_amd.h"
 
 namespace mk {
+
+typedef unsigned long long u64;
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
 constexpr int D = 128;        // head_dim
 constexpr int HQ = 16;        // query heads
@@ -53,41 +60,38 @@ constexpr int NMW = 7;        // math waves (1..7)
 constexpr int MG = NMW * 4;   // 16-lane math groups
 constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
 constexpr int QKV_WG = QKV_X / WPX;  // 16
-constexpr int APS = 132;      // floats per head in an attention partial: acc[128], m, l, pad
-constexpr int APF = 5;        // K/V positions per math wave loaded ahead of the attention phase
+constexpr int NKV = 2;        // K/V rows per math group held in registers (one layer ahead)
+constexpr int KV_SPLIT = MG * NKV;   // positions per attention split covered by registers
+constexpr int APW = 264;      // LL words per attention partial: acc[2][128], m0, l0, m1, l1, pad
 constexpr float EPS = 1e-6f;
 constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
 constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr uint32_t ERR_TIMEOUT = 1u;
 constexpr uint32_t ERR_PLACEMENT = 2u;
+#ifndef MK_PF_DIST
+#define MK_PF_DIST 2
+#endif
+constexpr int PF_DIST = MK_PF_DIST;  // phases of weights each math lane keeps in flight (0..5)
+static_assert(PF_DIST >= 0 && PF_DIST <= 5, "prefetch distance");
 constexpr int MAX_LAYERS = 62;  // epoch = seq << 6 | layer; 63 marks the final exchange
 
-// Workspace layout: float buffers, then 256-byte flag lines.
+// Exchange workspace, in 64-bit words. Every region starts on a 256-byte boundary; a cross-XCD
+// slot (one writer) is at least 256 bytes, so no cache line has writers on two XCDs.
 constexpr int MAX_H = 2048, MAX_I = 6144, MAX_IX = MAX_I / NXCD, MAX_HPW = MAX_H / WPX;
-constexpr size_t W_QKV = 0;                                       // [8][512]
-constexpr size_t W_ATT = W_QKV + NXCD * QKV_X;                    // [8][32][2*APS]
-constexpr size_t W_M = W_ATT + (size_t)NXCD * WPX * 2 * APS;      // [8][MAX_IX]
-constexpr size_t W_LC = W_M + (size_t)NXCD * MAX_IX;              // [8][MAX_H]
-constexpr size_t W_LE = W_LC + (size_t)NXCD * MAX_H;              // [8][MAX_H]
-constexpr size_t W_GC = W_LE + (size_t)NXCD * MAX_H;              // [32][8][MAX_HPW]
-constexpr size_t W_GE = W_GC + (size_t)WPX * NXCD * MAX_HPW;      // [32][8][MAX_HPW]
-constexpr size_t WS_FLOATS = W_GE + (size_t)WPX * NXCD * MAX_HPW;
-// Flags, in u32 words after the float buffers. A local flag line (256 B) holds the 32 flags of
-// one XCD's workgroups -- all its writers share that XCD's L2. Every flag or value written across
-// XCDs gets a 128-byte slot of its own, so no cache line has writers on two XCDs.
-constexpr int LINE = 64;  // u32 per local flag line (256 B)
-constexpr int SLOT = 32;  // u32 per cross-XCD slot (128 B)
-enum LocalFlag { F_QKV = 0, F_ATT = 1, F_M = 2, F_LC = 3, F_LE = 4, N_LOCAL = 5 };
-constexpr size_t FL_LOCAL = 0;                                     // [type][x] lines
-constexpr size_t FL_CROSS = FL_LOCAL + (size_t)N_LOCAL * NXCD * LINE;  // [kind C/E][j][y] slots
-constexpr size_t FL_DONE = FL_CROSS + (size_t)2 * WPX * NXCD * SLOT;  // [wg] slots: flag, pad, key u64
-constexpr size_t FL_STATUS = FL_DONE + (size_t)NWG * SLOT;         // own line
-constexpr size_t FL_SEQ = FL_STATUS + LINE;                        // own line
-constexpr size_t FL_WORDS = FL_SEQ + LINE;
-__host__ __device__ constexpr size_t fl_local(int type, int x) { return FL_LOCAL + ((size_t)type * NXCD + x) * LINE; }
-__host__ __device__ constexpr size_t fl_cross(int kind, int j, int y) { return FL_CROSS + (((size_t)kind * WPX + j) * NXCD + y) * SLOT; }
-__host__ __device__ constexpr size_t fl_done(int wg) { return FL_DONE + (size_t)wg * SLOT; }
-constexpr size_t WS_BYTES = WS_FLOATS * 4 + FL_WORDS * 4;
+constexpr size_t X_QKV = 0;                                     // [8][512]
+constexpr size_t X_ATT = X_QKV + NXCD * QKV_X;                  // [8][32][APW]
+constexpr size_t X_M = X_ATT + (size_t)NXCD * WPX * APW;        // [8][MAX_IX]
+constexpr size_t X_OL = X_M + (size_t)NXCD * MAX_IX;            // [8][MAX_H]
+constexpr size_t X_EL = X_OL + (size_t)NXCD * MAX_H;            // [8][MAX_H]
+constexpr size_t X_OX = X_EL + (size_t)NXCD * MAX_H;            // [32][8][MAX_HPW]
+constexpr size_t X_EX = X_OX + (size_t)WPX * NXCD * MAX_HPW;    // [32][8][MAX_HPW]
+constexpr size_t X_DONE = X_EX + (size_t)WPX * NXCD * MAX_HPW;  // [256][16]: key word, flag word
+constexpr size_t X_STATUS = X_DONE + (size_t)NWG * 16;          // u32 status in its own line
+constexpr size_t X_SEQ = X_STATUS + 32;                         // u32 launch sequence in its own line
+constexpr size_t X_WORDS = X_SEQ + 32;
+constexpr size_t WS_BYTES = X_WORDS * 8;
+static_assert(X_ATT % 32 == 0 && X_M % 32 == 0 && X_OL % 32 == 0 && X_OX % 32 == 0 && X_DONE % 32 == 0,
+              "exchange regions must be 256-byte aligned");
 
 struct KArgs {
   const uint16_t* embed;
@@ -100,637 +104,911 @@ struct KArgs {
   uint16_t* v_cache;
   float* logits;
   int32_t* out_token;
-  float* ws;
-  uint32_t* fl;     // flag lines
+  u64* xw;          // exchange workspace
   uint64_t* trace;  // optional: per-workgroup phase timestamps (TRACE_N per workgroup)
   int token, position, max_seq, num_layers, vocab;
 };
 
-// Phase timestamps (s_memrealtime, 100 MHz), TRACE_PER_LAYER slots per layer: for phase p in A..E,
-// [2p] when the phase's math starts and [2p + 1] when its outputs are published; [10 + k] when the
-// communication wave finishes its k-th wait of the layer (QKV, attention partials, cross o_proj,
-// local o_proj, MLP, cross down, local down). TRACE_TAIL slots after the layers: kernel start,
-// last exchange done, LM-head start and end.
+// Phase timestamps (s_memrealtime, 100 MHz), TRACE_PER_LAYER slots per layer, see TraceSlot.
+// TRACE_TAIL slots after the layers: kernel start, LM-head start, LM-head end, exit.
+enum TraceSlot {
+  T_A_START = 0, T_A_PUB, T_A_POLL, T_B_START, T_B_PUB, T_B_POLL, T_C_START, T_C_PUB, T_C_XPOLL, T_C_LPOLL,
+  T_D_START, T_D_PUB, T_D_POLL, T_E_START, T_E_PUB, T_E_XPOLL, T_E_LPOLL,
+  T_M_A_END, T_M_B_START, T_M_B_END,  // stamped by math wave 1
+  T_B_MAX, T_B_SUM, T_M_A_DOT, T_M_D_ISSUED, T_M_D_DOT, T_SLOTS
+};
 constexpr int TRACE_LAYERS = 64;
-constexpr int TRACE_PER_LAYER = 20;
+constexpr int TRACE_PER_LAYER = 32;
 constexpr int TRACE_TAIL = 8;
 constexpr int TRACE_N = TRACE_LAYERS * TRACE_PER_LAYER + TRACE_TAIL;
-__device__ __forceinline__ void mark(const KArgs& a, int idx) {
-  if (a.trace != nullptr && threadIdx.x == 0 && idx >= 0 && idx < TRACE_N)
+static_assert(T_SLOTS <= TRACE_PER_LAYER, "trace slots");
+__device__ __forceinline__ void mark(const KArgs& a, int idx, int by_thread = 0) {
+  if (a.trace != nullptr && threadIdx.x == by_thread && idx >= 0 && idx < TRACE_N)
     a.trace[(size_t)blockIdx.x * TRACE_N + idx] = wall_clock64();
 }
 
 // ------------------------------------------------------------------------------------------
-// Communication-wave helpers (called by wave 0 only; every lane participates)
+// LL exchange words (comm wave)
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
+  v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x); v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
+  v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ u64 ll_word(float v, uint32_t ep) { return ((u64)ep << 32) | __float_as_uint(v); }
+
 struct Comm {
   uint32_t* status;
   bool failed = false;
+  bool wt = false;  // write local exchanges through to memory (fallback when placement is unknown)
 };
 
-// Plain store: stays in this XCD's L2 until written back; visible to device-scope loads from the
-// same XCD.
-__device__ __forceinline__ void st_local_f32(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+// One LL word. Cross-XCD words are written through (device scope); local words stay in L2.
+__device__ __forceinline__ void ll_st(const Comm& c, u64* p, u64 w, bool cross) {
+  if (cross || c.wt) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void st_local_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-// All earlier stores of this wave are complete before anything after this point is issued.
-__device__ __forceinline__ void store_fence() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  wait_vmem();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+// Two consecutive LL words at word offset `off` (even) from a wave-uniform base, in one 16-byte
+// store; each 8-byte half is single-copy atomic.
+__device__ __forceinline__ void ll_st2(const Comm& c, u64* base, int off, float v0, float v1, uint32_t ep, bool cross) {
+  const u4v w = {__float_as_uint(v0), ep, __float_as_uint(v1), ep};
+  if (cross || c.wt) __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), off * 8, 0, CPOL_SC1);
+  else __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), off * 8, 0, 0);
 }
 
-// Wait until flags[0], flags[stride], ... flags[(n-1)*stride] all equal ep (n <= 64). Bounded;
-// on timeout sets the status word.
-__device__ __forceinline__ void poll_flags(Comm& c, const uint32_t* flags, int n, uint32_t ep, int stride = 1) {
+// Polls NL 16-byte pairs of LL words at word offsets off[k] from base (device-scope loads) until
+// every epoch equals ep; returns the 2*NL values. Two rounds of loads are kept in flight, so a
+// value that lands while one round is out is seen by the next one instead of a full round trip
+// later. Lanes with active == false are always ready. Bounded: on timeout sets the status word
+// and returns zeros.
+template <int NL>
+__device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&off)[NL], bool active, uint32_t ep,
+                                        float (&v)[2 * NL]) {
+#pragma unroll
+  for (int k = 0; k < 2 * NL; ++k) v[k] = 0.f;
   if (c.failed) return;
-  const int lane = threadIdx.x & 63;
-  for (uint32_t it = 0;; ++it) {
-    const uint32_t v = lane < n ? ld_dev_u32(flags + lane * stride) : ep;
-    if (__ballot(v != ep) == 0) return;
-    if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) { c.failed = true; return; }
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
+  auto issue = [&](u4v (&r)[NL]) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k)
+      r[k] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, active ? off[k] * 8 : 0, 0, CPOL_SC1));
+  };
+  auto ready = [&](const u4v (&r)[NL]) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < NL; ++k) ok &= (r[k][1] == ep) & (r[k][3] == ep);
+    return __ballot(!(ok | !active)) == 0;
+  };
+  auto take = [&](const u4v (&r)[NL]) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) { v[2 * k] = __uint_as_float(r[k][0]); v[2 * k + 1] = __uint_as_float(r[k][2]); }
+  };
+  u4v r0[NL], r1[NL];
+  issue(r0);
+  for (uint32_t it = 0;; it += 2) {
+    issue(r1);
+    if (ready(r0)) { take(r0); return; }
+    issue(r0);
+    if (ready(r1)) { take(r1); return; }
+    if ((it & 62u) == 62u && ld_dev_u32(c.status) != 0) { c.failed = true; return; }
     if (it > SPIN_LIMIT) {
-      if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT);
+      if ((threadIdx.x & 63) == 0) st_dev_u32(c.status, ERR_TIMEOUT);
       c.failed = true;
       return;
     }
   }
 }
 
-// s_res[i] += delta[i] (device-scope reads; delta may be null), then s_x = RMSNorm(s_res) * w in
-// fp32, the reference's form x * w * rsqrt(mean(x^2) + eps) (/root/reference/megakernel.cu:704-739).
-// Lane l owns the H/64 contiguous elements starting at l*H/64.
+// Activations enter the GEMVs as two bf16 vectors, hi = bf16(x) and lo = bf16(x - hi), so that
+// w . x = w . hi + w . lo is computed with bf16 dot instructions (v_dot2_f32_bf16: products exact
+// in fp32, fp32 accumulation) to within ~2^-17 relative of the fp32 product, the precision of the
+// reference kernel's fp32 activations (/root/reference/megakernel.cu:53-90, :100-142, :191-225).
+// xh/xl hold the pairs as uint32 (element 2i in the low half), 16-byte chunks of 8 elements.
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16x2(a, b);
+  lo = pack_bf16x2(a - bf16_lo(hi), b - bf16_hi(hi));
+}
+// Writes n (even) consecutive values starting at element e0 (even) into xh/xl.
+template <int N>
+__device__ __forceinline__ void store_hilo(uint4* xh, uint4* xl, int e0, const float* v) {
+  uint32_t* h = reinterpret_cast<uint32_t*>(xh) + e0 / 2;
+  uint32_t* l = reinterpret_cast<uint32_t*>(xl) + e0 / 2;
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int k = 0; k < N; k += 8) {
+      uint32_t hh[4], ll[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) split_pair(v[k + 2 * q], v[k + 2 * q + 1], hh[q], ll[q]);
+      *reinterpret_cast<uint4*>(h + k / 2) = make_uint4(hh[0], hh[1], hh[2], hh[3]);
+      *reinterpret_cast<uint4*>(l + k / 2) = make_uint4(ll[0], ll[1], ll[2], ll[3]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; k += 2) split_pair(v[k], v[k + 1], h[k / 2], l[k / 2]);
+  }
+}
+
+// x = res * w * rsqrt(mean(res^2) + eps) over the lane's E elements [E*lane, E*lane + E), the
+// reference's fp32 RMSNorm (/root/reference/megakernel.cu:704-739, :148-182); w is bf16 in LDS.
 template <int H>
-__device__ __forceinline__ void comm_residual_norm(float* s_res, const float* delta, const uint16_t* w, float* s_x) {
+__device__ __forceinline__ void comm_norm(const float (&res)[H / 64], const uint16_t* w, uint4* xh, uint4* xl) {
   constexpr int E = H / 64;
   const int lane = threadIdx.x & 63;
-  float v[E];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < E; k += 4) {
-    float4 r = *reinterpret_cast<const float4*>(s_res + lane * E + k);
-    if (delta != nullptr) {
-      const float4 d = ld_dev_f32x4(delta, (lane * E + k) * 4);
-      r.x += d.x; r.y += d.y; r.z += d.z; r.w += d.w;
-      *reinterpret_cast<float4*>(s_res + lane * E + k) = r;
-    }
-    v[k] = r.x; v[k + 1] = r.y; v[k + 2] = r.z; v[k + 3] = r.w;
-  }
-#pragma unroll
-  for (int k = 0; k < E; ++k) ss += v[k] * v[k];
+  for (int k = 0; k < E; ++k) ss = fmaf(res[k], res[k], ss);
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / (float)H + EPS);
-  const uint4* wp = reinterpret_cast<const uint4*>(w + lane * E);
+  float y[E];
 #pragma unroll
   for (int k = 0; k < E; k += 8) {
-    const uint4 ww = ld_global16(wp + k / 8);
-    const float wv[8] = {bf16_lo(ww.x), bf16_hi(ww.x), bf16_lo(ww.y), bf16_hi(ww.y),
-                         bf16_lo(ww.z), bf16_hi(ww.z), bf16_lo(ww.w), bf16_hi(ww.w)};
+    float wv[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + lane * E + k), wv);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) s_x[lane * E + k + q] = v[k + q] * wv[q] * rs;
+    for (int q = 0; q < 8; ++q) y[k + q] = res[k + q] * wv[q] * rs;
   }
+  store_hilo<E>(xh, xl, E * lane, y);
+}
+
+// Cross-XCD partial sum of one row block, then republish inside the XCD, then read the whole
+// vector and add it to the residual. xs: this workgroup's HPW row partials (lanes < HPW hold one
+// each). Block j is rows [HPW*j, HPW*j + HPW).
+template <int H>
+__device__ __forceinline__ void comm_cross_reduce(Comm& c, u64* xw, size_t xbase, size_t lbase, int xcd, int j,
+                                                  float mine, uint32_t ep, float (&res)[H / 64], const KArgs& a,
+                                                  int tslot_x, int tslot_l) {
+  constexpr int HPW = H / WPX, RPL = HPW / 8, E = H / 64;
+  const int lane = threadIdx.x & 63;
+  // hop 1: my partial of block j -> slot (j, xcd); written through
+  if (lane < HPW) ll_st(c, xw + xbase + ((size_t)j * NXCD + xcd) * MAX_HPW + lane, ll_word(mine, ep), true);
+  // gather block j from the 8 XCDs: lane -> XCD y = lane / 8, rows RPL*(lane % 8) ..
+  const int y = lane >> 3, r0 = RPL * (lane & 7);
+  int off[RPL / 2];
+#pragma unroll
+  for (int k = 0; k < RPL / 2; ++k) off[k] = (int)(((size_t)j * NXCD + y) * MAX_HPW + r0 + 2 * k);
+  float v[RPL];
+  ll_poll<RPL / 2>(c, xw + xbase, off, true, ep, v);
+  mark(a, tslot_x);
+  // sum over y in a fixed tree (lanes l, l^8, l^16, l^32 hold the same rows for different y)
+#pragma unroll
+  for (int k = 0; k < RPL; ++k) {
+    v[k] += dpp<0x128>(v[k]);  // row_ror:8 == lane ^ 8 inside a 16-lane row
+    v[k] = xsum32(xsum16(v[k]));
+  }
+  // hop 2: republish block j inside this XCD
+  if (lane < 8) {
+#pragma unroll
+    for (int k = 0; k < RPL; k += 2) ll_st2(c, xw + lbase, xcd * MAX_H + HPW * j + r0 + k, v[k], v[k + 1], ep, false);
+  }
+  int offl[E / 2];
+#pragma unroll
+  for (int k = 0; k < E / 2; ++k) offl[k] = (int)((size_t)xcd * MAX_H + E * lane + 2 * k);
+  float d[E];
+  ll_poll<E / 2>(c, xw + lbase, offl, true, ep, d);
+  mark(a, tslot_l);
+#pragma unroll
+  for (int k = 0; k < E; ++k) res[k] += d[k];
 }
 
 // ------------------------------------------------------------------------------------------
-// Math-wave helpers. A phase's weight tile is cut into units of 16 chunks (256 contiguous
-// bytes of one row); math group g (16 lanes) owns units g, g+28, g+56, ...; lane t of the group
-// loads chunk t of each unit. Unit u covers row u / UPR, column block u % UPR (128 elements).
+// Math-wave GEMV tiles. A phase's weight tile is ROWS rows of C bf16 columns. SPAN lanes share a
+// row: lane l holds CPL 16-byte chunks of it, chunk k at column chunk k*SPAN + l % SPAN (so every
+// load instruction of a wave reads contiguous bytes), and a wave covers RW = 64 / SPAN rows per
+// step. Math wave mw takes rows (s*7 + mw)*RW + l/SPAN at steps s = 0, 1, ...; the first PS steps
+// come from registers loaded phases ahead, the rest (large shapes) stream in the phase. A lane's
+// activation slice is the same for every row, so it is read from LDS once per phase.
 // ------------------------------------------------------------------------------------------
-// Loads are unconditional (a lane past the tile re-reads the tile's last unit): a conditional
-// load becomes a branch whose join forces the wave to wait for every outstanding load, which
-// would serialize the phase and drain the prefetch of later phases.
-template <int NU, int UPR, typename Ptr>
-__device__ __forceinline__ void load_units(uint4 (&w)[NU], int k0, int U, int g, int t, Ptr ptr) {
+struct NoOp {
+  __device__ void operator()() const {}
+};
+
+template <int ROWS_, int C_, int SPAN_, int PFS>
+struct Tile {
+  static constexpr int ROWS = ROWS_, C = C_, SPAN = SPAN_;
+  static constexpr int CPL = C / (8 * SPAN);
+  static constexpr int RW = 64 / SPAN;
+  static constexpr int STEPS = (ROWS + RW * NMW - 1) / (RW * NMW);
+  static constexpr int PS = STEPS < PFS ? STEPS : PFS;
+  static_assert(C % (8 * SPAN) == 0 && 64 % SPAN == 0 && CPL >= 1, "tile shape");
+};
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x), acc, false);
+}
+template <int CPL>
+__device__ __forceinline__ float dot_chunks(const uint4 (&w)[CPL], const uint4 (&xh)[CPL], const uint4 (&xl)[CPL]) {
+  float a = 0.f, b = 0.f;
 #pragma unroll
-  for (int k = 0; k < NU; ++k) {
-    int u = g + MG * (k0 + k);
-    u = u < U ? u : U - 1;
-    w[k] = ld_stream(ptr(u / UPR, u % UPR) + t);
+  for (int k = 0; k < CPL; ++k) {
+    a = dot2(w[k].x, xh[k].x, a); b = dot2(w[k].x, xl[k].x, b);
+    a = dot2(w[k].y, xh[k].y, a); b = dot2(w[k].y, xl[k].y, b);
+    a = dot2(w[k].z, xh[k].z, a); b = dot2(w[k].z, xl[k].z, b);
+    a = dot2(w[k].w, xh[k].w, a); b = dot2(w[k].w, xl[k].w, b);
+  }
+  return a + b;
+}
+// Sum over the SPAN lanes of a row; every lane of the row receives it.
+template <int SPAN>
+__device__ __forceinline__ float span_sum(float v) {
+  if constexpr (SPAN == 64) return wave_sum(v);
+  else if constexpr (SPAN == 32) return xsum16(row16_sum(v));
+  else { static_assert(SPAN == 16, "span"); return row16_sum(v); }
+}
+
+template <class T>
+__device__ __forceinline__ int tile_row(int s, int mw, int lane) {
+  return (s * NMW + mw) * T::RW + lane / T::SPAN;
+}
+// Loads steps [s0, s0 + NS) of this lane into w (rows past the tile re-read its last row: loads are
+// unconditional, see load order note in math_role).
+template <class T, int NS, typename RowPtr>
+__device__ __forceinline__ void tile_load(uint4 (&w)[NS][T::CPL], int s0, int mw, int lane, RowPtr rp) {
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    int r = tile_row<T>(s0 + s, mw, lane);
+    r = r < T::ROWS ? r : T::ROWS - 1;
+    const uint4* p = rp(r) + lane % T::SPAN;
+#pragma unroll
+    for (int k = 0; k < T::CPL; ++k) w[s][k] = ld_stream(p + k * T::SPAN);
+  }
+}
+template <class T>
+__device__ __forceinline__ void tile_dot_step(const uint4 (&w)[T::CPL], const uint4 (&xh)[T::CPL], const uint4 (&xl)[T::CPL],
+                                              int s, int mw, int lane, float* s_up) {
+  const float v = span_sum<T::SPAN>(dot_chunks<T::CPL>(w, xh, xl));
+  const int r = tile_row<T>(s, mw, lane);
+  if (lane % T::SPAN == 0 && r < T::ROWS) s_up[r] = v;
+}
+// One phase: row sums of the tile into s_up[row]. pf holds the first PS steps; `after` runs once
+// they are consumed (before any streamed step).
+template <class T, typename RowPtr, typename After>
+__device__ __forceinline__ void tile_consume(const uint4 (&pf)[T::PS][T::CPL], int mw, int lane, const uint4* xh_lds,
+                                             const uint4* xl_lds, float* s_up, RowPtr rp, After after) {
+  uint4 xh[T::CPL], xl[T::CPL];
+#pragma unroll
+  for (int k = 0; k < T::CPL; ++k) {
+    xh[k] = xh_lds[k * T::SPAN + lane % T::SPAN];
+    xl[k] = xl_lds[k * T::SPAN + lane % T::SPAN];
+  }
+#pragma unroll
+  for (int s = 0; s < T::PS; ++s) tile_dot_step<T>(pf[s], xh, xl, s, mw, lane, s_up);
+  after();
+#pragma unroll
+  for (int s = T::PS; s < T::STEPS; ++s) {
+    uint4 w[1][T::CPL];
+    tile_load<T, 1>(w, s, mw, lane, rp);
+    tile_dot_step<T>(w[0], xh, xl, s, mw, lane, s_up);
   }
 }
 
-template <int NU, int UPR>
-__device__ __forceinline__ void dot_units(const uint4 (&w)[NU], int k0, int U, int g, int t, const float* x, float* s_up) {
-#pragma unroll
-  for (int k = 0; k < NU; ++k) {
-    const int u = g + MG * (k0 + k);
-    const int uc = u < U ? u : U - 1;
-    float acc = dot8(w[k], x + (uc % UPR) * 128 + t * 8, 0.f);
-    acc = row16_sum(acc);
-    if (t == 0 && u < U) s_up[u] = acc;
-  }
-}
-
-// A GEMV phase whose first PFN units per lane were loaded ahead (pf); the rest stream here.
-template <int NU, int PFN, int UPR, typename Ptr>
-__device__ __forceinline__ void gemv_phase(const uint4 (&pf)[PFN], int U, int g, int t, Ptr ptr, const float* x, float* s_up) {
-  dot_units<PFN, UPR>(pf, 0, U, g, t, x, s_up);
-#pragma unroll
-  for (int k0 = PFN; k0 < NU; k0 += PFN) {
-    uint4 w[PFN];
-    load_units<PFN, UPR>(w, k0, U, g, t, ptr);
-    dot_units<PFN, UPR>(w, k0, U, g, t, x, s_up);
-  }
-}
-
-__device__ __forceinline__ unsigned long long argmax_key(float logit, int idx) {
+__device__ __forceinline__ u64 argmax_key(float logit, int idx) {
   // order-preserving map of the bf16-rounded logit, then the complemented index so that equal
   // values prefer the lower index under an unsigned max
   uint32_t u = (uint32_t)f32_to_bf16(logit) << 16;
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)u << 32) | (0xffffffffu - (uint32_t)idx);
+  return ((u64)u << 32) | (0xffffffffu - (uint32_t)idx);
 }
 
-__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+__device__ __forceinline__ u64 umax64(u64 a, u64 b) { return a > b ? a : b; }
 
 // Returns v unchanged but hides its origin from the optimizer, so per-unit indices derived from it
-// are recomputed inside each phase instead of being hoisted out of the layer loop and held in
-// registers for the whole kernel.
+// are recomputed inside each phase instead of being held in registers for the whole kernel.
 __device__ __forceinline__ int opaque(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
 
+// Online-softmax update of one key for one head: (m, l, acc[8]) <- key with score s and values v.
+// __expf is the hardware exp2 of x*log2(e) (relative error ~1e-7); exp(-inf) = 0.
+__device__ __forceinline__ void softmax_step(float s, const float (&v)[8], float& m, float& l, float (&acc)[8]) {
+  const float n = fmaxf(m, s);
+  const float cm = __expf(m - n), e = __expf(s - n);
+  l = l * cm + e;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = acc[i] * cm + e * v[i];
+  m = n;
+}
+
+
 // ------------------------------------------------------------------------------------------
-// The kernel
+// The kernel. The comm wave and the math waves run separate loops (so their register live
+// ranges never overlap) that meet at the same sequence of workgroup barriers: per layer and
+// phase, math work -> barrier -> comm work -> barrier.
 // ------------------------------------------------------------------------------------------
 template <int H, int I>
-__global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
-  constexpr int IX = I / NXCD;     // MLP intermediate slice per XCD
-  constexpr int IPW = IX / WPX;    // gate (and up) rows per workgroup
-  constexpr int HPW = H / WPX;     // o_proj / down_proj rows per workgroup
-  constexpr int UPR_H = H / 128, UPR_C = 2 * D / 128, UPR_E = IX / 128;
-  constexpr int U_A = QKV_WG * UPR_H, U_C = HPW * UPR_C, U_D = 2 * IPW * UPR_H, U_E = HPW * UPR_E;
-  constexpr int NU_A = (U_A + MG - 1) / MG, NU_C = (U_C + MG - 1) / MG;
-  constexpr int NU_D = (U_D + MG - 1) / MG, NU_E = (U_E + MG - 1) / MG;
-  constexpr int PF = H <= 1024 ? 8 : 4;  // max 16-byte chunks per lane loaded ahead of a GEMV phase
-  constexpr int PA = NU_A < PF ? NU_A : PF, PC = NU_C < PF ? NU_C : PF;
-  constexpr int PD = NU_D < PF ? NU_D : PF, PE = NU_E < PF ? NU_E : PF;
-  constexpr int XN = (H > IX ? H : IX);
-  constexpr int UMAX = (U_D > U_A ? U_D : U_A) > U_E ? (U_D > U_A ? U_D : U_A) : U_E;
+struct Geo {
+  static constexpr int E = H / 64;        // residual elements per comm lane
+  static constexpr int IX = I / NXCD;     // MLP intermediate slice per XCD
+  static constexpr int IPW = IX / WPX;    // gate (and up) rows per workgroup
+  static constexpr int HPW = H / WPX;     // o_proj / down_proj rows per workgroup
+  static constexpr bool SMALL = H <= 1024;
+  // phase tiles: A = QKV rows, C = o_proj partial, D = gate/up rows, E = down_proj partial; the
+  // last argument caps the steps held in registers ahead (the larger shape streams the rest)
+  typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 2> TA;
+  typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 2> TC;
+  typedef Tile<2 * IPW, H, 64, SMALL ? 8 : 2> TD;
+  typedef Tile<HPW, IX, 16, SMALL ? 8 : 1> TE;
+  static constexpr int XN = (H > IX ? H : IX);
+  static constexpr int UMAX = 2 * IPW > HPW ? 2 * IPW : HPW;
+  static constexpr int NSLOT = 2 * H + 2 * D;   // bf16 norm weights per layer: input, post-attention, q, k
+  static constexpr int NSL16 = NSLOT / 8;       // ... in 16-byte chunks
+  static constexpr int NSL_L = (NSL16 + 63) / 64;
+  static constexpr int IXL = IX / 64;           // MLP words per comm lane
   static_assert(HPW * WPX == H && IPW * WPX == IX && IX * NXCD == I, "shape must split evenly");
-  static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64, "unsupported shape");
+  static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64 && IXL % 2 == 0, "unsupported shape");
+  static_assert(QKV_WG <= UMAX, "s_up too small");
+};
 
-  __shared__ __attribute__((aligned(16))) float s_res[H];
-  __shared__ __attribute__((aligned(16))) float s_x[XN];
-  __shared__ __attribute__((aligned(16))) float s_up[UMAX];
-  __shared__ __attribute__((aligned(16))) float s_q[2][D];
-  __shared__ __attribute__((aligned(16))) float s_k[D];
-  __shared__ __attribute__((aligned(16))) float s_v[D];
-  __shared__ __attribute__((aligned(16))) float s_wp[NMW][2][D + 2];
-  __shared__ unsigned long long s_best[NMW];
+template <int H, int I>
+struct Smem {
+  uint4 xh[Geo<H, I>::XN / 8];       // GEMV input of the current phase, bf16 hi part
+  uint4 xl[Geo<H, I>::XN / 8];       // ... and lo part
+  float up[Geo<H, I>::UMAX];         // row sums of the current phase
+  float q[2][D];                     // normed, rotated queries
+  uint16_t kvn[2][D];                // new K (normed, rotated) and V, bf16
+  float cs[2][D];                    // cos, sin at position
+  uint16_t nw[2][Geo<H, I>::NSLOT];  // per-layer norm weights by layer parity
+  float gp[NMW][2][D + 4];           // attention partials of the 7 math waves: acc[128], m, l
+  u64 best[NMW];
+  mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
+};
 
-  const int xcd = blockIdx.x % NXCD;
-  const int j = blockIdx.x / NXCD;
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
+// outstanding global loads (a full __syncthreads fence would also wait for the weight loads that
+// run phases ahead). Exchanges through global memory never rely on it.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left alone
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Per-launch constants every role needs.
+struct Step {
+  int xcd, j, position, ctx, L, S, p0, p1;
+  bool att_wg;
+};
+
+__device__ __forceinline__ Step make_step(const KArgs& a) {
+  Step s;
+  s.xcd = blockIdx.x % NXCD;
+  s.j = blockIdx.x / NXCD;
+  s.position = a.position;
+  s.ctx = a.position + 1;
+  s.L = a.num_layers;
+  // Split-K attention: the context is cut into S splits handled by local workgroups 0..S-1.
+  // Up to KV_SPLIT positions per split come from registers loaded a layer ahead.
+  int S = (s.ctx + KV_SPLIT - 1) / KV_SPLIT;
+  s.S = S < WPX ? S : WPX;
+  s.att_wg = s.j < s.S;
+  s.p0 = s.att_wg ? (int)(((long long)s.ctx * s.j) / s.S) : 0;
+  s.p1 = s.att_wg ? (int)(((long long)s.ctx * (s.j + 1)) / s.S) : 0;
+  return s;
+}
+
+// ---- math waves ------------------------------------------------------------------------------
+template <int H, int I, int DIST>
+__device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const Step& st) {
+  typedef Geo<H, I> G;
+  typedef typename G::TA TA;
+  typedef typename G::TC TC;
+  typedef typename G::TD TD;
+  typedef typename G::TE TE;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const bool comm = wave == 0;
-  const int g = comm ? 0 : (wave - 1) * 4 + (lane >> 4);  // math group
-  const int t = lane & 15;
-
-  float* ws = a.ws;
-  uint32_t* fl = a.fl;
-  Comm c;
-  c.status = fl + FL_STATUS;
-  const int position = a.position;
-  const int ctx = position + 1;
-  const int L = a.num_layers;
-
-  // Split-K attention: the context is cut into S = min(32, ceil(ctx / 32)) splits handled by local
-  // workgroups 0..S-1; math wave w of a split takes positions p0 + w, p0 + w + 7, ...
-  const int S = ctx >= WPX * 32 ? WPX : (ctx + 31) / 32;
-  const int p0 = j < S ? (int)(((long long)ctx * j) / S) : 0;
-  const int p1 = j < S ? (int)(((long long)ctx * (j + 1)) / S) : 0;
   const int mw = wave - 1;
-  const int np_w = (!comm && p1 - p0 > mw) ? (p1 - p0 - mw + NMW - 1) / NMW : 0;
+  const int g = mw * 4 + (lane >> 4);  // 16-lane group (attention: one key row per group)
+  const int t = lane & 15;
+  const int xcd = st.xcd, j = st.j, L = st.L;
 
-  // ---- per-phase weight tiles (unit (r, b) starts at chunk 16*b of tile row r) -------------
-  auto ptr_A = [&](const mk_layer_weights& lw) {
+  // tile row r -> first 16-byte chunk of that row's columns
+  auto rows_A = [&](const mk_layer_weights& lw) {
     const uint16_t* base;
     int row0;
     if (j < 16) { base = (const uint16_t*)lw.q_weight; row0 = 2 * D * xcd + QKV_WG * j; }
     else if (j < 24) { base = (const uint16_t*)lw.k_weight; row0 = D * xcd + QKV_WG * (j - 16); }
     else { base = (const uint16_t*)lw.v_weight; row0 = D * xcd + QKV_WG * (j - 24); }
-    return [=](int r, int b) { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * H) + 16 * b; };
+    return [=](int r) { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * H); };
   };
-  auto ptr_C = [&](const mk_layer_weights& lw) {
+  auto rows_C = [&](const mk_layer_weights& lw) {
     const uint16_t* wo = (const uint16_t*)lw.o_proj_weight;
-    const int row0 = HPW * j;
-    return [=](int r, int b) {
-      return reinterpret_cast<const uint4*>(wo + (size_t)(row0 + r) * (HQ * D) + 2 * D * xcd) + 16 * b;
-    };
+    const int row0 = G::HPW * j;
+    return [=](int r) { return reinterpret_cast<const uint4*>(wo + (size_t)(row0 + r) * (HQ * D) + 2 * D * xcd); };
   };
-  auto ptr_D = [&](const mk_layer_weights& lw) {
+  auto rows_D = [&](const mk_layer_weights& lw) {
     const uint16_t* wg = (const uint16_t*)lw.gate_proj_weight;
     const uint16_t* wu = (const uint16_t*)lw.up_proj_weight;
-    const int row0 = IX * xcd + IPW * j;
-    return [=](int r, int b) {
-      const uint16_t* row = r < IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - IPW) * H;
-      return reinterpret_cast<const uint4*>(row) + 16 * b;
+    const int row0 = G::IX * xcd + G::IPW * j;
+    return [=](int r) {
+      return reinterpret_cast<const uint4*>(r < G::IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - G::IPW) * H);
     };
   };
-  auto ptr_E = [&](const mk_layer_weights& lw) {
+  auto rows_E = [&](const mk_layer_weights& lw) {
     const uint16_t* wd = (const uint16_t*)lw.down_proj_weight;
-    const int row0 = HPW * j;
-    return [=](int r, int b) { return reinterpret_cast<const uint4*>(wd + (size_t)(row0 + r) * I + IX * xcd) + 16 * b; };
+    const int row0 = G::HPW * j;
+    return [=](int r) { return reinterpret_cast<const uint4*>(wd + (size_t)(row0 + r) * I + G::IX * xcd); };
+  };
+  // K/V row of position p (16 chunks; lane t reads chunk t)
+  auto kv_row = [&](const uint16_t* cache, int layer, int p) {
+    return reinterpret_cast<const uint4*>(cache + (((size_t)layer * HKV + xcd) * a.max_seq + p) * D) + t;
+  };
+  // K/V rows this math group attends to from registers: p0 + g + MG*r; unused slots re-read p0
+  auto kv_pos = [&](int r) {
+    const int p = st.p0 + g + MG * r;
+    return (p < st.p1 && p != st.position) ? p : st.p0;
+  };
+  // norm-weight slot: chunk q of [input norm | post norm | q norm | k norm] for layer `layer`,
+  // or of the final norm (every piece) when layer == L
+  auto slot_chunk = [&](int layer, int q) {
+    q = q < G::NSL16 ? q : G::NSL16 - 1;
+    if (layer >= L) return reinterpret_cast<const uint4*>(a.final_norm) + (q % (H / 8));
+    const mk_layer_weights& lw = sm.layers[layer];
+    if (q < H / 8) return reinterpret_cast<const uint4*>(lw.norm_weight) + q;
+    if (q < H / 4) return reinterpret_cast<const uint4*>(lw.post_attn_norm_weight) + (q - H / 8);
+    if (q < H / 4 + D / 8) return reinterpret_cast<const uint4*>(lw.q_norm_weight) + (q - H / 4);
+    return reinterpret_cast<const uint4*>(lw.k_norm_weight) + (q - H / 4 - D / 8);
   };
 
-  // K/V of the first APF positions of this math wave, loaded ahead of the attention phase
-  uint32_t kv_k[APF], kv_v[APF];
-  auto load_kv = [&](int layer) {
-    const size_t hb = ((size_t)layer * HKV + xcd) * a.max_seq * D;
-    const uint32_t* kc = reinterpret_cast<const uint32_t*>(a.k_cache + hb);
-    const uint32_t* vc = reinterpret_cast<const uint32_t*>(a.v_cache + hb);
-#pragma unroll
-    for (int i = 0; i < APF; ++i) {
-      // unconditional (see load_units); positions outside [p0, p1) or the new one are not used
-      int p = p0 + mw + NMW * i;
-      p = (i < np_w && p != position) ? p : 0;
-      kv_k[i] = gp(kc)[(size_t)p * (D / 2) + lane];
-      kv_v[i] = gp(vc)[(size_t)p * (D / 2) + lane];
-    }
-  };
+  uint4 wA[TA::PS][TA::CPL], wC[TC::PS][TC::CPL], wD[TD::PS][TD::CPL], wE[TE::PS][TE::CPL];
+  uint4 kK[NKV], kV[NKV];
+  uint4 nsl[G::NSL_L];
 
-  uint4 wA[PA], wC[PC], wD[PD], wE[PE];
-  uint32_t seq = 0;
-  float cs_c0 = 0.f, cs_c1 = 0.f, cs_s0 = 0.f, cs_s1 = 0.f;  // comm: cos/sin at dims lane, lane+64
-
-  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 0);
-  if (comm) {
-    seq = ld_dev_u32(fl + FL_SEQ);
-    if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, ERR_PLACEMENT);
-    const uint16_t* row = a.embed + (size_t)a.token * H;
-    for (int i = lane; i < H; i += 64) s_res[i] = bf16_to_f32(gp(row)[i]);
-    const uint16_t* cr = a.cos_tab + (size_t)position * D;
-    const uint16_t* sr = a.sin_tab + (size_t)position * D;
-    cs_c0 = bf16_to_f32(gp(cr)[lane]); cs_c1 = bf16_to_f32(gp(cr)[lane + 64]);
-    cs_s0 = bf16_to_f32(gp(sr)[lane]); cs_s1 = bf16_to_f32(gp(sr)[lane + 64]);
-    comm_residual_norm<H>(s_res, nullptr, (const uint16_t*)a.layers[0].norm_weight, s_x);
-  } else {
-    const mk_layer_weights lw0 = a.layers[0];
-    load_units<PA, UPR_H>(wA, 0, U_A, g, t, ptr_A(lw0));
+  // prologue: the layer table into LDS, then layer 0's norm weights (synchronously, wave 1)
+  {
+    constexpr int TW = (int)(sizeof(mk_layer_weights) / 8);
+    const int n = L * TW;
+    for (int i = threadIdx.x - 64; i < n; i += NT - 64)
+      reinterpret_cast<u64*>(sm.layers)[i] = reinterpret_cast<const u64*>(a.layers)[i];
   }
-  __syncthreads();
+  lds_barrier();  // (P0) layer table in LDS
+  if (wave == 1)
+    for (int q = lane; q < G::NSL16; q += 64) reinterpret_cast<uint4*>(sm.nw[0])[q] = ld_global16(slot_chunk(0, q));
+
+  // Loads of phase Q's registers (A=0: QKV, B=1: K/V rows, C=2: o_proj, D=3: gate/up, E=4: down)
+  // for `layer`; past the last layer they re-read the last one. Every path issues the same loads
+  // in the same order, so the compiler's wait counts stay exact (a load under a data-dependent
+  // condition would make it wait for all outstanding loads). Phase P of layer l issues the loads
+  // of phase P + DIST (of layer l, or of layer l + 1 when it wraps): DIST sets how many phases'
+  // weights each CU keeps in flight.
+  auto load_phase = [&](auto qc, int layer) {
+    constexpr int Q = decltype(qc)::value;
+    layer = layer < L ? layer : L - 1;
+    const mk_layer_weights& lw = sm.layers[layer];
+    const int mwq = opaque(mw), lq = opaque(lane);
+    if constexpr (Q == 0) tile_load<TA, TA::PS>(wA, 0, mwq, lq, rows_A(lw));
+    if constexpr (Q == 1) {
+#pragma unroll
+      for (int r = 0; r < NKV; ++r) {
+        kK[r] = ld_stream(kv_row(a.k_cache, layer, kv_pos(r)));
+        kV[r] = ld_stream(kv_row(a.v_cache, layer, kv_pos(r)));
+      }
+    }
+    if constexpr (Q == 2) tile_load<TC, TC::PS>(wC, 0, mwq, lq, rows_C(lw));
+    if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, rows_D(lw));
+    if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, rows_E(lw));
+  };
+  // at the start of phase P (DIST < 5) or after its consumption (DIST == 5)
+  auto issue_ahead = [&](auto pc, int layer) {
+    constexpr int P = decltype(pc)::value;
+    constexpr int Q = P + DIST;
+    if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
+    else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  constexpr bool AFTER = DIST == 5;
+  if constexpr (DIST > 0) load_phase(I0(), 0);
+  if constexpr (DIST > 1) load_phase(I1(), 0);
+  if constexpr (DIST > 2) load_phase(I2(), 0);
+  if constexpr (DIST > 3) load_phase(I3(), 0);
+  if constexpr (DIST > 4) load_phase(I4(), 0);
+  lds_barrier();  // (P1) norm weights of layer 0 in LDS
+  lds_barrier();  // (P2) comm: x = RMSNorm(embedding)
 
   for (int layer = 0; layer < L; ++layer) {
-    const mk_layer_weights lw = a.layers[layer];
-    const uint32_t ep = (seq << 6) | (uint32_t)layer;
+    const mk_layer_weights& lw = sm.layers[layer];
     const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
-    float* qkv_x = ws + W_QKV + xcd * QKV_X;
-    float* att_x = ws + W_ATT + (size_t)xcd * WPX * 2 * APS;
-    float* m_x = ws + W_M + xcd * IX;
-    float* lc_x = ws + W_LC + xcd * H;
-    float* le_x = ws + W_LE + xcd * H;
 
-    // ---- A: QKV rows of this XCD's group -------------------------------------------------
-    mark(a, tl + 0);
-    if (!comm) {
-      const int gq = opaque(g), tq = opaque(t);
-      load_units<PC, UPR_C>(wC, 0, U_C, gq, tq, ptr_C(lw));
-      load_kv(layer);
-      gemv_phase<NU_A, PA, UPR_H>(wA, U_A, gq, tq, ptr_A(lw), s_x, s_up);
+    // A: QKV rows
+    if constexpr (!AFTER) issue_ahead(I0(), layer);
+    tile_consume<TA>(wA, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_A(lw), [&]() { mark(a, tl + T_M_A_DOT, 64); });
+    if constexpr (AFTER) issue_ahead(I0(), layer);
+    if (wave == 1) {
+#pragma unroll
+      for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, lane + 64 * k));
     }
-    __syncthreads();
-    if (comm) {
-      if (lane < QKV_WG) {
-        float s = 0.f;
-#pragma unroll
-        for (int b = 0; b < UPR_H; ++b) s += s_up[lane * UPR_H + b];
-        st_local_f32(qkv_x + QKV_WG * j + lane, s);
-      }
-      store_fence();
-      mark(a, tl + 1);
-      if (lane == 0) st_local_u32(fl + fl_local(F_QKV, xcd) + j, ep);
-      poll_flags(c, fl + fl_local(F_QKV, xcd), WPX, ep);
-      mark(a, tl + 10);
-      // q heads 2x, 2x+1 at [0, 256), k head x at [256, 384), v head x at [384, 512)
-      float t0[3], t1[3];
-#pragma unroll
-      for (int h = 0; h < 3; ++h) {
-        t0[h] = ld_dev_f32(qkv_x + h * D + lane);
-        t1[h] = ld_dev_f32(qkv_x + h * D + lane + 64);
-      }
-      const float v0 = ld_dev_f32(qkv_x + 3 * D + lane), v1 = ld_dev_f32(qkv_x + 3 * D + lane + 64);
-      const uint16_t* qn = (const uint16_t*)lw.q_norm_weight;
-      const uint16_t* kn = (const uint16_t*)lw.k_norm_weight;
-#pragma unroll
-      for (int h = 0; h < 3; ++h) {
-        // per-head RMSNorm then rotate-half RoPE (/root/reference/megakernel.cu:490-630)
-        const uint16_t* nw = h < 2 ? qn : kn;
-        const float rs = rsqrtf(wave_sum(t0[h] * t0[h] + t1[h] * t1[h]) / (float)D + EPS);
-        const float u0 = t0[h] * rs * bf16_to_f32(gp(nw)[lane]);
-        const float u1 = t1[h] * rs * bf16_to_f32(gp(nw)[lane + 64]);
-        const float o0 = u0 * cs_c0 - u1 * cs_s0;
-        const float o1 = u1 * cs_c1 + u0 * cs_s1;
-        if (h < 2) { s_q[h][lane] = o0; s_q[h][lane + 64] = o1; }
-        else { s_k[lane] = round_bf16(o0); s_k[lane + 64] = round_bf16(o1); }
-      }
-      s_v[lane] = round_bf16(v0);
-      s_v[lane + 64] = round_bf16(v1);
-      if (j == 0) {
-        const size_t slot = (((size_t)layer * HKV + xcd) * a.max_seq + position) * D;
-        gpw(a.k_cache)[slot + lane] = f32_to_bf16(s_k[lane]);
-        gpw(a.k_cache)[slot + lane + 64] = f32_to_bf16(s_k[lane + 64]);
-        gpw(a.v_cache)[slot + lane] = f32_to_bf16(v0);
-        gpw(a.v_cache)[slot + lane + 64] = f32_to_bf16(v1);
-      }
-    }
-    __syncthreads();
+    mark(a, tl + T_M_A_END, 64);
+    lds_barrier();  // (A1)
+    lds_barrier();  // (A2) comm: q, new K/V in LDS
+    mark(a, tl + T_M_B_START, 64);
 
-    // ---- B: split-K attention over this workgroup's positions ----------------------------
-    mark(a, tl + 2);
-    if (!comm) {
-      load_units<PD, UPR_H>(wD, 0, U_D, opaque(g), opaque(t), ptr_D(lw));
-      const float q00 = s_q[0][2 * lane], q01 = s_q[0][2 * lane + 1];
-      const float q10 = s_q[1][2 * lane], q11 = s_q[1][2 * lane + 1];
+    // B: split-K attention
+    if constexpr (!AFTER) issue_ahead(I1(), layer);
+    if (st.att_wg) {
+      float qa[8], qb[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { qa[i] = sm.q[0][8 * t + i]; qb[i] = sm.q[1][8 * t + i]; }
+      const uint4 knew = *reinterpret_cast<const uint4*>(&sm.kvn[0][8 * t]);
+      const uint4 vnew = *reinterpret_cast<const uint4*>(&sm.kvn[1][8 * t]);
       float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-      float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
-      const size_t hb = ((size_t)layer * HKV + xcd) * a.max_seq * D;
-      const uint32_t* kc = reinterpret_cast<const uint32_t*>(a.k_cache + hb);
-      const uint32_t* vc = reinterpret_cast<const uint32_t*>(a.v_cache + hb);
-      for (int i = 0; i < np_w; ++i) {
-        const int p = p0 + mw + NMW * i;
-        uint32_t kw, vw;
-        if (p == position) {
-          kw = (uint32_t)f32_to_bf16(s_k[2 * lane]) | ((uint32_t)f32_to_bf16(s_k[2 * lane + 1]) << 16);
-          vw = (uint32_t)f32_to_bf16(s_v[2 * lane]) | ((uint32_t)f32_to_bf16(s_v[2 * lane + 1]) << 16);
-        } else if (i < APF) {
-          kw = kv_k[0]; vw = kv_v[0];
+      float a0[8], a1[8];
 #pragma unroll
-          for (int q = 1; q < APF; ++q) if (i == q) { kw = kv_k[q]; vw = kv_v[q]; }
-        } else {
-          kw = gp(kc)[(size_t)p * (D / 2) + lane];
-          vw = gp(vc)[(size_t)p * (D / 2) + lane];
-        }
-        const float k0 = bf16_lo(kw), k1 = bf16_hi(kw), v0 = bf16_lo(vw), v1 = bf16_hi(vw);
-        const float s0 = wave_sum(q00 * k0 + q01 * k1) * ATT_SCALE;
-        const float s1 = wave_sum(q10 * k0 + q11 * k1) * ATT_SCALE;
-        const float n0 = fmaxf(m0, s0), n1 = fmaxf(m1, s1);
-        const float c0 = expf(m0 - n0), c1 = expf(m1 - n1);
-        const float e0 = expf(s0 - n0), e1 = expf(s1 - n1);
-        l0 = l0 * c0 + e0; l1 = l1 * c1 + e1;
-        a00 = a00 * c0 + e0 * v0; a01 = a01 * c0 + e0 * v1;
-        a10 = a10 * c1 + e1 * v0; a11 = a11 * c1 + e1 * v1;
-        m0 = n0; m1 = n1;
+      for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
+      auto attend = [&](uint4 kw, uint4 vw) {
+        float kf[8], vf[8];
+        unpack8(kw, kf);
+        unpack8(vw, vf);
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
+        d0 = row16_sum(d0) * ATT_SCALE;
+        d1 = row16_sum(d1) * ATT_SCALE;
+        softmax_step(d0, vf, m0, l0, a0);
+        softmax_step(d1, vf, m1, l1, a1);
+      };
+#pragma unroll
+      for (int r = 0; r < NKV; ++r) {
+        const int p = st.p0 + g + MG * r;
+        if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r]);
       }
-      s_wp[mw][0][2 * lane] = a00; s_wp[mw][0][2 * lane + 1] = a01;
-      s_wp[mw][1][2 * lane] = a10; s_wp[mw][1][2 * lane + 1] = a11;
-      if (lane == 0) { s_wp[mw][0][D] = m0; s_wp[mw][0][D + 1] = l0; s_wp[mw][1][D] = m1; s_wp[mw][1][D + 1] = l1; }
+      // positions beyond the register-held ones (long contexts) stream here
+      for (int p = st.p0 + g + MG * NKV; p < st.p1; p += MG) {
+        const uint4 kw = p == st.position ? knew : ld_global16(kv_row(a.k_cache, layer, p));
+        const uint4 vw = p == st.position ? vnew : ld_global16(kv_row(a.v_cache, layer, p));
+        attend(kw, vw);
+      }
+      // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
+      // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
+      auto merge_rows = [&](float& m, float& l, float (&acc)[8]) {
+        float M = xmax32(xmax16(m));
+        const float f = M == -INFINITY ? 0.f : __expf(m - M);
+        l = xsum32(xsum16(l * f));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = xsum32(xsum16(acc[i] * f));
+        m = M;
+      };
+      merge_rows(m0, l0, a0);
+      merge_rows(m1, l1, a1);
+      if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) {
+          *reinterpret_cast<float4*>(&sm.gp[mw][0][8 * t + i]) = make_float4(a0[i], a0[i + 1], a0[i + 2], a0[i + 3]);
+          *reinterpret_cast<float4*>(&sm.gp[mw][1][8 * t + i]) = make_float4(a1[i], a1[i + 1], a1[i + 2], a1[i + 3]);
+        }
+        if (t == 0) { sm.gp[mw][0][D] = m0; sm.gp[mw][0][D + 1] = l0; sm.gp[mw][1][D] = m1; sm.gp[mw][1][D + 1] = l1; }
+      }
     }
-    __syncthreads();
-    if (comm) {
-      // merge the 7 waves' partials: lane -> head h = lane / 32, dims 4*(lane % 32) .. +3
-      const int h = lane >> 5, d0 = (lane & 31) * 4;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < NMW; ++w) M = fmaxf(M, s_wp[w][h][D]);
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      float Lsum = 0.f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < NMW; ++w) {
-          const float mw_ = s_wp[w][h][D];
-          if (mw_ != -INFINITY) {
-            const float f = expf(mw_ - M);
-            acc.x += s_wp[w][h][d0] * f; acc.y += s_wp[w][h][d0 + 1] * f;
-            acc.z += s_wp[w][h][d0 + 2] * f; acc.w += s_wp[w][h][d0 + 3] * f;
-            Lsum += s_wp[w][h][D + 1] * f;
-          }
-        }
-      }
-      float* dst = att_x + ((size_t)j * 2 + h) * APS;
-      if (j < S) {
-        st_local_f32(dst + d0, acc.x); st_local_f32(dst + d0 + 1, acc.y);
-        st_local_f32(dst + d0 + 2, acc.z); st_local_f32(dst + d0 + 3, acc.w);
-        if ((lane & 31) == 0) { st_local_f32(dst + D, M); st_local_f32(dst + D + 1, Lsum); }
-      }
-      store_fence();
-      mark(a, tl + 3);
-      if (lane == 0) st_local_u32(fl + fl_local(F_ATT, xcd) + j, ep);
-      poll_flags(c, fl + fl_local(F_ATT, xcd), S, ep);
-      mark(a, tl + 11);
-      // merge the S split partials of this XCD's two heads -> s_x[0, 256): lane jj < S reads
-      // split jj's (m, l) for both heads, the wave reduces them, then every lane accumulates its
-      // 4 dims of one head over the splits with the loads of a batch in flight together
-      float mj[2], lj[2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const float* src = att_x + ((size_t)(lane < S ? lane : 0) * 2 + hh) * APS;
-        mj[hh] = ld_dev_f32(src + D);
-        lj[hh] = ld_dev_f32(src + D + 1);
-        if (lane >= S) { mj[hh] = -INFINITY; lj[hh] = 0.f; }
-      }
-      float Mh[2], Lh[2], fh[2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        Mh[hh] = wave_max(mj[hh]);
-        fh[hh] = mj[hh] == -INFINITY ? 0.f : expf(mj[hh] - Mh[hh]);
-        Lh[hh] = wave_sum(lj[hh] * fh[hh]);
-      }
-      float* s_f = &s_wp[0][0][0];  // merge weights [2][32], reusing the wave-partial buffer
-      if (lane < WPX) { s_f[lane] = fh[0]; s_f[WPX + lane] = fh[1]; }
-      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int j0 = 0; j0 < S; j0 += 8) {
-        float4 aj[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int jj = j0 + q < S ? j0 + q : j0;
-          aj[q] = ld_dev_f32x4(att_x + ((size_t)jj * 2 + h) * APS, d0 * 4);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (j0 + q < S) {
-            const float f = s_f[h * WPX + j0 + q];
-            o.x += aj[q].x * f; o.y += aj[q].y * f; o.z += aj[q].z * f; o.w += aj[q].w * f;
-          }
-        }
-      }
-      const float inv = 1.f / Lh[h];
-      s_x[h * D + d0] = o.x * inv; s_x[h * D + d0 + 1] = o.y * inv;
-      s_x[h * D + d0 + 2] = o.z * inv; s_x[h * D + d0 + 3] = o.w * inv;
-    }
-    __syncthreads();
+    if constexpr (AFTER) issue_ahead(I1(), layer);
+    mark(a, tl + T_M_B_END, 64);
+    lds_barrier();  // (B1)
+    lds_barrier();  // (B2) comm: attention output in x[0, 256)
 
-    // ---- C: o_proj partial over this group's 256 columns --------------------------------------
-    mark(a, tl + 4);
-    if (!comm) {
-      const int gq = opaque(g), tq = opaque(t);
-      load_units<PE, UPR_E>(wE, 0, U_E, gq, tq, ptr_E(lw));
-      gemv_phase<NU_C, PC, UPR_C>(wC, U_C, gq, tq, ptr_C(lw), s_x, s_up);
-    }
-    __syncthreads();
-    if (comm) {
-      float* gc = ws + W_GC + (size_t)j * NXCD * MAX_HPW;  // [8][MAX_HPW] for row block j
-      if (lane < HPW) st_dev_f32(gc + xcd * MAX_HPW + lane, s_up[lane * UPR_C] + s_up[lane * UPR_C + 1]);
-      store_fence();
-      mark(a, tl + 5);
-      if (lane == 0) st_dev_u32(fl + fl_cross(0, j, xcd), ep);
-      poll_flags(c, fl + fl_cross(0, j, 0), NXCD, ep, SLOT);
-      mark(a, tl + 12);
-      if (lane < HPW) {
-        float s = 0.f;
-#pragma unroll
-        for (int y = 0; y < NXCD; ++y) s += ld_dev_f32(gc + y * MAX_HPW + lane);
-        st_local_f32(lc_x + HPW * j + lane, s);
-      }
-      store_fence();
-      if (lane == 0) st_local_u32(fl + fl_local(F_LC, xcd) + j, ep);
-      poll_flags(c, fl + fl_local(F_LC, xcd), WPX, ep);
-      mark(a, tl + 13);
-      comm_residual_norm<H>(s_res, lc_x, (const uint16_t*)lw.post_attn_norm_weight, s_x);
-    }
-    __syncthreads();
+    // C: o_proj partial over this group's 256 columns
+    if constexpr (!AFTER) issue_ahead(I2(), layer);
+    tile_consume<TC>(wC, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_C(lw), NoOp());
+    if constexpr (AFTER) issue_ahead(I2(), layer);
+    lds_barrier();  // (C1)
+    lds_barrier();  // (C2) comm: x = RMSNorm(residual) * post-attention norm
 
-    // ---- D: gate/up rows of MLP slice x ------------------------------------------------------
-    mark(a, tl + 6);
-    if (!comm) {
-      const int gq = opaque(g), tq = opaque(t);
-      if (layer + 1 < L) load_units<PA, UPR_H>(wA, 0, U_A, gq, tq, ptr_A(a.layers[layer + 1]));
-      gemv_phase<NU_D, PD, UPR_H>(wD, U_D, gq, tq, ptr_D(lw), s_x, s_up);
-    }
-    __syncthreads();
-    if (comm) {
-      if (lane < IPW) {
-        float gs = 0.f, us = 0.f;
-#pragma unroll
-        for (int b = 0; b < UPR_H; ++b) { gs += s_up[lane * UPR_H + b]; us += s_up[(lane + IPW) * UPR_H + b]; }
-        st_local_f32(m_x + IPW * j + lane, gs / (1.f + expf(-gs)) * us);  // silu(g) * u
-      }
-      store_fence();
-      mark(a, tl + 7);
-      if (lane == 0) st_local_u32(fl + fl_local(F_M, xcd) + j, ep);
-      poll_flags(c, fl + fl_local(F_M, xcd), WPX, ep);
-      mark(a, tl + 14);
-      for (int i = lane * 4; i < IX; i += 256) {
-        const float4 v = ld_dev_f32x4(m_x, i * 4);
-        *reinterpret_cast<float4*>(s_x + i) = v;
-      }
-    }
-    __syncthreads();
+    // D: gate/up rows of MLP slice x
+    if constexpr (!AFTER) issue_ahead(I3(), layer);
+    mark(a, tl + T_M_D_ISSUED, 64);
+    tile_consume<TD>(wD, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_D(lw), [&]() { mark(a, tl + T_M_D_DOT, 64); });
+    if constexpr (AFTER) issue_ahead(I3(), layer);
+    lds_barrier();  // (D1)
+    lds_barrier();  // (D2) comm: x[0, IX) = silu(gate) * up of the slice
 
-    // ---- E: down_proj partial over slice x's columns -----------------------------------------
-    mark(a, tl + 8);
-    if (!comm) gemv_phase<NU_E, PE, UPR_E>(wE, U_E, opaque(g), opaque(t), ptr_E(lw), s_x, s_up);
-    __syncthreads();
-    if (comm) {
-      float* ge = ws + W_GE + (size_t)j * NXCD * MAX_HPW;
-      if (lane < HPW) {
-        float s = 0.f;
+    // E: down_proj partial over slice x's columns
+    if constexpr (!AFTER) issue_ahead(I4(), layer);
+    tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
+    if constexpr (AFTER) issue_ahead(I4(), layer);
+    if (wave == 1) {
+      // the next layer's norm weights (or the final norm) into the other LDS slot
+      uint4* dst = reinterpret_cast<uint4*>(sm.nw[(layer + 1) & 1]);
 #pragma unroll
-        for (int b = 0; b < UPR_E; ++b) s += s_up[lane * UPR_E + b];
-        st_dev_f32(ge + xcd * MAX_HPW + lane, s);
-      }
-      store_fence();
-      mark(a, tl + 9);
-      if (lane == 0) st_dev_u32(fl + fl_cross(1, j, xcd), ep);
-      poll_flags(c, fl + fl_cross(1, j, 0), NXCD, ep, SLOT);
-      mark(a, tl + 15);
-      if (lane < HPW) {
-        float s = 0.f;
-#pragma unroll
-        for (int y = 0; y < NXCD; ++y) s += ld_dev_f32(ge + y * MAX_HPW + lane);
-        st_local_f32(le_x + HPW * j + lane, s);
-      }
-      store_fence();
-      if (lane == 0) st_local_u32(fl + fl_local(F_LE, xcd) + j, ep);
-      poll_flags(c, fl + fl_local(F_LE, xcd), WPX, ep);
-      mark(a, tl + 16);
-      const uint16_t* nw = layer + 1 < L ? (const uint16_t*)a.layers[layer + 1].norm_weight : a.final_norm;
-      comm_residual_norm<H>(s_res, le_x, nw, s_x);
+      for (int k = 0; k < G::NSL_L; ++k)
+        if (lane + 64 * k < G::NSL16) dst[lane + 64 * k] = nsl[k];
     }
-    __syncthreads();
+    lds_barrier();  // (E1)
+    lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
   }
 
-  // ---- tied LM head over rows [r0, r1), greedy argmax ------------------------------------------
-  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 1);
+  // tied LM head over rows [r0, r1): wave mw takes rows r0 + mw + 7*s, one row per step (64 lanes
+  // x LCPL chunks), LP rows in flight per wave; fused greedy argmax
   {
+    constexpr int LCPL = H / 512;
+    constexpr int LP = 4;
     const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
     const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
-    mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 2);
-    if (!comm) {
-      unsigned long long best = 0;
-      // each group takes whole rows r0+g, r0+g+28, ...; a row is SEG segments of 8 chunks per lane;
-      // the next segment's loads are issued before the current one is consumed
-      constexpr int SEG = UPR_H / 8;
-      const int gq = opaque(g), tq = opaque(t);
-      int r = r0 + gq;
-      int sg = 0;
-      uint4 cur[8], nxt[8];
-      auto seg_ptr = [&](int row, int seg) {
-        return reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + 128 * seg + tq;
-      };
-      {
-        const int rl = r < r1 ? r : r0;
+    const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
+    const int lq = opaque(lane), mwq = opaque(mw);
+    uint4 xh[LCPL], xl[LCPL];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) cur[b] = ld_stream(seg_ptr(rl, 0) + 16 * b);
-      }
-      float acc = 0.f;
-      while (r < r1) {
-        const int sn = sg + 1 == SEG ? 0 : sg + 1;
-        const int rn = sg + 1 == SEG ? r + MG : r;
-        {
-          const int rl = rn < r1 ? rn : r;  // past the end: re-read the current segment, unused
-          const int sl = rn < r1 ? sn : sg;
+    for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
+    auto lm_load = [&](int s, uint4 (&b)[LCPL]) {
+      int row = r0 + mwq + NMW * s;
+      row = row < r1 ? row : r1 - 1;  // past the end: re-read the last row (unconditional loads)
+      const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lq;
 #pragma unroll
-          for (int b = 0; b < 8; ++b) nxt[b] = ld_stream(seg_ptr(rl, sl) + 16 * b);
+      for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
+    };
+    uint4 buf[LP][LCPL];
+#pragma unroll
+    for (int i = 0; i < LP; ++i) lm_load(i, buf[i]);
+    u64 best = 0;
+    for (int s0 = 0; s0 < nmine; s0 += LP) {
+#pragma unroll
+      for (int i = 0; i < LP; ++i) {
+        const float v = wave_sum(dot_chunks<LCPL>(buf[i], xh, xl));
+        const int s = s0 + i;
+        if (s < nmine) {
+          const int row = r0 + mwq + NMW * s;
+          if (lq == 0) gpw(a.logits)[row] = v;
+          best = umax64(best, argmax_key(v, row));
         }
-        const float* xs = s_x + 1024 * sg + tq * 8;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) acc = dot8(cur[b], xs + 128 * b, acc);
-        if (sg + 1 == SEG) {
-          const float v = row16_sum(acc);
-          if (tq == 0) {
-            gpw(a.logits)[r] = v;
-            best = umax64(best, argmax_key(v, r));
-          }
-          acc = 0.f;
-        }
-#pragma unroll
-        for (int b = 0; b < 8; ++b) cur[b] = nxt[b];
-        r = rn;
-        sg = sn;
+        lm_load(s + LP, buf[i]);
       }
-      for (int off = 32; off >= 1; off >>= 1) best = umax64(best, __shfl_xor(best, off));
-      if (lane == 0) s_best[mw] = best;
     }
-    __syncthreads();
-    mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 3);
-    if (comm) {
-      const uint32_t ep_end = (seq << 6) | 63u;
-      unsigned long long b = 0;
+    if (lane == 0) sm.best[mw] = best;
+  }
+  lds_barrier();  // (F) per-wave argmax keys in LDS
+}
+
+// ---- comm wave -------------------------------------------------------------------------------
+template <int H, int I>
+__device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const Step& st) {
+  typedef Geo<H, I> G;
+  const int lane = threadIdx.x & 63;
+  const int xcd = st.xcd, j = st.j, L = st.L, S = st.S;
+  u64* xw = a.xw;
+  Comm c;
+  c.status = reinterpret_cast<uint32_t*>(xw + X_STATUS);
+  float res[G::E];
+
+  lds_barrier();  // (P0)
+#ifdef MK_COMM_PRIO
+  __builtin_amdgcn_s_setprio(MK_COMM_PRIO);  // the comm wave's instructions issue ahead of math waves'
+#endif
+  const uint32_t seq = ld_dev_u32(reinterpret_cast<const uint32_t*>(xw + X_SEQ));
+  {
+    const uint32_t st0 = ld_dev_u32(c.status);
+    c.wt = (st0 & ERR_PLACEMENT) != 0;
+    if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, st0 | ERR_PLACEMENT);
+  }
+  {
+    const uint16_t* row = a.embed + (size_t)a.token * H;
 #pragma unroll
-      for (int w = 0; w < NMW; ++w) b = umax64(b, s_best[w]);
-      // this workgroup's best key and done flag, in its own slot: key first, flag after it
-      uint32_t* mine = fl + fl_done(blockIdx.x);
-      if (lane == 0) __hip_atomic_store(reinterpret_cast<unsigned long long*>(mine + 2), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      store_fence();
-      if (lane == 0) st_dev_u32(mine, ep_end);
-      if (blockIdx.x == 0) {
-        // the grid's greedy token: poll all 256 done flags (4 per lane), then reduce the keys
-        for (uint32_t it = 0; !c.failed; ++it) {
-          bool ok = true;
+    for (int k = 0; k < G::E; k += 8) {
+      float v[8];
+      unpack8(ld_global16(reinterpret_cast<const uint4*>(row + G::E * lane + k)), v);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ok &= ld_dev_u32(fl + fl_done(lane * 4 + q)) == ep_end;
-          if (__ballot(!ok) == 0) break;
-          if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) c.failed = true;
-          if (it > SPIN_LIMIT) { if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT); c.failed = true; }
+      for (int q = 0; q < 8; ++q) res[k + q] = v[q];
+    }
+    const uint16_t* cr = a.cos_tab + (size_t)st.position * D;
+    const uint16_t* sr = a.sin_tab + (size_t)st.position * D;
+    sm.cs[0][lane] = bf16_to_f32(gp(cr)[lane]); sm.cs[0][lane + 64] = bf16_to_f32(gp(cr)[lane + 64]);
+    sm.cs[1][lane] = bf16_to_f32(gp(sr)[lane]); sm.cs[1][lane + 64] = bf16_to_f32(gp(sr)[lane + 64]);
+  }
+  lds_barrier();  // (P1)
+  comm_norm<H>(res, sm.nw[0], sm.xh, sm.xl);
+  lds_barrier();  // (P2)
+
+  for (int layer = 0; layer < L; ++layer) {
+    const uint32_t ep = (seq << 6) | (uint32_t)layer;
+    const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
+    const uint16_t* nw = sm.nw[layer & 1];
+
+    // ---- A: publish QKV rows; attention workgroups gather q, k, v of the group --------------
+    mark(a, tl + T_A_START);
+    lds_barrier();  // (A1)
+    if (lane < QKV_WG) ll_st(c, xw + X_QKV + xcd * QKV_X + QKV_WG * j + lane, ll_word(sm.up[lane], ep), false);
+    mark(a, tl + T_A_PUB);
+    if (st.att_wg) {
+      // lane -> 8 values: q head 2x (lanes 0-15), q head 2x+1 (16-31), k head x (32-47), v (48-63)
+      int off[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) off[k] = xcd * QKV_X + 8 * lane + 2 * k;
+      float v[8];
+      ll_poll<4>(c, xw + X_QKV, off, true, ep, v);
+      mark(a, tl + T_A_POLL);
+      const int tt = lane & 15, part = lane >> 4;
+      // per-head RMSNorm (/root/reference/megakernel.cu:490-630): a head is one 16-lane row
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+      ss = row16_sum(ss);
+      const float rs = rsqrtf(ss / (float)D + EPS);
+      const uint16_t* hw = nw + 2 * H + (part == 2 ? D : 0);
+      float u[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = v[i] * rs * bf16_to_f32(hw[8 * tt + i]);
+      // rotate-half RoPE with the table entry of dim d mod 64 (/root/reference/megakernel.cu:548-555);
+      // dim d's partner d +- 64 sits in lane tt ^ 8 of the same row
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float pr = dpp<0x128>(u[i]);
+        const int d = (8 * tt + i) & 63;
+        const float cv = sm.cs[0][d], sv = sm.cs[1][d];
+        o[i] = tt < 8 ? u[i] * cv - pr * sv : u[i] * cv + pr * sv;
+      }
+      if (part < 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sm.q[part][8 * tt + i] = o[i];
+      } else {
+        const float* src = part == 2 ? o : v;
+        const u4v pk = {pack_bf16x2(src[0], src[1]), pack_bf16x2(src[2], src[3]), pack_bf16x2(src[4], src[5]),
+                        pack_bf16x2(src[6], src[7])};
+        *reinterpret_cast<u4v*>(&sm.kvn[part - 2][8 * tt]) = pk;
+        if (j == S - 1) {  // the split that owns `position` stores the new K/V in the cache
+          uint16_t* cache = part == 2 ? a.k_cache : a.v_cache;
+          *gpw(reinterpret_cast<u4v*>(cache + (((size_t)layer * HKV + xcd) * a.max_seq + st.position) * D + 8 * tt)) = pk;
         }
-        unsigned long long m = 0;
+      }
+    }
+    lds_barrier();  // (A2)
+
+    // ---- B: publish this split's partial; merge all splits of the group ----------------------
+    mark(a, tl + T_B_START);
+    lds_barrier();  // (B1)
+    {
+      const int h = lane >> 5, d0 = (lane & 31) * 4;
+      u64* att_x = xw + X_ATT + (size_t)xcd * WPX * APW;
+      if (st.att_wg) {
+        // merge the 7 wave partials of this split: lane -> head h, dims d0 .. d0+3. A wave without
+        // keys has m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0.
+        float mq[NMW];
+#pragma unroll
+        for (int q = 0; q < NMW; ++q) mq[q] = sm.gp[q][h][D];
+        float M = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < NMW; ++q) M = fmaxf(M, mq[q]);
+        mark(a, tl + T_B_MAX);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float Ls = 0.f;
+#pragma unroll
+        for (int q = 0; q < NMW; ++q) {
+          const float f = __expf(mq[q] - M);
+          const float4 p = *reinterpret_cast<const float4*>(&sm.gp[q][h][d0]);
+          acc.x = fmaf(p.x, f, acc.x); acc.y = fmaf(p.y, f, acc.y);
+          acc.z = fmaf(p.z, f, acc.z); acc.w = fmaf(p.w, f, acc.w);
+          Ls = fmaf(sm.gp[q][h][D + 1], f, Ls);
+        }
+        mark(a, tl + T_B_SUM);
+        const int mine = j * APW;
+        ll_st2(c, att_x, mine + h * D + d0, acc.x, acc.y, ep, false);
+        ll_st2(c, att_x, mine + h * D + d0 + 2, acc.z, acc.w, ep, false);
+        if ((lane & 31) == 0) ll_st2(c, att_x, mine + 2 * D + 2 * h, M, Ls, ep, false);
+        mark(a, tl + T_B_PUB);
+      }
+      // merge the S split partials of this XCD's two heads -> s_x[0, 256), in split order
+      float M = -INFINITY, Ls = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int s0 = 0; s0 < S; s0 += 2) {
+        int off[6];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int s = s0 + q < S ? s0 + q : s0;
+          off[3 * q + 0] = s * APW + h * D + d0;
+          off[3 * q + 1] = s * APW + h * D + d0 + 2;
+          off[3 * q + 2] = s * APW + 2 * D + 2 * h;
+        }
+        float v[12];
+        ll_poll<6>(c, att_x, off, true, ep, v);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (s0 + q < S) {
+            const float ms = v[6 * q + 4], ls = v[6 * q + 5];
+            const float n = fmaxf(M, ms);
+            const float cm = __expf(M - n), cs = __expf(ms - n);
+            Ls = Ls * cm + ls * cs;
+            acc.x = acc.x * cm + v[6 * q + 0] * cs; acc.y = acc.y * cm + v[6 * q + 1] * cs;
+            acc.z = acc.z * cm + v[6 * q + 2] * cs; acc.w = acc.w * cm + v[6 * q + 3] * cs;
+            M = n;
+          }
+        }
+      }
+      mark(a, tl + T_B_POLL);
+      const float inv = 1.f / Ls;
+      const float o[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+      store_hilo<4>(sm.xh, sm.xl, h * D + d0, o);
+    }
+    lds_barrier();  // (B2)
+
+    // ---- C: o_proj partials -> residual -> post-attention RMSNorm ------------------------------
+    mark(a, tl + T_C_START);
+    lds_barrier();  // (C1)
+    {
+      const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
+      mark(a, tl + T_C_PUB);
+      comm_cross_reduce<H>(c, xw, X_OX, X_OL, xcd, j, mine, ep, res, a, tl + T_C_XPOLL, tl + T_C_LPOLL);
+      comm_norm<H>(res, nw + H, sm.xh, sm.xl);
+    }
+    lds_barrier();  // (C2)
+
+    // ---- D: silu(gate) * up of this workgroup's rows; gather the XCD's slice ------------------
+    mark(a, tl + T_D_START);
+    lds_barrier();  // (D1)
+    {
+      u64* m_x = xw + X_M + (size_t)xcd * MAX_IX;
+      if (lane < G::IPW) {
+        const float gs = sm.up[lane], us = sm.up[lane + G::IPW];
+        ll_st(c, m_x + G::IPW * j + lane, ll_word(gs / (1.f + expf(-gs)) * us, ep), false);  // silu(g) * u
+      }
+      mark(a, tl + T_D_PUB);
+      int off[G::IXL / 2];
+#pragma unroll
+      for (int k = 0; k < G::IXL / 2; ++k) off[k] = G::IXL * lane + 2 * k;
+      float v[G::IXL];
+      ll_poll<G::IXL / 2>(c, m_x, off, true, ep, v);
+      mark(a, tl + T_D_POLL);
+      store_hilo<G::IXL>(sm.xh, sm.xl, G::IXL * lane, v);
+    }
+    lds_barrier();  // (D2)
+
+    // ---- E: down_proj partials -> residual -> next layer's input RMSNorm ----------------------
+    mark(a, tl + T_E_START);
+    lds_barrier();  // (E1)
+    {
+      const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
+      mark(a, tl + T_E_PUB);
+      comm_cross_reduce<H>(c, xw, X_EX, X_EL, xcd, j, mine, ep, res, a, tl + T_E_XPOLL, tl + T_E_LPOLL);
+      comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm, or the final norm
+    }
+    lds_barrier();  // (E2)
+  }
+
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 1);
+  lds_barrier();  // (F)
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 2);
+  {
+    const uint32_t ep_end = (seq << 6) | 63u;
+    u64 b = 0;
+#pragma unroll
+    for (int w = 0; w < NMW; ++w) b = umax64(b, sm.best[w]);
+    // this workgroup's best key and done flag, in its own slot: key first, flag after it
+    u64* mine = xw + X_DONE + (size_t)blockIdx.x * 16;
+    if (lane == 0) __hip_atomic_store(mine, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmem();
+    if (lane == 0) __hip_atomic_store(mine + 1, (u64)ep_end, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (blockIdx.x == 0) {
+      // the grid's greedy token: poll all 256 done flags (4 per lane), then reduce the keys
+      for (uint32_t it = 0; !c.failed; ++it) {
+        bool ok = true;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          m = umax64(m, __hip_atomic_load(reinterpret_cast<unsigned long long*>(fl + fl_done(lane * 4 + q) + 2),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        for (int off = 32; off >= 1; off >>= 1) m = umax64(m, __shfl_xor(m, off));
-        if (lane == 0) {
-          if (a.out_token) *gpw(a.out_token) = m ? (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu)) : -1;
-          st_dev_u32(fl + FL_SEQ, seq + 1);  // every workgroup read seq at its start
-        }
+          ok &= __hip_atomic_load(xw + X_DONE + (size_t)(lane * 4 + q) * 16 + 1, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) == (u64)ep_end;
+        if (__ballot(!ok) == 0) break;
+        if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) c.failed = true;
+        if (it > SPIN_LIMIT) { if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT); c.failed = true; }
+      }
+      u64 m = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        m = umax64(m, __hip_atomic_load(xw + X_DONE + (size_t)(lane * 4 + q) * 16, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT));
+      for (int off = 32; off >= 1; off >>= 1) m = umax64(m, __shfl_xor(m, off));
+      if (lane == 0) {
+        if (a.out_token) *gpw(a.out_token) = m ? (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu)) : -1;
+        st_dev_u32(reinterpret_cast<uint32_t*>(xw + X_SEQ), seq + 1);  // every workgroup read seq at its start
       }
     }
   }
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 3);
+}
+
+template <int H, int I>
+__global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
+  __shared__ __attribute__((aligned(16))) Smem<H, I> sm;
+  const Step st = make_step(a);
+  mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 0);
+  if (threadIdx.x < 64) comm_role<H, I>(a, sm, st);
+  else math_role<H, I, PF_DIST>(a, sm, st);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -754,13 +1032,13 @@ static hipError_t check_kernel_fits() {
   return blocks >= 1 ? hipSuccess : hipErrorCooperativeLaunchTooLarge;
 }
 
-// Zero every flag and start the launch sequence at 1 (flag value 0 never matches an epoch).
-static hipError_t clear_flags(void* ws) {
-  char* fl = (char*)ws + WS_FLOATS * 4;
-  hipError_t e = hipMemset(fl, 0, FL_WORDS * 4);
+// Zero every exchange word, the status word and start the launch sequence at 1 (epoch 0 never
+// matches).
+static hipError_t clear_workspace(void* ws) {
+  hipError_t e = hipMemset(ws, 0, WS_BYTES);
   if (e != hipSuccess) return e;
   const uint32_t one = 1;
-  e = hipMemcpy(fl + FL_SEQ * 4, &one, 4, hipMemcpyHostToDevice);
+  e = hipMemcpy((char*)ws + X_SEQ * 8, &one, 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return e;
   return hipDeviceSynchronize();
 }
@@ -781,8 +1059,7 @@ static hipError_t device_state(DeviceState** out) {
     if ((e = check_kernel_fits<1024, 3072>()) != hipSuccess) return e;
     if ((e = check_kernel_fits<2048, 6144>()) != hipSuccess) return e;
     if ((e = hipMalloc(&s.ws, WS_BYTES)) != hipSuccess) return e;
-    if ((e = hipMemset(s.ws, 0, WS_BYTES)) != hipSuccess) return e;
-    if ((e = clear_flags(s.ws)) != hipSuccess) return e;
+    if ((e = clear_workspace(s.ws)) != hipSuccess) return e;
     s.ok = true;
   }
   if (!s.ok) return hipErrorNotSupported;
@@ -827,8 +1104,7 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.v_cache = (uint16_t*)v_cache;
   k.logits = logits;
   k.out_token = out_token;
-  k.ws = (float*)st->ws;
-  k.fl = (uint32_t*)((char*)st->ws + WS_FLOATS * 4);
+  k.xw = (u64*)st->ws;
   k.trace = st->trace;
   k.token = token_id;
   k.position = position;
@@ -860,7 +1136,7 @@ extern "C" hipError_t mk_status(uint32_t* status) {
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  return hipMemcpy(status, (char*)st->ws + WS_FLOATS * 4 + FL_STATUS * 4, 4, hipMemcpyDeviceToHost);
+  return hipMemcpy(status, (char*)st->ws + X_STATUS * 8, 4, hipMemcpyDeviceToHost);
 }
 
 extern "C" hipError_t mk_reset(void) {
@@ -868,7 +1144,7 @@ extern "C" hipError_t mk_reset(void) {
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  return clear_flags(st->ws);
+  return clear_workspace(st->ws);
 }
 
 extern "C" hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes) {
@@ -887,4 +1163,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.2 (gfx950; comm/math waves, flag exchanges)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.3 (gfx950; LL exchanges, layer-ahead weight registers)"; }

@@ -142,7 +142,10 @@ int main(int argc, char** argv) {
   CK(hipEventCreate(&t1));
   CK(hipEventRecord(t0, stream));
   for (int s = 0; s < steps; ++s) {
-    if (trace && s == steps - 1) CK(mk_set_trace(trace, mk_trace_bytes()));
+    if (trace && s == steps - 1) {
+      CK(hipMemsetAsync(trace, 0, mk_trace_bytes(), stream));
+      CK(mk_set_trace(trace, mk_trace_bytes()));
+    }
     CK(hipEventRecord(ev[2 * s], stream));
     CK(mk_decode(&dims, (token + 7 * s) % (int)V, embed, embed, fnorm, dtable, cosd, sind, kc, vc, prompt + s, max_seq, logits,
                  tok, stream));
