@@ -5,20 +5,19 @@
 // residual} -> final RMSNorm -> tied LM head -> greedy argmax. This is the work of the reference's
 // decode_kernel (/root/reference/megakernel.cu:744-893), re-planned for 256 CUs in 8 XCDs.
 //
-// Placement. One 512-thread workgroup per CU. Workgroup b runs on XCD x = b % 8 as local
-// workgroup j = b / 8 (the dispatcher's round-robin placement; every workgroup checks its
+// Placement. One 576-thread workgroup (9 waves) per CU. Workgroup b runs on XCD x = b % 8 as
+// local workgroup j = b / 8 (the dispatcher's round-robin placement; every workgroup checks its
 // HW_REG_XCC_ID). XCD x owns K/V head x -- the 512 Q/K/V rows of that group, its attention and its
 // 256 columns of o_proj -- plus a 1/8 slice of the MLP intermediate, so within a layer only two
 // exchanges (the o_proj and down_proj partial sums) leave the XCD.
 //
 // Roles. Wave 0 of every workgroup is the communication wave: it publishes this workgroup's
 // results, polls for other workgroups' results and does the vector work (residual, RMSNorm, q/k
-// norm + RoPE, attention merges, SiLU). Waves 1-7 are math waves. Each math lane holds the weights
-// of every phase of the NEXT layer in registers: a phase's weights are consumed from registers and
-// the same registers are immediately reloaded with the next layer's weights, so weight traffic runs
-// a full layer ahead of the dependency chain and never waits on it. Because vector-memory
-// completions are counted in issue order per wave, the math waves never poll; the comm wave never
-// prefetches.
+// norm + RoPE, attention merges, SiLU). Waves 1-8 are math waves: each phase's weight tile is
+// loaded into their registers a fixed number of phases ahead (PF_DIST) and consumed from there with
+// bf16 dot instructions; they also run the attention and stream the LM head. Because
+// vector-memory completions are counted in issue order per wave, the math waves never poll and the
+// comm wave never prefetches.
 //
 // Exchanges are "LL" words: 64-bit stores of (value bits | epoch << 32), epoch = launch sequence
 // << 6 | layer. A reader polls the words themselves until every epoch matches, so one store and
@@ -55,12 +54,15 @@ constexpr int HKV = 8;        // K/V heads
 constexpr int NXCD = 8;       // XCDs on MI355X
 constexpr int WPX = 32;       // workgroups per XCD
 constexpr int NWG = NXCD * WPX;
-constexpr int NT = 512;       // threads per workgroup
-constexpr int NMW = 7;        // math waves (1..7)
+constexpr int NMW = 8;        // math waves (1..8); wave 0 is the communication wave
+constexpr int NT = 64 * (NMW + 1);  // threads per workgroup
 constexpr int MG = NMW * 4;   // 16-lane math groups
 constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
 constexpr int QKV_WG = QKV_X / WPX;  // 16
-constexpr int NKV = 2;        // K/V rows per math group held in registers (one layer ahead)
+#ifndef MK_NKV
+#define MK_NKV 1
+#endif
+constexpr int NKV = MK_NKV;   // K/V rows per math group held in registers (phases ahead)
 constexpr int KV_SPLIT = MG * NKV;   // positions per attention split covered by registers
 constexpr int APW = 264;      // LL words per attention partial: acc[2][128], m0, l0, m1, l1, pad
 constexpr float EPS = 1e-6f;
@@ -115,7 +117,7 @@ enum TraceSlot {
   T_A_START = 0, T_A_PUB, T_A_POLL, T_B_START, T_B_PUB, T_B_POLL, T_C_START, T_C_PUB, T_C_XPOLL, T_C_LPOLL,
   T_D_START, T_D_PUB, T_D_POLL, T_E_START, T_E_PUB, T_E_XPOLL, T_E_LPOLL,
   T_M_A_END, T_M_B_START, T_M_B_END,  // stamped by math wave 1
-  T_B_MAX, T_B_SUM, T_M_A_DOT, T_M_D_ISSUED, T_M_D_DOT, T_SLOTS
+  T_B_MAX, T_B_SUM, T_M_A_DOT, T_M_D_ISSUED, T_M_D_DOT, T_M_B_ISSUED, T_M_B_ATT, T_SLOTS
 };
 constexpr int TRACE_LAYERS = 64;
 constexpr int TRACE_PER_LAYER = 32;
@@ -157,9 +159,9 @@ __device__ __forceinline__ void ll_st2(const Comm& c, u64* base, int off, float 
 }
 
 // Polls NL 16-byte pairs of LL words at word offsets off[k] from base (device-scope loads) until
-// every epoch equals ep; returns the 2*NL values. Two rounds of loads are kept in flight, so a
-// value that lands while one round is out is seen by the next one instead of a full round trip
-// later. Lanes with active == false are always ready. Bounded: on timeout sets the status word
+// every epoch equals ep; returns the 2*NL values. Up to NL = 8, two rounds of loads are kept in
+// flight, so a value that lands while one round is out is seen by the next one instead of a full
+// round trip later. Lanes with active == false are always ready. Bounded: on timeout sets the status word
 // and returns zeros.
 template <int NL>
 __device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&off)[NL], bool active, uint32_t ep,
@@ -183,18 +185,31 @@ __device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&of
 #pragma unroll
     for (int k = 0; k < NL; ++k) { v[2 * k] = __uint_as_float(r[k][0]); v[2 * k + 1] = __uint_as_float(r[k][2]); }
   };
-  u4v r0[NL], r1[NL];
-  issue(r0);
-  for (uint32_t it = 0;; it += 2) {
-    issue(r1);
-    if (ready(r0)) { take(r0); return; }
-    issue(r0);
-    if (ready(r1)) { take(r1); return; }
-    if ((it & 62u) == 62u && ld_dev_u32(c.status) != 0) { c.failed = true; return; }
+  auto check = [&](uint32_t it) {
+    if ((it & 62u) == 62u && ld_dev_u32(c.status) != 0) { c.failed = true; return true; }
     if (it > SPIN_LIMIT) {
       if ((threadIdx.x & 63) == 0) st_dev_u32(c.status, ERR_TIMEOUT);
       c.failed = true;
-      return;
+      return true;
+    }
+    return false;
+  };
+  if constexpr (NL <= 8) {
+    u4v r0[NL], r1[NL];
+    issue(r0);
+    for (uint32_t it = 0;; it += 2) {
+      issue(r1);
+      if (ready(r0)) { take(r0); return; }
+      issue(r0);
+      if (ready(r1)) { take(r1); return; }
+      if (check(it)) return;
+    }
+  } else {  // large polls keep one round in flight (register budget)
+    u4v r0[NL];
+    for (uint32_t it = 0;; it += 2) {
+      issue(r0);
+      if (ready(r0)) { take(r0); return; }
+      if (check(it)) return;
     }
   }
 }
@@ -425,15 +440,15 @@ struct Geo {
   static constexpr bool SMALL = H <= 1024;
   // phase tiles: A = QKV rows, C = o_proj partial, D = gate/up rows, E = down_proj partial; the
   // last argument caps the steps held in registers ahead (the larger shape streams the rest)
-  typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 2> TA;
-  typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 2> TC;
-  typedef Tile<2 * IPW, H, 64, SMALL ? 8 : 2> TD;
+  typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 1> TA;
+  typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 1> TC;
+  typedef Tile<2 * IPW, H, 64, SMALL ? 8 : 1> TD;
   typedef Tile<HPW, IX, 16, SMALL ? 8 : 1> TE;
   static constexpr int XN = (H > IX ? H : IX);
   static constexpr int UMAX = 2 * IPW > HPW ? 2 * IPW : HPW;
   static constexpr int NSLOT = 2 * H + 2 * D;   // bf16 norm weights per layer: input, post-attention, q, k
   static constexpr int NSL16 = NSLOT / 8;       // ... in 16-byte chunks
-  static constexpr int NSL_L = (NSL16 + 63) / 64;
+  static constexpr int NSL_L = (NSL16 + 64 * NMW - 1) / (64 * NMW);  // chunks per math lane
   static constexpr int IXL = IX / 64;           // MLP words per comm lane
   static_assert(HPW * WPX == H && IPW * WPX == IX && IX * NXCD == I, "shape must split evenly");
   static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64 && IXL % 2 == 0, "unsupported shape");
@@ -449,7 +464,7 @@ struct Smem {
   uint16_t kvn[2][D];                // new K (normed, rotated) and V, bf16
   float cs[2][D];                    // cos, sin at position
   uint16_t nw[2][Geo<H, I>::NSLOT];  // per-layer norm weights by layer parity
-  float gp[NMW][2][D + 4];           // attention partials of the 7 math waves: acc[128], m, l
+  float gp[NMW][2][D + 4];           // attention partials of the math waves: acc[128], m, l
   u64 best[NMW];
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
 };
@@ -600,7 +615,11 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
   using I4 = std::integral_constant<int, 4>;
-  constexpr bool AFTER = DIST == 5;
+#ifndef MK_ISSUE_AFTER
+#define MK_ISSUE_AFTER 0
+#endif
+  // issue after the phase's own compute instead of before it (required for DIST == 5)
+  constexpr bool AFTER = DIST == 5 || (DIST > 0 && MK_ISSUE_AFTER);
   if constexpr (DIST > 0) load_phase(I0(), 0);
   if constexpr (DIST > 1) load_phase(I1(), 0);
   if constexpr (DIST > 2) load_phase(I2(), 0);
@@ -617,9 +636,11 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (!AFTER) issue_ahead(I0(), layer);
     tile_consume<TA>(wA, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_A(lw), [&]() { mark(a, tl + T_M_A_DOT, 64); });
     if constexpr (AFTER) issue_ahead(I0(), layer);
-    if (wave == 1) {
+    {
+      // the next layer's norm weights (or the final norm), one chunk per math lane
+      const int q0 = mw * 64 + lane;
 #pragma unroll
-      for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, lane + 64 * k));
+      for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, q0 + 64 * NMW * k));
     }
     mark(a, tl + T_M_A_END, 64);
     lds_barrier();  // (A1)
@@ -628,6 +649,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
 
     // B: split-K attention
     if constexpr (!AFTER) issue_ahead(I1(), layer);
+    mark(a, tl + T_M_B_ISSUED, 64);
     if (st.att_wg) {
       float qa[8], qb[8];
 #pragma unroll
@@ -638,7 +660,9 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
       float a0[8], a1[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
-      auto attend = [&](uint4 kw, uint4 vw) {
+      // scores of both query heads of the group against one key row, then the online-softmax update
+      // (the first key of a group initialises m, l, acc directly)
+      auto attend = [&](uint4 kw, uint4 vw, bool first) {
         float kf[8], vf[8];
         unpack8(kw, kf);
         unpack8(vw, vf);
@@ -647,19 +671,25 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
         d0 = row16_sum(d0) * ATT_SCALE;
         d1 = row16_sum(d1) * ATT_SCALE;
-        softmax_step(d0, vf, m0, l0, a0);
-        softmax_step(d1, vf, m1, l1, a1);
+        if (first) {
+          m0 = d0; m1 = d1; l0 = 1.f; l1 = 1.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) { a0[i] = vf[i]; a1[i] = vf[i]; }
+        } else {
+          softmax_step(d0, vf, m0, l0, a0);
+          softmax_step(d1, vf, m1, l1, a1);
+        }
       };
 #pragma unroll
       for (int r = 0; r < NKV; ++r) {
         const int p = st.p0 + g + MG * r;
-        if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r]);
+        if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r], r == 0);
       }
       // positions beyond the register-held ones (long contexts) stream here
       for (int p = st.p0 + g + MG * NKV; p < st.p1; p += MG) {
         const uint4 kw = p == st.position ? knew : ld_global16(kv_row(a.k_cache, layer, p));
         const uint4 vw = p == st.position ? vnew : ld_global16(kv_row(a.v_cache, layer, p));
-        attend(kw, vw);
+        attend(kw, vw, false);
       }
       // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
       // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
@@ -671,6 +701,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         for (int i = 0; i < 8; ++i) acc[i] = xsum32(xsum16(acc[i] * f));
         m = M;
       };
+      mark(a, tl + T_M_B_ATT, 64);
       merge_rows(m0, l0, a0);
       merge_rows(m1, l1, a1);
       if (lane < 16) {
@@ -706,12 +737,13 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (!AFTER) issue_ahead(I4(), layer);
     tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
     if constexpr (AFTER) issue_ahead(I4(), layer);
-    if (wave == 1) {
+    {
       // the next layer's norm weights (or the final norm) into the other LDS slot
       uint4* dst = reinterpret_cast<uint4*>(sm.nw[(layer + 1) & 1]);
+      const int q0 = mw * 64 + lane;
 #pragma unroll
       for (int k = 0; k < G::NSL_L; ++k)
-        if (lane + 64 * k < G::NSL16) dst[lane + 64 * k] = nsl[k];
+        if (q0 + 64 * NMW * k < G::NSL16) dst[q0 + 64 * NMW * k] = nsl[k];
     }
     lds_barrier();  // (E1)
     lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
@@ -721,7 +753,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // x LCPL chunks), LP rows in flight per wave; fused greedy argmax
   {
     constexpr int LCPL = H / 512;
-    constexpr int LP = 4;
+    constexpr int LP = H <= 1024 ? 4 : 2;  // rows in flight per wave (register budget)
     const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
     const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
     const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
@@ -859,7 +891,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       const int h = lane >> 5, d0 = (lane & 31) * 4;
       u64* att_x = xw + X_ATT + (size_t)xcd * WPX * APW;
       if (st.att_wg) {
-        // merge the 7 wave partials of this split: lane -> head h, dims d0 .. d0+3. A wave without
+        // merge the math waves' partials of this split: lane -> head h, dims d0 .. d0+3. A wave without
         // keys has m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0.
         float mq[NMW];
 #pragma unroll
@@ -1163,4 +1195,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.3 (gfx950; LL exchanges, layer-ahead weight registers)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.4 (gfx950; LL exchanges, 8 math waves, phase-ahead weight prefetch)"; }

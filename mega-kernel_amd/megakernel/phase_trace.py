@@ -27,7 +27,7 @@ SLOTS = ("A start", "A pub (qkv)", "A poll (qkv)", "B start", "B pub (partial)",
          "C start", "C pub", "C cross poll", "C local poll", "D start", "D pub (mlp)", "D poll (mlp)",
          "E start", "E pub", "E cross poll", "E local poll", "math A end", "math B start", "math B end",
          "B merge max", "B merge sum", "math A dot done",
-         "math D issued", "math D dot done")
+         "math D issued", "math D dot done", "math B issued", "math B scores done")
 
 
 def phase_bytes(hidden, inter, ctx):

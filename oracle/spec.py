@@ -71,6 +71,7 @@ SHAPES = {
     "tiny": Shape("tiny", 64, 192, 2, 4, 2, 16, 512),
     # the kernel's fixed head geometry (16 q / 8 kv heads of 128) with few layers and a small vocab
     "mini": Shape("mini", 1024, 3072, 2, 16, 8, 128, 4096),
+    "mini-1.7b": Shape("mini-1.7b", 2048, 6144, 2, 16, 8, 128, 4096),
 }
 
 WEIGHT_SEED = 0   # torch.manual_seed before constructing the model

@@ -65,6 +65,11 @@ def mini():
 
 
 @pytest.fixture(scope="module")
+def mini17():
+    return Session("mini-1.7b", 512)
+
+
+@pytest.fixture(scope="module")
 def q06():
     return Session("qwen3-0.6b", 512)
 
@@ -102,6 +107,25 @@ def test_mini_matches_fp32_restatement(mini):
         assert dk <= 2 ** -6 * max(1.0, kc[:, :, pos].float().abs().max().item()), dk
     # positions beyond the decoded range are untouched
     assert kd[:, :, P + steps:].abs().sum().item() == 0
+
+
+def test_mini_1_7b_shape_matches_fp32_restatement(mini17):
+    """The (2048, 6144) instantiation (the Qwen3-1.7B layer shape, 2 layers, small vocabulary)
+    against the fp32 restatement, including a context long enough for several attention splits."""
+    P, steps = 100, 4
+    ids, last, cache, kc, vc = mini17.prefill(P)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    tok = int(last.float().argmax())
+    for t in range(steps):
+        pos = P + t
+        print(f"[mini-1.7b] step {t} pos {pos} token {tok}", flush=True)
+        logits, dev_tok = mini17.decode(tok, kd, vd, pos, greedy=True)
+        want, _ = restate.decode_step(mini17.W, kc, vc, tok, pos, mini17.cos_cpu, mini17.sin_cpu, numerics="fp32")
+        got = logits.cpu()
+        maxabs, cos = _stats(got, want)
+        assert maxabs < 5e-3, f"step {t}: max|kernel - restatement| = {maxabs}"
+        assert int(dev_tok.item()) == restate.argmax_bf16(got)
+        tok = int(dev_tok.item())
 
 
 def test_decode_writes_only_its_slot(mini):
