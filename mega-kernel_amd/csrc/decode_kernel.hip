@@ -19,15 +19,18 @@
 // vector-memory completions are counted in issue order per wave, the math waves never poll and the
 // comm wave never prefetches.
 //
-// Exchanges are "LL" words: 64-bit stores of (value bits | epoch << 32), epoch = launch sequence
-// << 6 | layer. A reader polls the words themselves until every epoch matches, so one store and
-// one load carry both data and readiness (no flag, no store-acknowledge wait). Within an XCD the
+// Exchanges are "LL" words: 32-bit stores of a value rounded to 24 bits (sign, exponent and 15
+// stored mantissa bits, relative error <= 2^-16) in bits 8..31 and an 8-bit epoch in bits 0..7,
+// epoch = (launch sequence * 64 + layer) mod 255 + 1. A reader polls the words themselves until
+// every epoch matches, so one store and one load carry both data and readiness (no flag, no
+// store-acknowledge wait), and a poll moves no more bytes than the fp32 values would. Within an XCD the
 // words live in that XCD's L2 (plain stores, device-scope loads); across XCDs they are written
 // through to memory (device-scope stores). Cross-XCD partial sums go in two hops: workgroup j of
 // each XCD gathers row block j from the 8 XCDs, sums it in XCD order and republishes it inside its
 // own XCD; then every workgroup reads the whole vector from its L2. Every buffer is written once
-// per layer and read before any writer can reach the next layer's write, and epochs differ per
-// layer and launch, so no buffer needs clearing.
+// per layer and read before any writer can reach the next layer's write; consecutive writes of a
+// word carry epochs 1 to 64 apart (never 0 mod 255), so no buffer needs clearing. Each model shape
+// has its own workspace, so that every word of it is written by every layer of every launch.
 //
 // Numerics follow the reference kernel's fp32 design: bf16 weights and cache, fp32 activations and
 // accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to bf16 as stored. Logits are fp32;
@@ -77,23 +80,27 @@ constexpr int PF_DIST = MK_PF_DIST;  // phases of weights each math lane keeps i
 static_assert(PF_DIST >= 0 && PF_DIST <= 5, "prefetch distance");
 constexpr int MAX_LAYERS = 62;  // epoch = seq << 6 | layer; 63 marks the final exchange
 
-// Exchange workspace, in 64-bit words. Every region starts on a 256-byte boundary; a cross-XCD
-// slot (one writer) is at least 256 bytes, so no cache line has writers on two XCDs.
+// Exchange workspace of one model shape. LL regions in 32-bit words (W_*), then the done flags,
+// status and sequence in 64-bit words (X_*). Every region and every XCD's part of a region starts
+// on a 256-byte boundary, and a cross-XCD slot (one writer) is 256 bytes, so no cache line has
+// writers on two XCDs.
 constexpr int MAX_H = 2048, MAX_I = 6144, MAX_IX = MAX_I / NXCD, MAX_HPW = MAX_H / WPX;
-constexpr size_t X_QKV = 0;                                     // [8][512]
-constexpr size_t X_ATT = X_QKV + NXCD * QKV_X;                  // [8][32][APW]
-constexpr size_t X_M = X_ATT + (size_t)NXCD * WPX * APW;        // [8][MAX_IX]
-constexpr size_t X_OL = X_M + (size_t)NXCD * MAX_IX;            // [8][MAX_H]
-constexpr size_t X_EL = X_OL + (size_t)NXCD * MAX_H;            // [8][MAX_H]
-constexpr size_t X_OX = X_EL + (size_t)NXCD * MAX_H;            // [32][8][MAX_HPW]
-constexpr size_t X_EX = X_OX + (size_t)WPX * NXCD * MAX_HPW;    // [32][8][MAX_HPW]
-constexpr size_t X_DONE = X_EX + (size_t)WPX * NXCD * MAX_HPW;  // [256][16]: key word, flag word
+constexpr size_t W_QKV = 0;                                     // [8][512]
+constexpr size_t W_ATT = W_QKV + NXCD * QKV_X;                  // [8][32][APW]
+constexpr size_t W_M = W_ATT + (size_t)NXCD * WPX * APW;        // [8][MAX_IX]
+constexpr size_t W_OL = W_M + (size_t)NXCD * MAX_IX;            // [8][MAX_H]
+constexpr size_t W_EL = W_OL + (size_t)NXCD * MAX_H;            // [8][MAX_H]
+constexpr size_t W_OX = W_EL + (size_t)NXCD * MAX_H;            // [32][8][MAX_HPW]
+constexpr size_t W_EX = W_OX + (size_t)WPX * NXCD * MAX_HPW;    // [32][8][MAX_HPW]
+constexpr size_t W_END = W_EX + (size_t)WPX * NXCD * MAX_HPW;
+constexpr size_t X_DONE = W_END / 2;                            // [256][16]: key word, flag word
 constexpr size_t X_STATUS = X_DONE + (size_t)NWG * 16;          // u32 status in its own line
 constexpr size_t X_SEQ = X_STATUS + 32;                         // u32 launch sequence in its own line
 constexpr size_t X_WORDS = X_SEQ + 32;
 constexpr size_t WS_BYTES = X_WORDS * 8;
-static_assert(X_ATT % 32 == 0 && X_M % 32 == 0 && X_OL % 32 == 0 && X_OX % 32 == 0 && X_DONE % 32 == 0,
-              "exchange regions must be 256-byte aligned");
+static_assert(W_ATT % 64 == 0 && W_M % 64 == 0 && W_OL % 64 == 0 && W_EL % 64 == 0 && W_OX % 64 == 0 &&
+              W_EX % 64 == 0 && W_END % 64 == 0 && (WPX * APW) % 64 == 0 && MAX_IX % 64 == 0 &&
+              MAX_HPW % 64 == 0, "exchange regions must be 256-byte aligned");
 
 struct KArgs {
   const uint16_t* embed;
@@ -137,7 +144,18 @@ __device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
   v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
 }
 
-__device__ __forceinline__ u64 ll_word(float v, uint32_t ep) { return ((u64)ep << 32) | __float_as_uint(v); }
+// LL word of value v: v rounded to nearest (ties away from zero) at mantissa bit 8, epoch ep in
+// [1, 255] in the low byte.
+__device__ __forceinline__ uint32_t ll_word(float v, uint32_t ep) {
+  return ((__float_as_uint(v) + 0x80u) & 0xFFFFFF00u) | ep;
+}
+__device__ __forceinline__ float ll_value(uint32_t w) { return __uint_as_float(w & 0xFFFFFF00u); }
+// Epoch of a layer's exchanges: nonzero, and 1 to 64 apart (never 0 mod 255) between consecutive
+// writes of one word, which are one layer apart or the last layer of one launch and the first of
+// the next.
+__device__ __forceinline__ uint32_t ll_epoch(uint32_t seq, int layer) {
+  return ((seq % 255u) * 64u + (uint32_t)layer) % 255u + 1u;
+}
 
 struct Comm {
   uint32_t* status;
@@ -145,45 +163,67 @@ struct Comm {
   bool wt = false;  // write local exchanges through to memory (fallback when placement is unknown)
 };
 
-// One LL word. Cross-XCD words are written through (device scope); local words stay in L2.
-__device__ __forceinline__ void ll_st(const Comm& c, u64* p, u64 w, bool cross) {
-  if (cross || c.wt) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-// Two consecutive LL words at word offset `off` (even) from a wave-uniform base, in one 16-byte
-// store; each 8-byte half is single-copy atomic.
-__device__ __forceinline__ void ll_st2(const Comm& c, u64* base, int off, float v0, float v1, uint32_t ep, bool cross) {
-  const u4v w = {__float_as_uint(v0), ep, __float_as_uint(v1), ep};
-  if (cross || c.wt) __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), off * 8, 0, CPOL_SC1);
-  else __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), off * 8, 0, 0);
+// W (1, 2 or 4) consecutive LL words at word offset off (a multiple of W) from a wave-uniform
+// base, in one store; each 4-byte word is single-copy atomic. Cross-XCD words are written through
+// (device scope); local words stay in the XCD's L2.
+template <int W>
+__device__ __forceinline__ void ll_store(const Comm& c, uint32_t* base, int off, const float* v, uint32_t ep,
+                                         bool cross) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
+  const bool wt = cross || c.wt;
+  if constexpr (W == 1) {
+    const uint32_t w = ll_word(v[0], ep);
+    if (wt) __builtin_amdgcn_raw_buffer_store_b32(w, rs, off * 4, 0, CPOL_SC1);
+    else __builtin_amdgcn_raw_buffer_store_b32(w, rs, off * 4, 0, 0);
+  } else if constexpr (W == 2) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    const u2v w = {ll_word(v[0], ep), ll_word(v[1], ep)};
+    if (wt) __builtin_amdgcn_raw_buffer_store_b64(w, rs, off * 4, 0, CPOL_SC1);
+    else __builtin_amdgcn_raw_buffer_store_b64(w, rs, off * 4, 0, 0);
+  } else {
+    static_assert(W == 4, "LL store width");
+    const u4v w = {ll_word(v[0], ep), ll_word(v[1], ep), ll_word(v[2], ep), ll_word(v[3], ep)};
+    if (wt) __builtin_amdgcn_raw_buffer_store_b128(w, rs, off * 4, 0, CPOL_SC1);
+    else __builtin_amdgcn_raw_buffer_store_b128(w, rs, off * 4, 0, 0);
+  }
 }
 
-// Polls NL 16-byte pairs of LL words at word offsets off[k] from base (device-scope loads) until
-// every epoch equals ep; returns the 2*NL values. Up to NL = 8, two rounds of loads are kept in
-// flight, so a value that lands while one round is out is seen by the next one instead of a full
-// round trip later. Lanes with active == false are always ready. Bounded: on timeout sets the status word
-// and returns zeros.
-template <int NL>
-__device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&off)[NL], bool active, uint32_t ep,
-                                        float (&v)[2 * NL]) {
+// Polls NL loads of W (2 or 4) LL words at word offsets off[k] from base (device-scope loads)
+// until every epoch equals ep; returns the W*NL values. Up to TWO_MAX words per lane, two rounds
+// of loads are kept in flight, so a value that lands while one round is out is seen by the next
+// one instead of a full round trip later. Bounded: on timeout sets the status word and returns
+// zeros.
+template <int NL, int W, int TWO_MAX = 32>
+__device__ __forceinline__ void ll_poll(Comm& c, const uint32_t* base, const int (&off)[NL], uint32_t ep,
+                                        float (&v)[W * NL]) {
+  static_assert(W == 2 || W == 4, "LL poll width");
+  typedef unsigned uwv __attribute__((ext_vector_type(W)));
 #pragma unroll
-  for (int k = 0; k < 2 * NL; ++k) v[k] = 0.f;
+  for (int k = 0; k < W * NL; ++k) v[k] = 0.f;
   if (c.failed) return;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
-  auto issue = [&](u4v (&r)[NL]) {
+  auto issue = [&](uwv (&r)[NL]) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      if constexpr (W == 4)
+        r[k] = __builtin_bit_cast(uwv, __builtin_amdgcn_raw_buffer_load_b128(rs, off[k] * 4, 0, CPOL_SC1));
+      else
+        r[k] = __builtin_bit_cast(uwv, __builtin_amdgcn_raw_buffer_load_b64(rs, off[k] * 4, 0, CPOL_SC1));
+    }
+  };
+  auto ready = [&](const uwv (&r)[NL]) {
+    uint32_t bad = 0;
 #pragma unroll
     for (int k = 0; k < NL; ++k)
-      r[k] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, active ? off[k] * 8 : 0, 0, CPOL_SC1));
-  };
-  auto ready = [&](const u4v (&r)[NL]) {
-    bool ok = true;
 #pragma unroll
-    for (int k = 0; k < NL; ++k) ok &= (r[k][1] == ep) & (r[k][3] == ep);
-    return __ballot(!(ok | !active)) == 0;
+      for (int i = 0; i < W; ++i) bad |= (r[k][i] ^ ep) & 0xFFu;
+    return __ballot(bad != 0) == 0;
   };
-  auto take = [&](const u4v (&r)[NL]) {
+  auto take = [&](const uwv (&r)[NL]) {
 #pragma unroll
-    for (int k = 0; k < NL; ++k) { v[2 * k] = __uint_as_float(r[k][0]); v[2 * k + 1] = __uint_as_float(r[k][2]); }
+    for (int k = 0; k < NL; ++k)
+#pragma unroll
+      for (int i = 0; i < W; ++i) v[W * k + i] = ll_value(r[k][i]);
   };
   auto check = [&](uint32_t it) {
     if ((it & 62u) == 62u && ld_dev_u32(c.status) != 0) { c.failed = true; return true; }
@@ -194,8 +234,8 @@ __device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&of
     }
     return false;
   };
-  if constexpr (NL <= 8) {
-    u4v r0[NL], r1[NL];
+  if constexpr (NL * W <= TWO_MAX) {
+    uwv r0[NL], r1[NL];
     issue(r0);
     for (uint32_t it = 0;; it += 2) {
       issue(r1);
@@ -205,7 +245,7 @@ __device__ __forceinline__ void ll_poll(Comm& c, const u64* base, const int (&of
       if (check(it)) return;
     }
   } else {  // large polls keep one round in flight (register budget)
-    u4v r0[NL];
+    uwv r0[NL];
     for (uint32_t it = 0;; it += 2) {
       issue(r0);
       if (ready(r0)) { take(r0); return; }
@@ -266,23 +306,24 @@ __device__ __forceinline__ void comm_norm(const float (&res)[H / 64], const uint
 }
 
 // Cross-XCD partial sum of one row block, then republish inside the XCD, then read the whole
-// vector and add it to the residual. xs: this workgroup's HPW row partials (lanes < HPW hold one
-// each). Block j is rows [HPW*j, HPW*j + HPW).
+// vector and add it to the residual. mine: this workgroup's partial of row HPW*j + lane (lanes <
+// HPW). Block j is rows [HPW*j, HPW*j + HPW).
 template <int H>
-__device__ __forceinline__ void comm_cross_reduce(Comm& c, u64* xw, size_t xbase, size_t lbase, int xcd, int j,
+__device__ __forceinline__ void comm_cross_reduce(Comm& c, uint32_t* xl, size_t xbase, size_t lbase, int xcd, int j,
                                                   float mine, uint32_t ep, float (&res)[H / 64], const KArgs& a,
                                                   int tslot_x, int tslot_l) {
   constexpr int HPW = H / WPX, RPL = HPW / 8, E = H / 64;
+  static_assert(RPL % 4 == 0 && E % 4 == 0, "LL widths");
   const int lane = threadIdx.x & 63;
   // hop 1: my partial of block j -> slot (j, xcd); written through
-  if (lane < HPW) ll_st(c, xw + xbase + ((size_t)j * NXCD + xcd) * MAX_HPW + lane, ll_word(mine, ep), true);
+  if (lane < HPW) ll_store<1>(c, xl + xbase, (j * NXCD + xcd) * MAX_HPW + lane, &mine, ep, true);
   // gather block j from the 8 XCDs: lane -> XCD y = lane / 8, rows RPL*(lane % 8) ..
   const int y = lane >> 3, r0 = RPL * (lane & 7);
-  int off[RPL / 2];
+  int off[RPL / 4];
 #pragma unroll
-  for (int k = 0; k < RPL / 2; ++k) off[k] = (int)(((size_t)j * NXCD + y) * MAX_HPW + r0 + 2 * k);
+  for (int k = 0; k < RPL / 4; ++k) off[k] = (j * NXCD + y) * MAX_HPW + r0 + 4 * k;
   float v[RPL];
-  ll_poll<RPL / 2>(c, xw + xbase, off, true, ep, v);
+  ll_poll<RPL / 4, 4>(c, xl + xbase, off, ep, v);
   mark(a, tslot_x);
   // sum over y in a fixed tree (lanes l, l^8, l^16, l^32 hold the same rows for different y)
 #pragma unroll
@@ -293,13 +334,13 @@ __device__ __forceinline__ void comm_cross_reduce(Comm& c, u64* xw, size_t xbase
   // hop 2: republish block j inside this XCD
   if (lane < 8) {
 #pragma unroll
-    for (int k = 0; k < RPL; k += 2) ll_st2(c, xw + lbase, xcd * MAX_H + HPW * j + r0 + k, v[k], v[k + 1], ep, false);
+    for (int k = 0; k < RPL; k += 4) ll_store<4>(c, xl + lbase, xcd * MAX_H + HPW * j + r0 + k, v + k, ep, false);
   }
-  int offl[E / 2];
+  int offl[E / 4];
 #pragma unroll
-  for (int k = 0; k < E / 2; ++k) offl[k] = (int)((size_t)xcd * MAX_H + E * lane + 2 * k);
+  for (int k = 0; k < E / 4; ++k) offl[k] = xcd * MAX_H + E * lane + 4 * k;
   float d[E];
-  ll_poll<E / 2>(c, xw + lbase, offl, true, ep, d);
+  ll_poll<E / 4, 4, (H <= 1024 ? 32 : 16)>(c, xl + lbase, offl, ep, d);
   mark(a, tslot_l);
 #pragma unroll
   for (int k = 0; k < E; ++k) res[k] += d[k];
@@ -516,6 +557,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   const int g = mw * 4 + (lane >> 4);  // 16-lane group (attention: one key row per group)
   const int t = lane & 15;
   const int xcd = st.xcd, j = st.j, L = st.L;
+  const bool att = __builtin_amdgcn_readfirstlane((int)st.att_wg) != 0;  // workgroup-uniform branch
 
   // tile row r -> first 16-byte chunk of that row's columns
   auto rows_A = [&](const mk_layer_weights& lw) {
@@ -603,27 +645,46 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, rows_D(lw));
     if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, rows_E(lw));
   };
-  // at the start of phase P (DIST < 5) or after its consumption (DIST == 5)
+#ifndef MK_D_AT
+#define MK_D_AT -1
+#endif
+  // gate/up weights: -1 = on the DIST schedule; 4 = at the start of the previous layer's E;
+  // 2 = in C after C1
+  constexpr int D_AT = MK_D_AT;
+  // at the start of phase P (DIST < 5) or after its consumption (DIST == 5). The K/V rows of layer
+  // l + 1 are not on this schedule: phase C of layer l issues them (after its own loads), four
+  // phases ahead, so that at B they wait on nothing newer than themselves but the A weights.
   auto issue_ahead = [&](auto pc, int layer) {
     constexpr int P = decltype(pc)::value;
     constexpr int Q = P + DIST;
-    if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
-    else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
+    if constexpr (Q % 5 != 1 && !(Q % 5 == 3 && D_AT >= 0)) {
+      if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
+      else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
+    }
+    if constexpr (P == 2) load_phase(std::integral_constant<int, 1>(), layer + 1);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
   using I4 = std::integral_constant<int, 4>;
-#ifndef MK_ISSUE_AFTER
-#define MK_ISSUE_AFTER 0
+#ifndef MK_ISSUE_MID
+#define MK_ISSUE_MID 0
 #endif
-  // issue after the phase's own compute instead of before it (required for DIST == 5)
-  constexpr bool AFTER = DIST == 5 || (DIST > 0 && MK_ISSUE_AFTER);
+  // MID: a phase issues its loads after handing its results to the comm wave (between the phase's
+  // two barriers, while the comm wave exchanges), not before its own compute; required for
+  // DIST == 5, where a phase reloads its own registers
+  constexpr bool MID = DIST == 5 || MK_ISSUE_MID;
+  auto load_norms = [&](int layer) {
+    // the next layer's norm weights (or the final norm), one chunk per math lane
+    const int q0 = mw * 64 + lane;
+#pragma unroll
+    for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, q0 + 64 * NMW * k));
+  };
   if constexpr (DIST > 0) load_phase(I0(), 0);
-  if constexpr (DIST > 1) load_phase(I1(), 0);
+  load_phase(I1(), 0);
   if constexpr (DIST > 2) load_phase(I2(), 0);
-  if constexpr (DIST > 3) load_phase(I3(), 0);
+  if constexpr ((DIST > 3 && D_AT < 0) || D_AT == 4) load_phase(I3(), 0);
   if constexpr (DIST > 4) load_phase(I4(), 0);
   lds_barrier();  // (P1) norm weights of layer 0 in LDS
   lds_barrier();  // (P2) comm: x = RMSNorm(embedding)
@@ -633,24 +694,16 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
 
     // A: QKV rows
-    if constexpr (!AFTER) issue_ahead(I0(), layer);
+    if constexpr (!MID) { issue_ahead(I0(), layer); load_norms(layer); }
     tile_consume<TA>(wA, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_A(lw), [&]() { mark(a, tl + T_M_A_DOT, 64); });
-    if constexpr (AFTER) issue_ahead(I0(), layer);
-    {
-      // the next layer's norm weights (or the final norm), one chunk per math lane
-      const int q0 = mw * 64 + lane;
-#pragma unroll
-      for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, q0 + 64 * NMW * k));
-    }
     mark(a, tl + T_M_A_END, 64);
     lds_barrier();  // (A1)
+    if constexpr (MID) { issue_ahead(I0(), layer); load_norms(layer); }
     lds_barrier();  // (A2) comm: q, new K/V in LDS
     mark(a, tl + T_M_B_START, 64);
 
-    // B: split-K attention
-    if constexpr (!AFTER) issue_ahead(I1(), layer);
-    mark(a, tl + T_M_B_ISSUED, 64);
-    if (st.att_wg) {
+    // B: split-K attention; this phase's loads are issued after it, off the attention's path
+    if (att) {
       float qa[8], qb[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) { qa[i] = sm.q[0][8 * t + i]; qb[i] = sm.q[1][8 * t + i]; }
@@ -713,30 +766,36 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         if (t == 0) { sm.gp[mw][0][D] = m0; sm.gp[mw][0][D + 1] = l0; sm.gp[mw][1][D] = m1; sm.gp[mw][1][D + 1] = l1; }
       }
     }
-    if constexpr (AFTER) issue_ahead(I1(), layer);
+    // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
+    // issued only after the comm wave has published this workgroup's attention partial (B3):
+    // neither the attention nor the publish queues behind them.
     mark(a, tl + T_M_B_END, 64);
     lds_barrier();  // (B1)
+    lds_barrier();  // (B3) comm: this split's partial published
+    issue_ahead(I1(), layer);
+    mark(a, tl + T_M_B_ISSUED, 64);
     lds_barrier();  // (B2) comm: attention output in x[0, 256)
 
     // C: o_proj partial over this group's 256 columns
-    if constexpr (!AFTER) issue_ahead(I2(), layer);
+    if constexpr (!MID) issue_ahead(I2(), layer);
     tile_consume<TC>(wC, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_C(lw), NoOp());
-    if constexpr (AFTER) issue_ahead(I2(), layer);
     lds_barrier();  // (C1)
+    if constexpr (MID) issue_ahead(I2(), layer);
+    if constexpr (D_AT == 2) load_phase(I3(), layer);
     lds_barrier();  // (C2) comm: x = RMSNorm(residual) * post-attention norm
 
     // D: gate/up rows of MLP slice x
-    if constexpr (!AFTER) issue_ahead(I3(), layer);
+    if constexpr (!MID) issue_ahead(I3(), layer);
     mark(a, tl + T_M_D_ISSUED, 64);
     tile_consume<TD>(wD, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_D(lw), [&]() { mark(a, tl + T_M_D_DOT, 64); });
-    if constexpr (AFTER) issue_ahead(I3(), layer);
     lds_barrier();  // (D1)
+    if constexpr (MID) issue_ahead(I3(), layer);
     lds_barrier();  // (D2) comm: x[0, IX) = silu(gate) * up of the slice
 
     // E: down_proj partial over slice x's columns
-    if constexpr (!AFTER) issue_ahead(I4(), layer);
+    if constexpr (!MID) issue_ahead(I4(), layer);
+    if constexpr (D_AT == 4) load_phase(I3(), layer + 1);
     tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
-    if constexpr (AFTER) issue_ahead(I4(), layer);
     {
       // the next layer's norm weights (or the final norm) into the other LDS slot
       uint4* dst = reinterpret_cast<uint4*>(sm.nw[(layer + 1) & 1]);
@@ -746,6 +805,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         if (q0 + 64 * NMW * k < G::NSL16) dst[q0 + 64 * NMW * k] = nsl[k];
     }
     lds_barrier();  // (E1)
+    if constexpr (MID) issue_ahead(I4(), layer);
     lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
   }
 
@@ -797,6 +857,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   const int lane = threadIdx.x & 63;
   const int xcd = st.xcd, j = st.j, L = st.L, S = st.S;
   u64* xw = a.xw;
+  uint32_t* xl = reinterpret_cast<uint32_t*>(xw);
   Comm c;
   c.status = reinterpret_cast<uint32_t*>(xw + X_STATUS);
   float res[G::E];
@@ -830,22 +891,22 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   lds_barrier();  // (P2)
 
   for (int layer = 0; layer < L; ++layer) {
-    const uint32_t ep = (seq << 6) | (uint32_t)layer;
+    const uint32_t ep = ll_epoch(seq, layer);
     const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
     const uint16_t* nw = sm.nw[layer & 1];
 
     // ---- A: publish QKV rows; attention workgroups gather q, k, v of the group --------------
     mark(a, tl + T_A_START);
     lds_barrier();  // (A1)
-    if (lane < QKV_WG) ll_st(c, xw + X_QKV + xcd * QKV_X + QKV_WG * j + lane, ll_word(sm.up[lane], ep), false);
+    if (lane < QKV_WG) ll_store<1>(c, xl + W_QKV, xcd * QKV_X + QKV_WG * j + lane, &sm.up[lane], ep, false);
     mark(a, tl + T_A_PUB);
     if (st.att_wg) {
       // lane -> 8 values: q head 2x (lanes 0-15), q head 2x+1 (16-31), k head x (32-47), v (48-63)
-      int off[4];
+      int off[2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) off[k] = xcd * QKV_X + 8 * lane + 2 * k;
+      for (int k = 0; k < 2; ++k) off[k] = xcd * QKV_X + 8 * lane + 4 * k;
       float v[8];
-      ll_poll<4>(c, xw + X_QKV, off, true, ep, v);
+      ll_poll<2, 4>(c, xl + W_QKV, off, ep, v);
       mark(a, tl + T_A_POLL);
       const int tt = lane & 15, part = lane >> 4;
       // per-head RMSNorm (/root/reference/megakernel.cu:490-630): a head is one 16-lane row
@@ -889,10 +950,11 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     lds_barrier();  // (B1)
     {
       const int h = lane >> 5, d0 = (lane & 31) * 4;
-      u64* att_x = xw + X_ATT + (size_t)xcd * WPX * APW;
-      if (st.att_wg) {
+      uint32_t* att_x = xl + W_ATT + (size_t)xcd * WPX * APW;
+      {
         // merge the math waves' partials of this split: lane -> head h, dims d0 .. d0+3. A wave without
-        // keys has m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0.
+        // keys has m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0. Workgroups without a split
+        // publish their (unused) slot too, so that every LL word is written at every layer.
         float mq[NMW];
 #pragma unroll
         for (int q = 0; q < NMW; ++q) mq[q] = sm.gp[q][h][D];
@@ -900,46 +962,49 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
 #pragma unroll
         for (int q = 0; q < NMW; ++q) M = fmaxf(M, mq[q]);
         mark(a, tl + T_B_MAX);
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
         float Ls = 0.f;
 #pragma unroll
         for (int q = 0; q < NMW; ++q) {
           const float f = __expf(mq[q] - M);
           const float4 p = *reinterpret_cast<const float4*>(&sm.gp[q][h][d0]);
-          acc.x = fmaf(p.x, f, acc.x); acc.y = fmaf(p.y, f, acc.y);
-          acc.z = fmaf(p.z, f, acc.z); acc.w = fmaf(p.w, f, acc.w);
+          acc[0] = fmaf(p.x, f, acc[0]); acc[1] = fmaf(p.y, f, acc[1]);
+          acc[2] = fmaf(p.z, f, acc[2]); acc[3] = fmaf(p.w, f, acc[3]);
           Ls = fmaf(sm.gp[q][h][D + 1], f, Ls);
         }
         mark(a, tl + T_B_SUM);
         const int mine = j * APW;
-        ll_st2(c, att_x, mine + h * D + d0, acc.x, acc.y, ep, false);
-        ll_st2(c, att_x, mine + h * D + d0 + 2, acc.z, acc.w, ep, false);
-        if ((lane & 31) == 0) ll_st2(c, att_x, mine + 2 * D + 2 * h, M, Ls, ep, false);
+        const float ml[2] = {M, Ls};
+        ll_store<4>(c, att_x, mine + h * D + d0, acc, ep, false);
+        if ((lane & 31) == 0) ll_store<2>(c, att_x, mine + 2 * D + 2 * h, ml, ep, false);
         mark(a, tl + T_B_PUB);
       }
-      // merge the S split partials of this XCD's two heads -> s_x[0, 256), in split order
+      lds_barrier();  // (B3)
+      // merge the S split partials of this XCD's two heads, in split order; a lane reads its 4
+      // dims and the (m, l) pairs of both heads of each split
       float M = -INFINITY, Ls = 0.f;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int s0 = 0; s0 < S; s0 += 2) {
-        int off[6];
+      constexpr int SB = H <= 1024 ? 4 : 2;  // splits per poll (register budget)
+      for (int s0 = 0; s0 < S; s0 += SB) {
+        int off[2 * SB];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < SB; ++q) {
           const int s = s0 + q < S ? s0 + q : s0;
-          off[3 * q + 0] = s * APW + h * D + d0;
-          off[3 * q + 1] = s * APW + h * D + d0 + 2;
-          off[3 * q + 2] = s * APW + 2 * D + 2 * h;
+          off[2 * q + 0] = s * APW + h * D + d0;
+          off[2 * q + 1] = s * APW + 2 * D;
         }
-        float v[12];
-        ll_poll<6>(c, att_x, off, true, ep, v);
+        float v[8 * SB];
+        ll_poll<2 * SB, 4>(c, att_x, off, ep, v);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < SB; ++q) {
           if (s0 + q < S) {
-            const float ms = v[6 * q + 4], ls = v[6 * q + 5];
+            const float* w = v + 8 * q;
+            const float ms = h ? w[6] : w[4], ls = h ? w[7] : w[5];
             const float n = fmaxf(M, ms);
             const float cm = __expf(M - n), cs = __expf(ms - n);
             Ls = Ls * cm + ls * cs;
-            acc.x = acc.x * cm + v[6 * q + 0] * cs; acc.y = acc.y * cm + v[6 * q + 1] * cs;
-            acc.z = acc.z * cm + v[6 * q + 2] * cs; acc.w = acc.w * cm + v[6 * q + 3] * cs;
+            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
+            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
             M = n;
           }
         }
@@ -957,7 +1022,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     {
       const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
       mark(a, tl + T_C_PUB);
-      comm_cross_reduce<H>(c, xw, X_OX, X_OL, xcd, j, mine, ep, res, a, tl + T_C_XPOLL, tl + T_C_LPOLL);
+      comm_cross_reduce<H>(c, xl, W_OX, W_OL, xcd, j, mine, ep, res, a, tl + T_C_XPOLL, tl + T_C_LPOLL);
       comm_norm<H>(res, nw + H, sm.xh, sm.xl);
     }
     lds_barrier();  // (C2)
@@ -966,17 +1031,20 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     mark(a, tl + T_D_START);
     lds_barrier();  // (D1)
     {
-      u64* m_x = xw + X_M + (size_t)xcd * MAX_IX;
+      uint32_t* m_x = xl + W_M + (size_t)xcd * MAX_IX;
       if (lane < G::IPW) {
         const float gs = sm.up[lane], us = sm.up[lane + G::IPW];
-        ll_st(c, m_x + G::IPW * j + lane, ll_word(gs / (1.f + expf(-gs)) * us, ep), false);  // silu(g) * u
+        const float m = gs / (1.f + expf(-gs)) * us;  // silu(g) * u
+        ll_store<1>(c, m_x, G::IPW * j + lane, &m, ep, false);
       }
       mark(a, tl + T_D_PUB);
-      int off[G::IXL / 2];
+      constexpr int MW = G::IXL % 4 == 0 ? 4 : 2;
+      static_assert(G::IXL % MW == 0, "LL widths");
+      int off[G::IXL / MW];
 #pragma unroll
-      for (int k = 0; k < G::IXL / 2; ++k) off[k] = G::IXL * lane + 2 * k;
+      for (int k = 0; k < G::IXL / MW; ++k) off[k] = G::IXL * lane + MW * k;
       float v[G::IXL];
-      ll_poll<G::IXL / 2>(c, m_x, off, true, ep, v);
+      ll_poll<G::IXL / MW, MW>(c, m_x, off, ep, v);
       mark(a, tl + T_D_POLL);
       store_hilo<G::IXL>(sm.xh, sm.xl, G::IXL * lane, v);
     }
@@ -988,7 +1056,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     {
       const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
       mark(a, tl + T_E_PUB);
-      comm_cross_reduce<H>(c, xw, X_EX, X_EL, xcd, j, mine, ep, res, a, tl + T_E_XPOLL, tl + T_E_LPOLL);
+      comm_cross_reduce<H>(c, xl, W_EX, W_EL, xcd, j, mine, ep, res, a, tl + T_E_XPOLL, tl + T_E_LPOLL);
       comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm, or the final norm
     }
     lds_barrier();  // (E2)
@@ -1064,14 +1132,19 @@ static hipError_t check_kernel_fits() {
   return blocks >= 1 ? hipSuccess : hipErrorCooperativeLaunchTooLarge;
 }
 
-// Zero every exchange word, the status word and start the launch sequence at 1 (epoch 0 never
-// matches).
+// Workspaces per device, one per supported model shape: NSHAPE * WS_BYTES.
+constexpr int NSHAPE = 2;
+
+// Zero every exchange word and status word and start each launch sequence at 1 (a zeroed word
+// has epoch 0, which never matches).
 static hipError_t clear_workspace(void* ws) {
-  hipError_t e = hipMemset(ws, 0, WS_BYTES);
+  hipError_t e = hipMemset(ws, 0, NSHAPE * WS_BYTES);
   if (e != hipSuccess) return e;
   const uint32_t one = 1;
-  e = hipMemcpy((char*)ws + X_SEQ * 8, &one, 4, hipMemcpyHostToDevice);
-  if (e != hipSuccess) return e;
+  for (int i = 0; i < NSHAPE; ++i) {
+    e = hipMemcpy((char*)ws + i * WS_BYTES + X_SEQ * 8, &one, 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+  }
   return hipDeviceSynchronize();
 }
 
@@ -1090,7 +1163,7 @@ static hipError_t device_state(DeviceState** out) {
     if (cus != NWG || !coop) return hipErrorNotSupported;
     if ((e = check_kernel_fits<1024, 3072>()) != hipSuccess) return e;
     if ((e = check_kernel_fits<2048, 6144>()) != hipSuccess) return e;
-    if ((e = hipMalloc(&s.ws, WS_BYTES)) != hipSuccess) return e;
+    if ((e = hipMalloc(&s.ws, NSHAPE * WS_BYTES)) != hipSuccess) return e;
     if ((e = clear_workspace(s.ws)) != hipSuccess) return e;
     s.ok = true;
   }
@@ -1136,7 +1209,7 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.v_cache = (uint16_t*)v_cache;
   k.logits = logits;
   k.out_token = out_token;
-  k.xw = (u64*)st->ws;
+  k.xw = (u64*)((char*)st->ws + (s06 ? 0 : WS_BYTES));
   k.trace = st->trace;
   k.token = token_id;
   k.position = position;
@@ -1168,7 +1241,12 @@ extern "C" hipError_t mk_status(uint32_t* status) {
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  return hipMemcpy(status, (char*)st->ws + X_STATUS * 8, 4, hipMemcpyDeviceToHost);
+  uint32_t w[NSHAPE];
+  for (int i = 0; i < NSHAPE; ++i)
+    if ((e = hipMemcpy(&w[i], (char*)st->ws + i * WS_BYTES + X_STATUS * 8, 4, hipMemcpyDeviceToHost)) != hipSuccess)
+      return e;
+  *status = w[0] | w[1];
+  return hipSuccess;
 }
 
 extern "C" hipError_t mk_reset(void) {
@@ -1195,4 +1273,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.4 (gfx950; LL exchanges, 8 math waves, phase-ahead weight prefetch)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.5 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch)"; }
