@@ -813,7 +813,10 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // x LCPL chunks), LP rows in flight per wave; fused greedy argmax
   {
     constexpr int LCPL = H / 512;
-    constexpr int LP = H <= 1024 ? 4 : 2;  // rows in flight per wave (register budget)
+#ifndef MK_LP
+#define MK_LP 4
+#endif
+    constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
     const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
     const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
     const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
