@@ -543,6 +543,203 @@ __device__ __forceinline__ Step make_step(const KArgs& a) {
   return s;
 }
 
+// Weight and cache addressing of one workgroup, shared by the math waves and the loader wave: the
+// first 16-byte chunk of tile row r of each phase, the K/V row of a position, the norm-weight slots.
+template <int H, int I>
+struct Addr {
+  typedef Geo<H, I> G;
+  const KArgs& a;
+  const Smem<H, I>& sm;
+  const Step& st;
+  struct RowsA {
+    const uint16_t* base;
+    int row0;
+    __device__ const uint4* operator()(int r) const { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * H); }
+  };
+  struct RowsC {
+    const uint16_t* base;
+    int row0, col0;
+    __device__ const uint4* operator()(int r) const {
+      return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * (HQ * D) + col0);
+    }
+  };
+  struct RowsD {
+    const uint16_t* wg;
+    const uint16_t* wu;
+    int row0;
+    __device__ const uint4* operator()(int r) const {
+      return reinterpret_cast<const uint4*>(r < G::IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - G::IPW) * H);
+    }
+  };
+  struct RowsE {
+    const uint16_t* base;
+    int row0, col0;
+    __device__ const uint4* operator()(int r) const { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * I + col0); }
+  };
+  // A: 16 rows of this XCD's q (2 heads), k or v rows; C: o_proj rows x this XCD's 256 columns;
+  // D: gate then up rows of this XCD's MLP slice; E: down_proj rows x the slice's columns
+  __device__ RowsA A(const mk_layer_weights& lw) const {
+    const int j = st.j, xcd = st.xcd;
+    if (j < 16) return {(const uint16_t*)lw.q_weight, 2 * D * xcd + QKV_WG * j};
+    if (j < 24) return {(const uint16_t*)lw.k_weight, D * xcd + QKV_WG * (j - 16)};
+    return {(const uint16_t*)lw.v_weight, D * xcd + QKV_WG * (j - 24)};
+  }
+  __device__ RowsC C(const mk_layer_weights& lw) const {
+    return {(const uint16_t*)lw.o_proj_weight, G::HPW * st.j, 2 * D * st.xcd};
+  }
+  __device__ RowsD Dm(const mk_layer_weights& lw) const {
+    return {(const uint16_t*)lw.gate_proj_weight, (const uint16_t*)lw.up_proj_weight, G::IX * st.xcd + G::IPW * st.j};
+  }
+  __device__ RowsE E(const mk_layer_weights& lw) const {
+    return {(const uint16_t*)lw.down_proj_weight, G::HPW * st.j, G::IX * st.xcd};
+  }
+  // first 16-byte chunk of the K/V row of position p of this XCD's head
+  __device__ const uint4* kv_row(const uint16_t* cache, int layer, int p) const {
+    return reinterpret_cast<const uint4*>(cache + (((size_t)layer * HKV + st.xcd) * a.max_seq + p) * D);
+  }
+  // position math group g attends to from registers, slot r: p0 + g + MG*r; unused slots re-read p0
+  __device__ int kv_pos(int g, int r) const {
+    const int p = st.p0 + g + MG * r;
+    return (p < st.p1 && p != st.position) ? p : st.p0;
+  }
+  // norm-weight slot: chunk q of [input norm | post norm | q norm | k norm] for layer `layer`, or of
+  // the final norm (every piece) when layer == L; q past the end re-reads the last chunk
+  __device__ const uint4* slot_chunk(int layer, int q) const {
+    q = q < G::NSL16 ? q : G::NSL16 - 1;
+    if (layer >= st.L) return reinterpret_cast<const uint4*>(a.final_norm) + (q % (H / 8));
+    const mk_layer_weights& lw = sm.layers[layer];
+    if (q < H / 8) return reinterpret_cast<const uint4*>(lw.norm_weight) + q;
+    if (q < H / 4) return reinterpret_cast<const uint4*>(lw.post_attn_norm_weight) + (q - H / 8);
+    if (q < H / 4 + D / 8) return reinterpret_cast<const uint4*>(lw.q_norm_weight) + (q - H / 4);
+    return reinterpret_cast<const uint4*>(lw.k_norm_weight) + (q - H / 4 - D / 8);
+  }
+};
+
+// Split-K attention of this workgroup's split for one math wave (4 groups of 16 lanes, one key row
+// per group from registers; longer splits stream the rest), merged over the wave's groups into
+// sm.gp[mw]: per head acc[128], m, l. Online softmax per group for both query heads of the GQA pair,
+// so each K/V row is read once (/root/reference/megakernel.cu:228-370).
+template <int H, int I>
+__device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, const Step& st, const Addr<H, I>& ad,
+                                                int layer, int mw, int lane, const uint4 (&kK)[NKV],
+                                                const uint4 (&kV)[NKV], int tl) {
+  const int g = mw * 4 + (lane >> 4), t = lane & 15;
+  float qa[8], qb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { qa[i] = sm.q[0][8 * t + i]; qb[i] = sm.q[1][8 * t + i]; }
+  const uint4 knew = *reinterpret_cast<const uint4*>(&sm.kvn[0][8 * t]);
+  const uint4 vnew = *reinterpret_cast<const uint4*>(&sm.kvn[1][8 * t]);
+  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
+  float a0[8], a1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
+  // scores of both query heads of the group against one key row, then the online-softmax update
+  // (the first key of a group initialises m, l, acc directly)
+  auto attend = [&](uint4 kw, uint4 vw, bool first) {
+    float kf[8], vf[8];
+    unpack8(kw, kf);
+    unpack8(vw, vf);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
+    d0 = row16_sum(d0) * ATT_SCALE;
+    d1 = row16_sum(d1) * ATT_SCALE;
+    if (first) {
+      m0 = d0; m1 = d1; l0 = 1.f; l1 = 1.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { a0[i] = vf[i]; a1[i] = vf[i]; }
+    } else {
+      softmax_step(d0, vf, m0, l0, a0);
+      softmax_step(d1, vf, m1, l1, a1);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < NKV; ++r) {
+    const int p = st.p0 + g + MG * r;
+    if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r], r == 0);
+  }
+  // positions beyond the register-held ones (long contexts) stream here
+  for (int p = st.p0 + g + MG * NKV; p < st.p1; p += MG) {
+    const uint4 kw = p == st.position ? knew : ld_global16(ad.kv_row(a.k_cache, layer, p) + t);
+    const uint4 vw = p == st.position ? vnew : ld_global16(ad.kv_row(a.v_cache, layer, p) + t);
+    attend(kw, vw, false);
+  }
+  // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
+  // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
+  auto merge_rows = [&](float& m, float& l, float (&acc)[8]) {
+    float M = xmax32(xmax16(m));
+    const float f = M == -INFINITY ? 0.f : __expf(m - M);
+    l = xsum32(xsum16(l * f));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = xsum32(xsum16(acc[i] * f));
+    m = M;
+  };
+  mark(a, tl + T_M_B_ATT, 64);
+  merge_rows(m0, l0, a0);
+  merge_rows(m1, l1, a1);
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 4) {
+      *reinterpret_cast<float4*>(&sm.gp[mw][0][8 * t + i]) = make_float4(a0[i], a0[i + 1], a0[i + 2], a0[i + 3]);
+      *reinterpret_cast<float4*>(&sm.gp[mw][1][8 * t + i]) = make_float4(a1[i], a1[i + 1], a1[i + 2], a1[i + 3]);
+    }
+    if (t == 0) { sm.gp[mw][0][D] = m0; sm.gp[mw][0][D + 1] = l0; sm.gp[mw][1][D] = m1; sm.gp[mw][1][D + 1] = l1; }
+  }
+}
+
+// Tied LM head over this workgroup's vocabulary rows [r0, r1): wave mw takes rows r0 + mw + NMW*s,
+// one row per step (64 lanes x LCPL chunks), LP rows in flight per wave; fused greedy argmax key of
+// the wave into sm.best[mw].
+template <int H, int I>
+__device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, int lane) {
+  constexpr int LCPL = H / 512;
+#ifndef MK_LP
+#define MK_LP 4
+#endif
+  constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
+  const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
+  const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
+  const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
+  const int lq = opaque(lane), mwq = opaque(mw);
+  uint4 xh[LCPL], xl[LCPL];
+#pragma unroll
+  for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
+  auto lm_load = [&](int s, uint4 (&b)[LCPL]) {
+    int row = r0 + mwq + NMW * s;
+    row = row < r1 ? row : r1 - 1;  // past the end: re-read the last row (unconditional loads)
+    const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lq;
+#pragma unroll
+    for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
+  };
+  uint4 buf[LP][LCPL];
+#pragma unroll
+  for (int i = 0; i < LP; ++i) lm_load(i, buf[i]);
+  u64 best = 0;
+  for (int s0 = 0; s0 < nmine; s0 += LP) {
+#pragma unroll
+    for (int i = 0; i < LP; ++i) {
+      const float v = wave_sum(dot_chunks<LCPL>(buf[i], xh, xl));
+      const int s = s0 + i;
+      if (s < nmine) {
+        const int row = r0 + mwq + NMW * s;
+        if (lq == 0) gpw(a.logits)[row] = v;
+        best = umax64(best, argmax_key(v, row));
+      }
+      lm_load(s + LP, buf[i]);
+    }
+  }
+  if (lane == 0) sm.best[mw] = best;
+}
+
+// Copies the layer table into LDS (math waves, before the first barrier).
+template <int H, int I>
+__device__ __forceinline__ void copy_layer_table(const KArgs& a, Smem<H, I>& sm) {
+  constexpr int TW = (int)(sizeof(mk_layer_weights) / 8);
+  const int n = a.num_layers * TW;
+  for (int i = threadIdx.x - 64; i < n; i += NT - 64)
+    reinterpret_cast<u64*>(sm.layers)[i] = reinterpret_cast<const u64*>(a.layers)[i];
+}
+
 // ---- math waves ------------------------------------------------------------------------------
 template <int H, int I, int DIST>
 __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const Step& st) {
@@ -559,65 +756,21 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   const int xcd = st.xcd, j = st.j, L = st.L;
   const bool att = __builtin_amdgcn_readfirstlane((int)st.att_wg) != 0;  // workgroup-uniform branch
 
-  // tile row r -> first 16-byte chunk of that row's columns
-  auto rows_A = [&](const mk_layer_weights& lw) {
-    const uint16_t* base;
-    int row0;
-    if (j < 16) { base = (const uint16_t*)lw.q_weight; row0 = 2 * D * xcd + QKV_WG * j; }
-    else if (j < 24) { base = (const uint16_t*)lw.k_weight; row0 = D * xcd + QKV_WG * (j - 16); }
-    else { base = (const uint16_t*)lw.v_weight; row0 = D * xcd + QKV_WG * (j - 24); }
-    return [=](int r) { return reinterpret_cast<const uint4*>(base + (size_t)(row0 + r) * H); };
-  };
-  auto rows_C = [&](const mk_layer_weights& lw) {
-    const uint16_t* wo = (const uint16_t*)lw.o_proj_weight;
-    const int row0 = G::HPW * j;
-    return [=](int r) { return reinterpret_cast<const uint4*>(wo + (size_t)(row0 + r) * (HQ * D) + 2 * D * xcd); };
-  };
-  auto rows_D = [&](const mk_layer_weights& lw) {
-    const uint16_t* wg = (const uint16_t*)lw.gate_proj_weight;
-    const uint16_t* wu = (const uint16_t*)lw.up_proj_weight;
-    const int row0 = G::IX * xcd + G::IPW * j;
-    return [=](int r) {
-      return reinterpret_cast<const uint4*>(r < G::IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - G::IPW) * H);
-    };
-  };
-  auto rows_E = [&](const mk_layer_weights& lw) {
-    const uint16_t* wd = (const uint16_t*)lw.down_proj_weight;
-    const int row0 = G::HPW * j;
-    return [=](int r) { return reinterpret_cast<const uint4*>(wd + (size_t)(row0 + r) * I + G::IX * xcd); };
-  };
-  // K/V row of position p (16 chunks; lane t reads chunk t)
-  auto kv_row = [&](const uint16_t* cache, int layer, int p) {
-    return reinterpret_cast<const uint4*>(cache + (((size_t)layer * HKV + xcd) * a.max_seq + p) * D) + t;
-  };
-  // K/V rows this math group attends to from registers: p0 + g + MG*r; unused slots re-read p0
-  auto kv_pos = [&](int r) {
-    const int p = st.p0 + g + MG * r;
-    return (p < st.p1 && p != st.position) ? p : st.p0;
-  };
-  // norm-weight slot: chunk q of [input norm | post norm | q norm | k norm] for layer `layer`,
-  // or of the final norm (every piece) when layer == L
-  auto slot_chunk = [&](int layer, int q) {
-    q = q < G::NSL16 ? q : G::NSL16 - 1;
-    if (layer >= L) return reinterpret_cast<const uint4*>(a.final_norm) + (q % (H / 8));
-    const mk_layer_weights& lw = sm.layers[layer];
-    if (q < H / 8) return reinterpret_cast<const uint4*>(lw.norm_weight) + q;
-    if (q < H / 4) return reinterpret_cast<const uint4*>(lw.post_attn_norm_weight) + (q - H / 8);
-    if (q < H / 4 + D / 8) return reinterpret_cast<const uint4*>(lw.q_norm_weight) + (q - H / 4);
-    return reinterpret_cast<const uint4*>(lw.k_norm_weight) + (q - H / 4 - D / 8);
-  };
+  const Addr<H, I> ad{a, sm, st};
+  auto rows_A = [&](const mk_layer_weights& lw) { return ad.A(lw); };
+  auto rows_C = [&](const mk_layer_weights& lw) { return ad.C(lw); };
+  auto rows_D = [&](const mk_layer_weights& lw) { return ad.Dm(lw); };
+  auto rows_E = [&](const mk_layer_weights& lw) { return ad.E(lw); };
+  auto kv_row = [&](const uint16_t* cache, int layer, int p) { return ad.kv_row(cache, layer, p) + t; };
+  auto kv_pos = [&](int r) { return ad.kv_pos(g, r); };
+  auto slot_chunk = [&](int layer, int q) { return ad.slot_chunk(layer, q); };
 
   uint4 wA[TA::PS][TA::CPL], wC[TC::PS][TC::CPL], wD[TD::PS][TD::CPL], wE[TE::PS][TE::CPL];
   uint4 kK[NKV], kV[NKV];
   uint4 nsl[G::NSL_L];
 
   // prologue: the layer table into LDS, then layer 0's norm weights (synchronously, wave 1)
-  {
-    constexpr int TW = (int)(sizeof(mk_layer_weights) / 8);
-    const int n = L * TW;
-    for (int i = threadIdx.x - 64; i < n; i += NT - 64)
-      reinterpret_cast<u64*>(sm.layers)[i] = reinterpret_cast<const u64*>(a.layers)[i];
-  }
+  copy_layer_table(a, sm);
   lds_barrier();  // (P0) layer table in LDS
   if (wave == 1)
     for (int q = lane; q < G::NSL16; q += 64) reinterpret_cast<uint4*>(sm.nw[0])[q] = ld_global16(slot_chunk(0, q));
@@ -703,69 +856,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     mark(a, tl + T_M_B_START, 64);
 
     // B: split-K attention; this phase's loads are issued after it, off the attention's path
-    if (att) {
-      float qa[8], qb[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) { qa[i] = sm.q[0][8 * t + i]; qb[i] = sm.q[1][8 * t + i]; }
-      const uint4 knew = *reinterpret_cast<const uint4*>(&sm.kvn[0][8 * t]);
-      const uint4 vnew = *reinterpret_cast<const uint4*>(&sm.kvn[1][8 * t]);
-      float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-      float a0[8], a1[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
-      // scores of both query heads of the group against one key row, then the online-softmax update
-      // (the first key of a group initialises m, l, acc directly)
-      auto attend = [&](uint4 kw, uint4 vw, bool first) {
-        float kf[8], vf[8];
-        unpack8(kw, kf);
-        unpack8(vw, vf);
-        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
-        d0 = row16_sum(d0) * ATT_SCALE;
-        d1 = row16_sum(d1) * ATT_SCALE;
-        if (first) {
-          m0 = d0; m1 = d1; l0 = 1.f; l1 = 1.f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) { a0[i] = vf[i]; a1[i] = vf[i]; }
-        } else {
-          softmax_step(d0, vf, m0, l0, a0);
-          softmax_step(d1, vf, m1, l1, a1);
-        }
-      };
-#pragma unroll
-      for (int r = 0; r < NKV; ++r) {
-        const int p = st.p0 + g + MG * r;
-        if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r], r == 0);
-      }
-      // positions beyond the register-held ones (long contexts) stream here
-      for (int p = st.p0 + g + MG * NKV; p < st.p1; p += MG) {
-        const uint4 kw = p == st.position ? knew : ld_global16(kv_row(a.k_cache, layer, p));
-        const uint4 vw = p == st.position ? vnew : ld_global16(kv_row(a.v_cache, layer, p));
-        attend(kw, vw, false);
-      }
-      // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
-      // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
-      auto merge_rows = [&](float& m, float& l, float (&acc)[8]) {
-        float M = xmax32(xmax16(m));
-        const float f = M == -INFINITY ? 0.f : __expf(m - M);
-        l = xsum32(xsum16(l * f));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = xsum32(xsum16(acc[i] * f));
-        m = M;
-      };
-      mark(a, tl + T_M_B_ATT, 64);
-      merge_rows(m0, l0, a0);
-      merge_rows(m1, l1, a1);
-      if (lane < 16) {
-#pragma unroll
-        for (int i = 0; i < 8; i += 4) {
-          *reinterpret_cast<float4*>(&sm.gp[mw][0][8 * t + i]) = make_float4(a0[i], a0[i + 1], a0[i + 2], a0[i + 3]);
-          *reinterpret_cast<float4*>(&sm.gp[mw][1][8 * t + i]) = make_float4(a1[i], a1[i + 1], a1[i + 2], a1[i + 3]);
-        }
-        if (t == 0) { sm.gp[mw][0][D] = m0; sm.gp[mw][0][D + 1] = l0; sm.gp[mw][1][D] = m1; sm.gp[mw][1][D + 1] = l1; }
-      }
-    }
+    if (att) attention_split<H, I>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
     // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
     // issued only after the comm wave has published this workgroup's attention partial (B3):
     // neither the attention nor the publish queues behind them.
@@ -809,47 +900,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
   }
 
-  // tied LM head over rows [r0, r1): wave mw takes rows r0 + mw + 7*s, one row per step (64 lanes
-  // x LCPL chunks), LP rows in flight per wave; fused greedy argmax
-  {
-    constexpr int LCPL = H / 512;
-#ifndef MK_LP
-#define MK_LP 4
-#endif
-    constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
-    const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
-    const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
-    const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
-    const int lq = opaque(lane), mwq = opaque(mw);
-    uint4 xh[LCPL], xl[LCPL];
-#pragma unroll
-    for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
-    auto lm_load = [&](int s, uint4 (&b)[LCPL]) {
-      int row = r0 + mwq + NMW * s;
-      row = row < r1 ? row : r1 - 1;  // past the end: re-read the last row (unconditional loads)
-      const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lq;
-#pragma unroll
-      for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
-    };
-    uint4 buf[LP][LCPL];
-#pragma unroll
-    for (int i = 0; i < LP; ++i) lm_load(i, buf[i]);
-    u64 best = 0;
-    for (int s0 = 0; s0 < nmine; s0 += LP) {
-#pragma unroll
-      for (int i = 0; i < LP; ++i) {
-        const float v = wave_sum(dot_chunks<LCPL>(buf[i], xh, xl));
-        const int s = s0 + i;
-        if (s < nmine) {
-          const int row = r0 + mwq + NMW * s;
-          if (lq == 0) gpw(a.logits)[row] = v;
-          best = umax64(best, argmax_key(v, row));
-        }
-        lm_load(s + LP, buf[i]);
-      }
-    }
-    if (lane == 0) sm.best[mw] = best;
-  }
+  lm_head<H, I>(a, sm, mw, lane);
   lds_barrier();  // (F) per-wave argmax keys in LDS
 }
 

@@ -168,6 +168,7 @@ int main(int argc, char** argv) {
   CK(hipMemcpy(&htok, tok, 4, hipMemcpyDeviceToHost));
   printf("mk_bench: status=%u steps=%d kernel_us_avg=%.2f kernel_us_median=%.2f kernel_us_min=%.2f stream_us_per_step=%.2f tok/s=%.1f last_token=%d\n",
          status, steps, 1e3 * sum / steps, 1e3 * sorted[steps / 2], 1e3 * sorted[0], 1e3 * total / steps, steps / (total * 1e-3), htok);
+  fflush(stdout);  // a profiler's exit-time crash must not lose the result line
   if (trace) {
     std::vector<uint64_t> h(mk_trace_bytes() / 8);
     CK(hipMemcpy(h.data(), trace, mk_trace_bytes(), hipMemcpyDeviceToHost));

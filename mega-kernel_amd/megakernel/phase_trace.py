@@ -83,6 +83,56 @@ def report(t, layers, hidden, inter, ctx):
     return "\n".join(out)
 
 
+def hop_report(t, layers, nxcd=8):
+    """Latency of each exchange split into the hop itself and the wait for stragglers.
+
+    For every reader and layer: ``lat`` = its poll completion minus the publish stamp of the LAST
+    workgroup it reads from (the exchange's own latency: store visibility plus poll round trips),
+    ``own`` = its poll completion minus its own publish stamp (``own - lat`` is the time spent waiting
+    for slower writers). Workgroup b is local index b // nxcd on XCD b % nxcd. Writers per exchange:
+    QKV and MLP slice -- the reader's XCD; cross hop -- local index j on every XCD; republish -- the
+    reader's XCD at their cross-poll completion (the republish store follows it)."""
+    idx = {n: i for i, n in enumerate(SLOTS)}
+    grid = t.shape[0]
+    x = np.arange(grid) % nxcd
+    j = np.arange(grid) // nxcd
+    lo, hi = (2, layers - 2) if layers > 6 else (0, layers)
+
+    def col(layer, name):
+        return t[:, TRACE_PER_LAYER * layer + idx[name]].astype(np.float64) * TICK_US
+
+    acc = {}
+
+    def add(key, lat, own):
+        acc.setdefault(key, []).append((float(np.mean(lat)), float(np.mean(own))))
+
+    for layer in range(lo, hi):
+        apub, apoll = col(layer, "A pub (qkv)"), col(layer, "A poll (qkv)")
+        m = t[:, TRACE_PER_LAYER * layer + idx["A poll (qkv)"]] != 0
+        wx = np.array([apub[x == v].max() for v in x])
+        add("A  qkv -> attention (local)", (apoll - wx)[m], (apoll - apub)[m])
+        bpub, bpoll = col(layer, "B pub (partial)"), col(layer, "B poll (merge)")
+        att = t[:, TRACE_PER_LAYER * layer + idx["math B scores done"]] != 0
+        wb = np.array([bpub[(x == v) & att].max() if ((x == v) & att).any() else bpub[x == v].max() for v in x])
+        add("B  split partials (local)", bpoll - wb, bpoll - bpub)
+        for ph in "CE":
+            pub, cp, lp = col(layer, f"{ph} pub"), col(layer, f"{ph} cross poll"), col(layer, f"{ph} local poll")
+            wj = np.array([pub[j == v].max() for v in j])
+            add(f"{ph}  cross-XCD gather", cp - wj, cp - pub)
+            wl = np.array([cp[x == v].max() for v in x])
+            add(f"{ph}  republish (local)", lp - wl, lp - cp)
+        dpub, dpoll = col(layer, "D pub (mlp)"), col(layer, "D poll (mlp)")
+        wd = np.array([dpub[x == v].max() for v in x])
+        add("D  MLP slice (local)", dpoll - wd, dpoll - dpub)
+    out = [f"{'exchange':30s} {'lat us':>7s} {'own us':>7s}   (layers {lo}..{hi - 1}; lat = after the last writer, own = after this workgroup's publish)"]
+    for k in ("A  qkv -> attention (local)", "B  split partials (local)", "C  cross-XCD gather", "C  republish (local)",
+              "D  MLP slice (local)", "E  cross-XCD gather", "E  republish (local)"):
+        v = acc.get(k)
+        if v:
+            out.append(f"{k:30s} {np.mean([a for a, _ in v]):7.2f} {np.mean([b for _, b in v]):7.2f}")
+    return "\n".join(out)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
@@ -91,7 +141,9 @@ def main(argv=None):
     ap.add_argument("--layers", type=int, default=28)
     a = ap.parse_args(argv)
     h, i = (1024, 3072) if a.shape == "qwen3-0.6b" else (2048, 6144)
-    print(report(load(a.trace), a.layers, h, i, a.ctx))
+    t = load(a.trace)
+    print(report(t, a.layers, h, i, a.ctx))
+    print(hop_report(t, a.layers))
 
 
 if __name__ == "__main__":
