@@ -507,6 +507,7 @@ struct Smem {
   uint16_t nw[2][Geo<H, I>::NSLOT];  // per-layer norm weights by layer parity
   float gp[NMW][2][D + 4];           // attention partials of the math waves: acc[128], m, l
   u64 best[NMW];
+  uint32_t seq, wt;                  // launch sequence and write-through mode, set by the comm wave
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
 };
 
@@ -858,11 +859,40 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // B: split-K attention; this phase's loads are issued after it, off the attention's path
     if (att) attention_split<H, I>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
     // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
-    // issued only after the comm wave has published this workgroup's attention partial (B3):
-    // neither the attention nor the publish queues behind them.
+    // issued only after this workgroup's attention partial is published: neither the attention nor
+    // the publish queues behind them.
     mark(a, tl + T_M_B_END, 64);
-    lds_barrier();  // (B1)
-    lds_barrier();  // (B3) comm: this split's partial published
+    lds_barrier();  // (B1) every wave's partial in sm.gp
+    {
+      // Publish this split's partial (workgroups without a split publish their unused slot too, so
+      // that every LL word is written at every layer): wave mw merges the 8 wave partials of head
+      // mw / 4, dims 32 (mw % 4) .. +32, lanes 0-7 four dims each. A wave without keys has
+      // m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0.
+      const int h = mw >> 2, d0 = 32 * (mw & 3) + 4 * (lane & 7);
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NMW; ++q) M = fmaxf(M, sm.gp[q][h][D]);
+      mark(a, tl + T_B_MAX, 64);
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      float Ls = 0.f;
+#pragma unroll
+      for (int q = 0; q < NMW; ++q) {
+        const float f = __expf(sm.gp[q][h][D] - M);
+        const float4 pq = *reinterpret_cast<const float4*>(&sm.gp[q][h][d0]);
+        acc[0] = fmaf(pq.x, f, acc[0]); acc[1] = fmaf(pq.y, f, acc[1]);
+        acc[2] = fmaf(pq.z, f, acc[2]); acc[3] = fmaf(pq.w, f, acc[3]);
+        Ls = fmaf(sm.gp[q][h][D + 1], f, Ls);
+      }
+      Comm c;
+      c.wt = sm.wt != 0;
+      const uint32_t ep = ll_epoch(sm.seq, layer);
+      uint32_t* att_x = reinterpret_cast<uint32_t*>(a.xw) + W_ATT + (size_t)xcd * WPX * APW + (size_t)j * APW;
+      const float ml[2] = {M, Ls};
+      if (lane < 8) ll_store<4>(c, att_x, h * D + d0, acc, ep, false);
+      if (lane == 0 && (mw & 3) == 0) ll_store<2>(c, att_x, 2 * D + 2 * h, ml, ep, false);
+      mark(a, tl + T_B_PUB, 64);
+    }
+    lds_barrier();  // (B3) every wave's share of the partial is out before the loads below
     issue_ahead(I1(), layer);
     mark(a, tl + T_M_B_ISSUED, 64);
     lds_barrier();  // (B2) comm: attention output in x[0, 256)
@@ -924,6 +954,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   {
     const uint32_t st0 = ld_dev_u32(c.status);
     c.wt = (st0 & ERR_PLACEMENT) != 0;
+    if (lane == 0) { sm.seq = seq; sm.wt = c.wt ? 1u : 0u; }
     if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, st0 | ERR_PLACEMENT);
   }
   {
@@ -999,41 +1030,13 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     }
     lds_barrier();  // (A2)
 
-    // ---- B: publish this split's partial; merge all splits of the group ----------------------
+    // ---- B: merge all split partials of the group (the math waves publish this split's) --------
     mark(a, tl + T_B_START);
     lds_barrier();  // (B1)
+    lds_barrier();  // (B3) this workgroup's split partial published
     {
       const int h = lane >> 5, d0 = (lane & 31) * 4;
       uint32_t* att_x = xl + W_ATT + (size_t)xcd * WPX * APW;
-      {
-        // merge the math waves' partials of this split: lane -> head h, dims d0 .. d0+3. A wave without
-        // keys has m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0. Workgroups without a split
-        // publish their (unused) slot too, so that every LL word is written at every layer.
-        float mq[NMW];
-#pragma unroll
-        for (int q = 0; q < NMW; ++q) mq[q] = sm.gp[q][h][D];
-        float M = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < NMW; ++q) M = fmaxf(M, mq[q]);
-        mark(a, tl + T_B_MAX);
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        float Ls = 0.f;
-#pragma unroll
-        for (int q = 0; q < NMW; ++q) {
-          const float f = __expf(mq[q] - M);
-          const float4 p = *reinterpret_cast<const float4*>(&sm.gp[q][h][d0]);
-          acc[0] = fmaf(p.x, f, acc[0]); acc[1] = fmaf(p.y, f, acc[1]);
-          acc[2] = fmaf(p.z, f, acc[2]); acc[3] = fmaf(p.w, f, acc[3]);
-          Ls = fmaf(sm.gp[q][h][D + 1], f, Ls);
-        }
-        mark(a, tl + T_B_SUM);
-        const int mine = j * APW;
-        const float ml[2] = {M, Ls};
-        ll_store<4>(c, att_x, mine + h * D + d0, acc, ep, false);
-        if ((lane & 31) == 0) ll_store<2>(c, att_x, mine + 2 * D + 2 * h, ml, ep, false);
-        mark(a, tl + T_B_PUB);
-      }
-      lds_barrier();  // (B3)
       // merge the S split partials of this XCD's two heads, in split order; a lane reads its 4
       // dims and the (m, l) pairs of both heads of each split
       float M = -INFINITY, Ls = 0.f;
