@@ -107,10 +107,18 @@ hipError_t mk_reset(void);
 hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes);
 size_t mk_trace_bytes(void);
 
-/* Number of workgroups (one per CU) the cooperative launch uses on the current device, or a
- * negative value if the device cannot run the kernel. No reference counterpart (the reference
- * hard-codes 82 blocks, /root/reference/config.cuh:27). */
+/* Number of workgroups (one per CU) a launch uses on the current device, or a negative value if
+ * the device cannot run the kernel. No reference counterpart (the reference hard-codes 82 blocks,
+ * /root/reference/config.cuh:27). */
 int mk_grid_size(void);
+
+/* Launch mode on the current device for subsequent calls: 0 = plain launch (default), 1 =
+ * cooperative launch (hipLaunchCooperativeKernel: the runtime guarantees that all workgroups are
+ * resident before the grid starts, at ~16 us per token). Either way the grid needs every CU; with a
+ * plain launch a kernel of another stream or process that holds CUs makes the decode wait and, past
+ * its bounded spins, end with the status timeout bit set. No reference counterpart (the reference
+ * always launches cooperatively, /root/reference/megakernel.cu:975-990). */
+hipError_t mk_set_launch_mode(int cooperative);
 
 /* Library version string. */
 const char* mk_version(void);

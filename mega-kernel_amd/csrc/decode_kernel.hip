@@ -1174,6 +1174,7 @@ __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
 struct DeviceState {
   bool init = false;
   bool ok = false;
+  bool cooperative = false;  // launch mode, see launch()
   void* ws = nullptr;
   uint64_t* trace = nullptr;  // set by mk_set_trace; null in normal operation
 };
@@ -1229,10 +1230,19 @@ static hipError_t device_state(DeviceState** out) {
   return hipSuccess;
 }
 
+// The grid's workgroups wait on each other, so all 256 must be resident at once: one per CU, which
+// check_kernel_fits() verified, and kernels on one stream never overlap. A plain launch is the
+// default: it costs ~16 us less per token than a cooperative one (measured on the MI355X: 423 vs
+// 440 us per step). If a kernel from another stream or process holds CUs, the workgroups that did
+// start wait for the rest with bounded spins; past the bound the launch ends with the status
+// timeout bit set instead of hanging. mk_set_launch_mode(1) selects hipLaunchCooperativeKernel,
+// whose runtime guarantees co-residency before the grid starts.
 template <int H, int I>
-static hipError_t launch(KArgs& k, hipStream_t stream) {
+static hipError_t launch(KArgs& k, hipStream_t stream, bool cooperative) {
   void* args[] = {(void*)&k};
-  return hipLaunchCooperativeKernel((const void*)decode_kernel<H, I>, dim3(NWG), dim3(NT), args, 0, stream);
+  if (cooperative)
+    return hipLaunchCooperativeKernel((const void*)decode_kernel<H, I>, dim3(NWG), dim3(NT), args, 0, stream);
+  return hipLaunchKernel((const void*)decode_kernel<H, I>, dim3(NWG), dim3(NT), args, 0, stream);
 }
 
 }  // namespace mk
@@ -1273,7 +1283,7 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.max_seq = max_seq_len;
   k.num_layers = dims->num_layers;
   k.vocab = dims->vocab;
-  return s06 ? launch<1024, 3072>(k, stream) : launch<2048, 6144>(k, stream);
+  return s06 ? launch<1024, 3072>(k, stream, st->cooperative) : launch<2048, 6144>(k, stream, st->cooperative);
 }
 
 extern "C" hipError_t launch_decode_kernel(int token_id, const void* embed_weight, const void* lm_head_weight,
@@ -1320,6 +1330,15 @@ extern "C" hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes) {
   if (e != hipSuccess) return e;
   if (device_buffer != nullptr && bytes < (size_t)NWG * TRACE_N * sizeof(uint64_t)) return hipErrorInvalidValue;
   st->trace = device_buffer;
+  return hipSuccess;
+}
+
+extern "C" hipError_t mk_set_launch_mode(int cooperative) {
+  if (cooperative != 0 && cooperative != 1) return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  hipError_t e = device_state(&st);
+  if (e != hipSuccess) return e;
+  st->cooperative = cooperative != 0;
   return hipSuccess;
 }
 

@@ -170,6 +170,12 @@ int64_t status() {
 
 void reset() { MK_HIP_CHECK(mk_reset()); }
 
+// 0 = plain launch (default), 1 = cooperative launch, for the current device
+void set_launch_mode(int64_t cooperative) {
+  TORCH_CHECK(cooperative == 0 || cooperative == 1, "set_launch_mode: expected 0 or 1");
+  MK_HIP_CHECK(mk_set_launch_mode((int)cooperative));
+}
+
 // Runs decode's argument validation only (tensors may live on any one device, nothing is
 // launched) and returns (hidden, intermediate, num_layers, vocab). For host-side tests.
 std::tuple<int64_t, int64_t, int64_t, int64_t> check_args(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
@@ -186,7 +192,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode", &decode, "Qwen3 single-token decode (fp32 logits)");
   m.def("decode_greedy", &decode_greedy, "Qwen3 single-token decode; returns (fp32 logits, int32 greedy token on device)");
   m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
-  m.def("reset", &reset, "clear the decode workspace's status word and barrier counters; synchronizes");
+  m.def("reset", &reset, "clear the decode workspace (exchange words, status word) and restart its launch sequence; synchronizes");
+  m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");
   m.def("check_args", &check_args, "validate decode's arguments without launching; returns (hidden, intermediate, layers, vocab)");
   m.def("version", []() { return std::string(mk_version()); });
 }

@@ -319,3 +319,22 @@ def test_qwen17_config5():
     assert res["sampled_agree"] >= res["restate_agree"] - 1
     c = res["coss"]
     assert sum(c) / len(c) >= 0.999 and res["agree"] >= math.floor(0.88 * res["steps"])
+
+
+def test_launch_modes_agree(mini):
+    """The plain launch (default) and the cooperative launch run the same grid: one step decoded
+    in each mode gives bitwise-identical logits, token and cache row."""
+    P = 48
+    _, _, _, kc, vc = mini.prefill(P)
+    outs = []
+    try:
+        for mode in (0, 1):
+            mini.kernel.set_launch_mode(mode)
+            kd, vd = kc.to(DEV), vc.to(DEV)
+            logits, tok = mini.decode(11, kd, vd, P, greedy=True)
+            outs.append((logits.cpu(), int(tok.item()), kd[:, :, P].cpu()))
+    finally:
+        mini.kernel.set_launch_mode(0)
+    assert mini.kernel.status() == 0
+    assert torch.equal(outs[0][0], outs[1][0]) and outs[0][1] == outs[1][1]
+    assert torch.equal(outs[0][2], outs[1][2])
