@@ -66,6 +66,7 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib):
     assert call(None) == HIP_ERROR_INVALID_VALUE
     assert call(Dims(1024, 4096, 28, 151936)) == HIP_ERROR_INVALID_VALUE
     assert call(Dims(1024, 3072, 0, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 28, 255)) == HIP_ERROR_INVALID_VALUE  # fewer vocabulary rows than workgroups
     assert call(good, token=-1) == HIP_ERROR_INVALID_VALUE
     assert call(good, token=151936) == HIP_ERROR_INVALID_VALUE
     assert call(good, position=512) == HIP_ERROR_INVALID_VALUE
