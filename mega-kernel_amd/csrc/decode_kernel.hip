@@ -494,6 +494,9 @@ struct Geo {
   static_assert(HPW * WPX == H && IPW * WPX == IX && IX * NXCD == I, "shape must split evenly");
   static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64 && IXL % 2 == 0, "unsupported shape");
   static_assert(QKV_WG <= UMAX, "s_up too small");
+  // past the last layer, tile loads read the final norm (H / 8 chunks): every lane's chunk index fits
+  static_assert(TA::CPL * TA::SPAN <= H / 8 && TC::CPL * TC::SPAN <= H / 8 && TD::CPL * TD::SPAN <= H / 8 &&
+                TE::CPL * TE::SPAN <= H / 8, "dummy loads stay inside the final norm");
 };
 
 template <int H, int I>
@@ -782,12 +785,18 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // condition would make it wait for all outstanding loads). Phase P of layer l issues the loads
   // of phase P + DIST (of layer l, or of layer l + 1 when it wraps): DIST sets how many phases'
   // weights each CU keeps in flight.
+  // Past the last layer the loads still issue (same count, so the wait counts stay exact) but every
+  // row reads the final norm's 2-4 KB, which stays in L2: no weight traffic for a layer that never
+  // runs.
   auto load_phase = [&](auto qc, int layer) {
     constexpr int Q = decltype(qc)::value;
-    layer = layer < L ? layer : L - 1;
+    const bool past = layer >= L;
+    layer = past ? L - 1 : layer;
     const mk_layer_weights& lw = sm.layers[layer];
     const int mwq = opaque(mw), lq = opaque(lane);
-    if constexpr (Q == 0) tile_load<TA, TA::PS>(wA, 0, mwq, lq, rows_A(lw));
+    const uint4* hot = reinterpret_cast<const uint4*>(a.final_norm);
+    auto sel = [&](auto rp) { return [=](int r) { return past ? hot : rp(r); }; };
+    if constexpr (Q == 0) tile_load<TA, TA::PS>(wA, 0, mwq, lq, sel(rows_A(lw)));
     if constexpr (Q == 1) {
 #pragma unroll
       for (int r = 0; r < NKV; ++r) {
@@ -795,9 +804,9 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         kV[r] = ld_stream(kv_row(a.v_cache, layer, kv_pos(r)));
       }
     }
-    if constexpr (Q == 2) tile_load<TC, TC::PS>(wC, 0, mwq, lq, rows_C(lw));
-    if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, rows_D(lw));
-    if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, rows_E(lw));
+    if constexpr (Q == 2) tile_load<TC, TC::PS>(wC, 0, mwq, lq, sel(rows_C(lw)));
+    if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, sel(rows_D(lw)));
+    if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, sel(rows_E(lw)));
   };
 #ifndef MK_D_AT
 #define MK_D_AT -1
