@@ -662,11 +662,22 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
     const int p = st.p0 + g + MG * r;
     if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r], r == 0);
   }
-  // positions beyond the register-held ones (long contexts) stream here
-  for (int p = st.p0 + g + MG * NKV; p < st.p1; p += MG) {
-    const uint4 kw = p == st.position ? knew : ld_global16(ad.kv_row(a.k_cache, layer, p) + t);
-    const uint4 vw = p == st.position ? vnew : ld_global16(ad.kv_row(a.v_cache, layer, p) + t);
-    attend(kw, vw, false);
+  // positions beyond the register-held ones (long contexts) stream here, KV_BATCH keys of the group
+  // per round trip (positions past the split re-read its first row and are skipped)
+  constexpr int KV_BATCH = 4;
+  for (int p = st.p0 + g + MG * NKV; p < st.p1; p += KV_BATCH * MG) {
+    uint4 kw[KV_BATCH], vw[KV_BATCH];
+#pragma unroll
+    for (int u = 0; u < KV_BATCH; ++u) {
+      const int pu = p + u * MG < st.p1 ? p + u * MG : st.p0;
+      kw[u] = ld_global16(ad.kv_row(a.k_cache, layer, pu) + t);
+      vw[u] = ld_global16(ad.kv_row(a.v_cache, layer, pu) + t);
+    }
+#pragma unroll
+    for (int u = 0; u < KV_BATCH; ++u) {
+      const int pu = p + u * MG;
+      if (pu < st.p1) attend(pu == st.position ? knew : kw[u], pu == st.position ? vnew : vw[u], false);
+    }
   }
   // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
   // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
@@ -1046,32 +1057,59 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     {
       const int h = lane >> 5, d0 = (lane & 31) * 4;
       uint32_t* att_x = xl + W_ATT + (size_t)xcd * WPX * APW;
-      // merge the S split partials of this XCD's two heads, in split order; a lane reads its 4
-      // dims and the (m, l) pairs of both heads of each split
+      // Merge the S split partials of this XCD's two heads, in split order (lane -> head h, dims
+      // d0 .. d0+3, plus each split's (m0, l0, m1, l1)). Each poll round trip under load costs
+      // ~0.4-0.8 us whether the data is ready or not, so the number of sequential rounds after
+      // the last split is published is what matters: up to SB0 splits are polled in one round;
+      // beyond that the wait is done on the splits' (m, l) words alone (lane s < S polls split s,
+      // one 16-byte load per lane), then every split's accumulator slice is read in rounds of SB1.
       float M = -INFINITY, Ls = 0.f;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      constexpr int SB = H <= 1024 ? 4 : 2;  // splits per poll (register budget)
-      for (int s0 = 0; s0 < S; s0 += SB) {
-        int off[2 * SB];
+      auto merge_one = [&](float ms, float ls, const float* w) {
+        const float n = fmaxf(M, ms);
+        const float cm = __expf(M - n), cs = __expf(ms - n);
+        Ls = Ls * cm + ls * cs;
+        acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
+        acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
+        M = n;
+      };
+      constexpr int SB0 = H <= 1024 ? 4 : 2;
+      constexpr int SB1 = H <= 1024 ? 8 : 4;  // register budget
+      if (S <= SB0) {
+        int off[2 * SB0];
 #pragma unroll
-        for (int q = 0; q < SB; ++q) {
-          const int s = s0 + q < S ? s0 + q : s0;
+        for (int q = 0; q < SB0; ++q) {
+          const int s = q < S ? q : 0;
           off[2 * q + 0] = s * APW + h * D + d0;
           off[2 * q + 1] = s * APW + 2 * D;
         }
-        float v[8 * SB];
-        ll_poll<2 * SB, 4>(c, att_x, off, ep, v);
+        float v[8 * SB0];
+        ll_poll<2 * SB0, 4>(c, att_x, off, ep, v);
 #pragma unroll
-        for (int q = 0; q < SB; ++q) {
-          if (s0 + q < S) {
-            const float* w = v + 8 * q;
-            const float ms = h ? w[6] : w[4], ls = h ? w[7] : w[5];
-            const float n = fmaxf(M, ms);
-            const float cm = __expf(M - n), cs = __expf(ms - n);
-            Ls = Ls * cm + ls * cs;
-            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
-            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
-            M = n;
+        for (int q = 0; q < SB0; ++q) {
+          const float* w = v + 8 * q;
+          if (q < S) merge_one(h ? w[6] : w[4], h ? w[7] : w[5], w);
+        }
+      } else {
+        float ml[4];
+        {
+          const int off1[1] = {(lane < S ? lane : 0) * APW + 2 * D};
+          ll_poll<1, 4>(c, att_x, off1, ep, ml);
+        }
+        for (int s0 = 0; s0 < S; s0 += SB1) {
+          int off[SB1];
+#pragma unroll
+          for (int q = 0; q < SB1; ++q) off[q] = (s0 + q < S ? s0 + q : 0) * APW + h * D + d0;
+          float v[4 * SB1];
+          ll_poll<SB1, 4, 4 * SB1 - 1>(c, att_x, off, ep, v);  // one round in flight
+#pragma unroll
+          for (int q = 0; q < SB1; ++q) {
+            if (s0 + q < S) {
+              float mlq[4];  // lane (s0 + q)'s (m0, l0, m1, l1), read before this lane picks its head
+#pragma unroll
+              for (int i = 0; i < 4; ++i) mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[i]), s0 + q));
+              merge_one(h ? mlq[2] : mlq[0], h ? mlq[3] : mlq[1], v + 4 * q);
+            }
           }
         }
       }
