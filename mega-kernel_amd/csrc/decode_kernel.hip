@@ -62,6 +62,7 @@ constexpr int NT = 64 * (NMW + 1);  // threads per workgroup
 constexpr int MG = NMW * 4;   // 16-lane math groups
 constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
 constexpr int QKV_WG = QKV_X / WPX;  // 16
+constexpr int D_FREE = 8;            // local workgroups without gate/up rows (see Geo::DPW)
 #ifndef MK_NKV
 #define MK_NKV 1
 #endif
@@ -476,23 +477,26 @@ template <int H, int I>
 struct Geo {
   static constexpr int E = H / 64;        // residual elements per comm lane
   static constexpr int IX = I / NXCD;     // MLP intermediate slice per XCD
-  static constexpr int IPW = IX / WPX;    // gate (and up) rows per workgroup
+  // The MLP slice's gate/up rows go to local workgroups D_FREE..31 only, DPW intermediates (gate and
+  // up rows) each: the attention splits run on workgroups 0..S-1, and up to S = D_FREE of them then
+  // carry no gate/up weights, whose 48-64 KB of loads would otherwise queue ahead of their exchanges.
+  static constexpr int DPW = IX / (WPX - D_FREE);
   static constexpr int HPW = H / WPX;     // o_proj / down_proj rows per workgroup
   static constexpr bool SMALL = H <= 1024;
   // phase tiles: A = QKV rows, C = o_proj partial, D = gate/up rows, E = down_proj partial; the
   // last argument caps the steps held in registers ahead (the larger shape streams the rest)
   typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 1> TA;
   typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 1> TC;
-  typedef Tile<2 * IPW, H, 64, SMALL ? 8 : 1> TD;
+  typedef Tile<2 * DPW, H, 64, SMALL ? 8 : 1> TD;
   typedef Tile<HPW, IX, 16, SMALL ? 8 : 1> TE;
   static constexpr int XN = (H > IX ? H : IX);
-  static constexpr int UMAX = 2 * IPW > HPW ? 2 * IPW : HPW;
+  static constexpr int UMAX = 2 * DPW > HPW ? 2 * DPW : HPW;
   static constexpr int NSLOT = 2 * H + 2 * D;   // bf16 norm weights per layer: input, post-attention, q, k
   static constexpr int NSL16 = NSLOT / 8;       // ... in 16-byte chunks
   static constexpr int NSL_L = (NSL16 + 64 * NMW - 1) / (64 * NMW);  // chunks per math lane
   static constexpr int IXL = IX / 64;           // MLP words per comm lane
-  static_assert(HPW * WPX == H && IPW * WPX == IX && IX * NXCD == I, "shape must split evenly");
-  static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && IPW <= 64 && IXL % 2 == 0, "unsupported shape");
+  static_assert(HPW * WPX == H && DPW * (WPX - D_FREE) == IX && IX * NXCD == I, "shape must split evenly");
+  static_assert(IX % 128 == 0 && H % 512 == 0 && HPW <= 64 && DPW <= 64 && IXL % 2 == 0, "unsupported shape");
   static_assert(QKV_WG <= UMAX, "s_up too small");
   // past the last layer, tile loads read the final norm (H / 8 chunks): every lane's chunk index fits
   static_assert(TA::CPL * TA::SPAN <= H / 8 && TC::CPL * TC::SPAN <= H / 8 && TD::CPL * TD::SPAN <= H / 8 &&
@@ -571,8 +575,10 @@ struct Addr {
     const uint16_t* wg;
     const uint16_t* wu;
     int row0;
+    const uint16_t* none;  // non-null: this workgroup has no gate/up rows; its loads read this hot row
     __device__ const uint4* operator()(int r) const {
-      return reinterpret_cast<const uint4*>(r < G::IPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - G::IPW) * H);
+      if (none) return reinterpret_cast<const uint4*>(none);
+      return reinterpret_cast<const uint4*>(r < G::DPW ? wg + (size_t)(row0 + r) * H : wu + (size_t)(row0 + r - G::DPW) * H);
     }
   };
   struct RowsE {
@@ -592,7 +598,9 @@ struct Addr {
     return {(const uint16_t*)lw.o_proj_weight, G::HPW * st.j, 2 * D * st.xcd};
   }
   __device__ RowsD Dm(const mk_layer_weights& lw) const {
-    return {(const uint16_t*)lw.gate_proj_weight, (const uint16_t*)lw.up_proj_weight, G::IX * st.xcd + G::IPW * st.j};
+    if (st.j < D_FREE) return {nullptr, nullptr, 0, a.final_norm};
+    return {(const uint16_t*)lw.gate_proj_weight, (const uint16_t*)lw.up_proj_weight,
+            G::IX * st.xcd + G::DPW * (st.j - D_FREE), nullptr};
   }
   __device__ RowsE E(const mk_layer_weights& lw) const {
     return {(const uint16_t*)lw.down_proj_weight, G::HPW * st.j, G::IX * st.xcd};
@@ -1136,10 +1144,10 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     lds_barrier();  // (D1)
     {
       uint32_t* m_x = xl + W_M + (size_t)xcd * MAX_IX;
-      if (lane < G::IPW) {
-        const float gs = sm.up[lane], us = sm.up[lane + G::IPW];
+      if (j >= D_FREE && lane < G::DPW) {
+        const float gs = sm.up[lane], us = sm.up[lane + G::DPW];
         const float m = gs / (1.f + expf(-gs)) * us;  // silu(g) * u
-        ll_store<1>(c, m_x, G::IPW * j + lane, &m, ep, false);
+        ll_store<1>(c, m_x, G::DPW * (j - D_FREE) + lane, &m, ep, false);
       }
       mark(a, tl + T_D_PUB);
       constexpr int MW = G::IXL % 4 == 0 ? 4 : 2;
