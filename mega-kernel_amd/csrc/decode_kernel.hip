@@ -1066,57 +1066,65 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       const int h = lane >> 5, d0 = (lane & 31) * 4;
       uint32_t* att_x = xl + W_ATT + (size_t)xcd * WPX * APW;
       // Merge the S split partials of this XCD's two heads, in split order (lane -> head h, dims
-      // d0 .. d0+3, plus each split's (m0, l0, m1, l1)). Each poll round trip under load costs
-      // ~0.4-0.8 us whether the data is ready or not, so the number of sequential rounds after
-      // the last split is published is what matters: up to SB0 splits are polled in one round;
-      // beyond that the wait is done on the splits' (m, l) words alone (lane s < S polls split s,
-      // one 16-byte load per lane), then every split's accumulator slice is read in rounds of SB1.
+      // d0 .. d0+3, plus each split's (m0, l0, m1, l1)). A poll round under load costs ~0.5 us even
+      // when its data is ready, so the splits are taken in as few sequential polls as the registers
+      // allow: all of them at once up to SB0 splits, otherwise SB1 splits per poll.
       float M = -INFINITY, Ls = 0.f;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      auto merge_one = [&](float ms, float ls, const float* w) {
-        const float n = fmaxf(M, ms);
-        const float cm = __expf(M - n), cs = __expf(ms - n);
-        Ls = Ls * cm + ls * cs;
-        acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
-        acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
-        M = n;
+      auto merge_batch = [&](auto nb, int s0) {
+        constexpr int NB = decltype(nb)::value;
+        int off[2 * NB];
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+          const int s = s0 + q < S ? s0 + q : s0;
+          off[2 * q + 0] = s * APW + h * D + d0;
+          off[2 * q + 1] = s * APW + 2 * D;
+        }
+        float v[8 * NB];
+        ll_poll<2 * NB, 4, 32>(c, att_x, off, ep, v);  // two rounds in flight up to 4 splits, else one
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+          if (s0 + q < S) {
+            const float* w = v + 8 * q;
+            const float ms = h ? w[6] : w[4], ls = h ? w[7] : w[5];
+            const float n = fmaxf(M, ms);
+            const float cm = __expf(M - n), cs = __expf(ms - n);
+            Ls = Ls * cm + ls * cs;
+            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
+            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
+            M = n;
+          }
+        }
       };
       constexpr int SB0 = H <= 1024 ? 4 : 2;
       constexpr int SB1 = H <= 1024 ? 8 : 4;  // register budget
       if (S <= SB0) {
-        int off[2 * SB0];
-#pragma unroll
-        for (int q = 0; q < SB0; ++q) {
-          const int s = q < S ? q : 0;
-          off[2 * q + 0] = s * APW + h * D + d0;
-          off[2 * q + 1] = s * APW + 2 * D;
-        }
-        float v[8 * SB0];
-        ll_poll<2 * SB0, 4>(c, att_x, off, ep, v);
-#pragma unroll
-        for (int q = 0; q < SB0; ++q) {
-          const float* w = v + 8 * q;
-          if (q < S) merge_one(h ? w[6] : w[4], h ? w[7] : w[5], w);
-        }
+        merge_batch(std::integral_constant<int, SB0>(), 0);
       } else {
-        float ml[4];
-        {
-          const int off1[1] = {(lane < S ? lane : 0) * APW + 2 * D};
-          ll_poll<1, 4>(c, att_x, off1, ep, ml);
-        }
+        // SB1 splits per poll: each lane's accumulator slice of every split, plus one load of the
+        // splits' (m, l) words (lane q reads split s0 + q's), shared across lanes with readlane
         for (int s0 = 0; s0 < S; s0 += SB1) {
-          int off[SB1];
+          int off[SB1 + 1];
 #pragma unroll
-          for (int q = 0; q < SB1; ++q) off[q] = (s0 + q < S ? s0 + q : 0) * APW + h * D + d0;
-          float v[4 * SB1];
-          ll_poll<SB1, 4, 4 * SB1 - 1>(c, att_x, off, ep, v);  // one round in flight
+          for (int q = 0; q < SB1; ++q) off[q] = (s0 + q < S ? s0 + q : s0) * APW + h * D + d0;
+          off[SB1] = (lane < SB1 && s0 + lane < S ? s0 + lane : s0) * APW + 2 * D;
+          float v[4 * (SB1 + 1)];
+          ll_poll<SB1 + 1, 4, 16>(c, att_x, off, ep, v);  // one round in flight
 #pragma unroll
           for (int q = 0; q < SB1; ++q) {
             if (s0 + q < S) {
-              float mlq[4];  // lane (s0 + q)'s (m0, l0, m1, l1), read before this lane picks its head
+              float mlq[4];  // lane q's (m0, l0, m1, l1), read before this lane picks its head
 #pragma unroll
-              for (int i = 0; i < 4; ++i) mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[i]), s0 + q));
-              merge_one(h ? mlq[2] : mlq[0], h ? mlq[3] : mlq[1], v + 4 * q);
+              for (int i = 0; i < 4; ++i)
+                mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[4 * SB1 + i]), q));
+              const float ms = h ? mlq[2] : mlq[0], ls = h ? mlq[3] : mlq[1];
+              const float n = fmaxf(M, ms);
+              const float cm = __expf(M - n), cs = __expf(ms - n);
+              Ls = Ls * cm + ls * cs;
+              const float* w = v + 4 * q;
+              acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
+              acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
+              M = n;
             }
           }
         }
