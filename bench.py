@@ -200,7 +200,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": traffic,
-            "kernel": "mk::decode_kernel<1024, 3072>" if a.shape == "qwen3-0.6b" else "mk::decode_kernel<2048, 6144>",
+            # NKV = 1 while the attention splits are at most 32 positions long, 2 beyond
+            "kernel": ("mk::decode_kernel<1024, 3072, NKV>" if a.shape == "qwen3-0.6b"
+                       else "mk::decode_kernel<2048, 6144, NKV>"),
             "bytes_per_launch_avg": int(sum(bytes_steps) / a.steps),
             "kernel_us_avg": round(1e3 * region_ms / a.steps, 2),
         },

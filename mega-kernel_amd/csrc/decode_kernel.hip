@@ -63,11 +63,17 @@ constexpr int MG = NMW * 4;   // 16-lane math groups
 constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
 constexpr int QKV_WG = QKV_X / WPX;  // 16
 constexpr int D_FREE = 8;            // local workgroups without gate/up rows (see Geo::DPW)
-#ifndef MK_NKV
-#define MK_NKV 1
-#endif
-constexpr int NKV = MK_NKV;   // K/V rows per math group held in registers (phases ahead)
-constexpr int KV_SPLIT = MG * NKV;   // positions per attention split covered by registers
+// K/V rows per math group held in registers (loaded a layer ahead) is a kernel template parameter
+// NKV: 1 while every split is at most MG positions long, 2 beyond (kv_rows_for()).
+constexpr int SPLIT_POS = MG;        // positions per split while the split count is below its cap
+// Attention split merge: up to SB0 splits are polled with their (m, l) words in one round; beyond
+// that the comm wave polls SB1 splits per round (as many as its registers hold).
+template <int H> constexpr int merge_sb0() { return H <= 1024 ? 4 : 2; }
+constexpr int SB1 = 8;
+// Contexts above this many positions use two merge rounds' worth of splits, which spreads the
+// streamed K/V rows over twice as many CUs (measured on MI355X: at context 2000 (4000) 16 splits
+// take 525 (593) us per token at 0.6B against 556 (670) with 8).
+constexpr int S_LONG_CTX = 1024;
 constexpr int APW = 264;      // LL words per attention partial: acc[2][128], m0, l0, m1, l1, pad
 constexpr float EPS = 1e-6f;
 constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
@@ -199,9 +205,11 @@ __device__ __forceinline__ void ll_poll(Comm& c, const uint32_t* base, const int
                                         float (&v)[W * NL]) {
   static_assert(W == 2 || W == 4, "LL poll width");
   typedef unsigned uwv __attribute__((ext_vector_type(W)));
+  auto zero = [&]() {  // failure paths only, so v holds no registers while the loads are out
 #pragma unroll
-  for (int k = 0; k < W * NL; ++k) v[k] = 0.f;
-  if (c.failed) return;
+    for (int k = 0; k < W * NL; ++k) v[k] = 0.f;
+  };
+  if (c.failed) { zero(); return; }
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
   auto issue = [&](uwv (&r)[NL]) {
 #pragma unroll
@@ -243,14 +251,14 @@ __device__ __forceinline__ void ll_poll(Comm& c, const uint32_t* base, const int
       if (ready(r0)) { take(r0); return; }
       issue(r0);
       if (ready(r1)) { take(r1); return; }
-      if (check(it)) return;
+      if (check(it)) { zero(); return; }
     }
   } else {  // large polls keep one round in flight (register budget)
     uwv r0[NL];
     for (uint32_t it = 0;; it += 2) {
       issue(r0);
       if (ready(r0)) { take(r0); return; }
-      if (check(it)) return;
+      if (check(it)) { zero(); return; }
     }
   }
 }
@@ -542,9 +550,12 @@ __device__ __forceinline__ Step make_step(const KArgs& a) {
   s.ctx = a.position + 1;
   s.L = a.num_layers;
   // Split-K attention: the context is cut into S splits handled by local workgroups 0..S-1.
-  // Up to KV_SPLIT positions per split come from registers loaded a layer ahead.
-  int S = (s.ctx + KV_SPLIT - 1) / KV_SPLIT;
-  s.S = S < WPX ? S : WPX;
+  // Up to MG * NKV positions per split come from registers loaded a layer ahead, the rest stream
+  // in phase B. One split per SPLIT_POS positions, capped at what one merge round takes (two
+  // rounds' worth for long contexts): a merge round costs more than a longer split.
+  const int cap = s.ctx > S_LONG_CTX ? 2 * SB1 : SB1;
+  const int S = (s.ctx + SPLIT_POS - 1) / SPLIT_POS;
+  s.S = S < cap ? S : cap;
   s.att_wg = s.j < s.S;
   s.p0 = s.att_wg ? (int)(((long long)s.ctx * s.j) / s.S) : 0;
   s.p1 = s.att_wg ? (int)(((long long)s.ctx * (s.j + 1)) / s.S) : 0;
@@ -631,7 +642,7 @@ struct Addr {
 // per group from registers; longer splits stream the rest), merged over the wave's groups into
 // sm.gp[mw]: per head acc[128], m, l. Online softmax per group for both query heads of the GQA pair,
 // so each K/V row is read once (/root/reference/megakernel.cu:228-370).
-template <int H, int I>
+template <int H, int I, int NKV>
 __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, const Step& st, const Addr<H, I>& ad,
                                                 int layer, int mw, int lane, const uint4 (&kK)[NKV],
                                                 const uint4 (&kV)[NKV], int tl) {
@@ -710,9 +721,9 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
   }
 }
 
-// Tied LM head over this workgroup's vocabulary rows [r0, r1): wave mw takes rows r0 + mw + NMW*s,
-// one row per step (64 lanes x LCPL chunks), LP rows in flight per wave; fused greedy argmax key of
-// the wave into sm.best[mw].
+// Tied LM head over this workgroup's vocabulary rows: wave mw takes row mw of every row group the
+// workgroup owns, one row per step (64 lanes x LCPL chunks), LP rows in flight per wave; fused
+// greedy argmax key of the wave into sm.best[mw].
 template <int H, int I>
 __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, int lane) {
   constexpr int LCPL = H / 512;
@@ -720,16 +731,19 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
 #define MK_LP 4
 #endif
   constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
-  const int r0 = (int)(((long long)a.vocab * blockIdx.x) / NWG);
-  const int r1 = (int)(((long long)a.vocab * (blockIdx.x + 1)) / NWG);
-  const int nmine = (r1 - r0 - mw + NMW - 1) / NMW;
+  // row groups of NMW rows interleaved over the workgroups (step s reads group blockIdx.x + NWG*s),
+  // so the grid sweeps the table front to back instead of 256 separate streams
+  const int ngroups = (a.vocab + NMW - 1) / NMW;
+  const int nmine = ((int)blockIdx.x < ngroups) ? (ngroups - (int)blockIdx.x + NWG - 1) / NWG : 0;
+  auto row_of = [&](int s, int m) { return NMW * ((int)blockIdx.x + NWG * s) + m; };
+  const int rlast = a.vocab - 1;
   const int lq = opaque(lane), mwq = opaque(mw);
   uint4 xh[LCPL], xl[LCPL];
 #pragma unroll
   for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
   auto lm_load = [&](int s, uint4 (&b)[LCPL]) {
-    int row = r0 + mwq + NMW * s;
-    row = row < r1 ? row : r1 - 1;  // past the end: re-read the last row (unconditional loads)
+    int row = row_of(s, mwq);
+    row = (s < nmine && row <= rlast) ? row : rlast;  // past the end: re-read the last row (unconditional loads)
     const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lq;
 #pragma unroll
     for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
@@ -743,8 +757,8 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
     for (int i = 0; i < LP; ++i) {
       const float v = wave_sum(dot_chunks<LCPL>(buf[i], xh, xl));
       const int s = s0 + i;
-      if (s < nmine) {
-        const int row = r0 + mwq + NMW * s;
+      const int row = row_of(s, mwq);
+      if (s < nmine && row <= rlast) {
         if (lq == 0) gpw(a.logits)[row] = v;
         best = umax64(best, argmax_key(v, row));
       }
@@ -764,7 +778,7 @@ __device__ __forceinline__ void copy_layer_table(const KArgs& a, Smem<H, I>& sm)
 }
 
 // ---- math waves ------------------------------------------------------------------------------
-template <int H, int I, int DIST>
+template <int H, int I, int DIST, int NKV>
 __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const Step& st) {
   typedef Geo<H, I> G;
   typedef typename G::TA TA;
@@ -885,7 +899,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     mark(a, tl + T_M_B_START, 64);
 
     // B: split-K attention; this phase's loads are issued after it, off the attention's path
-    if (att) attention_split<H, I>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
+    if (att) attention_split<H, I, NKV>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
     // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
     // issued only after this workgroup's attention partial is published: neither the attention nor
     // the publish queues behind them.
@@ -1068,7 +1082,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       // Merge the S split partials of this XCD's two heads, in split order (lane -> head h, dims
       // d0 .. d0+3, plus each split's (m0, l0, m1, l1)). A poll round under load costs ~0.5 us even
       // when its data is ready, so the splits are taken in as few sequential polls as the registers
-      // allow: all of them at once up to SB0 splits, otherwise SB1 splits per poll.
+      // allow: all of them at once up to SB0 splits, otherwise SB1 splits per poll (at most two).
       float M = -INFINITY, Ls = 0.f;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       auto merge_batch = [&](auto nb, int s0) {
@@ -1096,38 +1110,41 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
           }
         }
       };
-      constexpr int SB0 = H <= 1024 ? 4 : 2;
-      constexpr int SB1 = H <= 1024 ? 8 : 4;  // register budget
+      constexpr int SB0 = merge_sb0<H>();
+      static_assert(2 * SB1 <= WPX, "split count");
+      // NB splits from s0 in one poll: each lane's accumulator slice of every split, plus one load
+      // of the splits' (m, l) words (lane q reads split s0 + q's), shared across lanes by readlane
+      auto merge_wide = [&](auto nb, int s0) {
+        constexpr int NB = decltype(nb)::value;
+        int off[NB + 1];
+#pragma unroll
+        for (int q = 0; q < NB; ++q) off[q] = (s0 + q < S ? s0 + q : s0) * APW + h * D + d0;
+        off[NB] = (lane < NB && s0 + lane < S ? s0 + lane : s0) * APW + 2 * D;
+        float v[4 * (NB + 1)];
+        ll_poll<NB + 1, 4, 16>(c, att_x, off, ep, v);  // one round in flight
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+          if (s0 + q < S) {
+            float mlq[4];  // lane q's (m0, l0, m1, l1), read before this lane picks its head
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[4 * NB + i]), q));
+            const float ms = h ? mlq[2] : mlq[0], ls = h ? mlq[3] : mlq[1];
+            const float n = fmaxf(M, ms);
+            const float cm = __expf(M - n), cs = __expf(ms - n);
+            Ls = Ls * cm + ls * cs;
+            const float* w = v + 4 * q;
+            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
+            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
+            M = n;
+          }
+        }
+      };
       if (S <= SB0) {
         merge_batch(std::integral_constant<int, SB0>(), 0);
       } else {
-        // SB1 splits per poll: each lane's accumulator slice of every split, plus one load of the
-        // splits' (m, l) words (lane q reads split s0 + q's), shared across lanes with readlane
-        for (int s0 = 0; s0 < S; s0 += SB1) {
-          int off[SB1 + 1];
-#pragma unroll
-          for (int q = 0; q < SB1; ++q) off[q] = (s0 + q < S ? s0 + q : s0) * APW + h * D + d0;
-          off[SB1] = (lane < SB1 && s0 + lane < S ? s0 + lane : s0) * APW + 2 * D;
-          float v[4 * (SB1 + 1)];
-          ll_poll<SB1 + 1, 4, 16>(c, att_x, off, ep, v);  // one round in flight
-#pragma unroll
-          for (int q = 0; q < SB1; ++q) {
-            if (s0 + q < S) {
-              float mlq[4];  // lane q's (m0, l0, m1, l1), read before this lane picks its head
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[4 * SB1 + i]), q));
-              const float ms = h ? mlq[2] : mlq[0], ls = h ? mlq[3] : mlq[1];
-              const float n = fmaxf(M, ms);
-              const float cm = __expf(M - n), cs = __expf(ms - n);
-              Ls = Ls * cm + ls * cs;
-              const float* w = v + 4 * q;
-              acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
-              acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
-              M = n;
-            }
-          }
-        }
+#pragma unroll 1
+        for (int s0 = 0; s0 < S; s0 += SB1) merge_wide(std::integral_constant<int, SB1>(), s0);
       }
       mark(a, tl + T_B_POLL);
       const float inv = 1.f / Ls;
@@ -1222,13 +1239,13 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 3);
 }
 
-template <int H, int I>
+template <int H, int I, int NKV>
 __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<H, I> sm;
   const Step st = make_step(a);
   mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 0);
   if (threadIdx.x < 64) comm_role<H, I>(a, sm, st);
-  else math_role<H, I, PF_DIST>(a, sm, st);
+  else math_role<H, I, PF_DIST, NKV>(a, sm, st);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1247,10 +1264,13 @@ static std::mutex g_mu;
 
 template <int H, int I>
 static hipError_t check_kernel_fits() {
-  int blocks = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)decode_kernel<H, I>, NT, 0);
-  if (e != hipSuccess) return e;
-  return blocks >= 1 ? hipSuccess : hipErrorCooperativeLaunchTooLarge;
+  for (const void* f : {(const void*)decode_kernel<H, I, 1>, (const void*)decode_kernel<H, I, 2>}) {
+    int blocks = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, NT, 0);
+    if (e != hipSuccess) return e;
+    if (blocks < 1) return hipErrorCooperativeLaunchTooLarge;
+  }
+  return hipSuccess;
 }
 
 // Workspaces per device, one per supported model shape: NSHAPE * WS_BYTES.
@@ -1300,12 +1320,21 @@ static hipError_t device_state(DeviceState** out) {
 // start wait for the rest with bounded spins; past the bound the launch ends with the status
 // timeout bit set instead of hanging. mk_set_launch_mode(1) selects hipLaunchCooperativeKernel,
 // whose runtime guarantees co-residency before the grid starts.
+// Register rows per math group for a context: one while the splits are at most SPLIT_POS long (a
+// second would only re-read a row), two once they are longer, so that contexts up to 512 (2048 at
+// two merge rounds) stream no K/V inside the attention phase. The kernel's split rule is the same.
+static int kv_rows_for(int ctx) {
+  const int cap = ctx > S_LONG_CTX ? 2 * SB1 : SB1;
+  return ctx > cap * SPLIT_POS ? 2 : 1;
+}
+
 template <int H, int I>
 static hipError_t launch(KArgs& k, hipStream_t stream, bool cooperative) {
   void* args[] = {(void*)&k};
-  if (cooperative)
-    return hipLaunchCooperativeKernel((const void*)decode_kernel<H, I>, dim3(NWG), dim3(NT), args, 0, stream);
-  return hipLaunchKernel((const void*)decode_kernel<H, I>, dim3(NWG), dim3(NT), args, 0, stream);
+  const void* f = kv_rows_for(k.position + 1) == 1 ? (const void*)decode_kernel<H, I, 1>
+                                                   : (const void*)decode_kernel<H, I, 2>;
+  if (cooperative) return hipLaunchCooperativeKernel(f, dim3(NWG), dim3(NT), args, 0, stream);
+  return hipLaunchKernel(f, dim3(NWG), dim3(NT), args, 0, stream);
 }
 
 }  // namespace mk
@@ -1412,4 +1441,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.7 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.8 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch)"; }

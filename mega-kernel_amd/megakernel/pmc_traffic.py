@@ -32,7 +32,7 @@ def summarize(path, counter, copy_bytes):
     if not dec or not copies:
         raise SystemExit(f"{path}: no {KERNEL} or {COPY} dispatches with {counter}")
     cal = max(copies)  # the calibration copy is the largest copyBuffer dispatch
-    return {"kernel": sorted(names)[0], "dispatches": len(dec), "kib_per_dispatch": statistics.mean(dec),
+    return {"kernels": sorted(names), "dispatches": len(dec), "kib_per_dispatch": statistics.mean(dec),
             "copy_kib": cal, "scale": copy_bytes / (cal * 1024.0)}
 
 
@@ -55,7 +55,8 @@ def main(argv=None):
     fs, ws = round(fe["scale"], 5), round(wr["scale"], 5)
     hbm = fe["kib_per_dispatch"] * 1024 * fs + wr["kib_per_dispatch"] * 1024 * ws
     out = {
-        "kernel": fe["kernel"].replace("void ", "").split("(")[0],
+        # the decode kernel's instantiations (register rows per context), averaged over all dispatches
+        "kernel": ", ".join(k.replace("void ", "").split("(")[0] for k in fe["kernels"]),
         "kernel_version": a.version,
         "shape": a.shape, "prompt": a.prompt, "max_seq_len": a.max_seq,
         "dispatches": fe["dispatches"],
