@@ -88,9 +88,33 @@ hipError_t mk_decode(const mk_model_dims* dims, int token_id, const void* embed_
                      void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
                      int32_t* out_token, hipStream_t stream);
 
+/*
+ * Several decode steps in one call, with no host synchronization between them: the device-side
+ * multi-token loop. Step i (0 <= i < n) runs at position + i and reads its input token from device
+ * memory, tokens[i] (int32, device array of n + 1 entries, tokens[0] set by the caller).
+ *   generate != 0: greedy generation. Step i writes its greedy token (as mk_decode's out_token) to
+ *                  tokens[i + 1], which step i + 1 then consumes; tokens[1..n] are the output.
+ *   generate == 0: teacher forcing, e.g. filling the cache for a prompt through the decode path.
+ *                  tokens[0..n-1] are all inputs; only the last step's greedy token is written,
+ *                  to tokens[n].
+ * logits (fp32 [vocab]) holds the last step's logits when the stream reaches the end of the call;
+ * every step writes its K/V row. Requires position + n <= max_seq_len; other argument errors as
+ * mk_decode. An input token out of range sets status bit 2 (see mk_status) and decodes token 0.
+ * Replaces the reference's host loop of one `decode` call plus `argmax().item()` per token
+ * (/root/reference/model.py:95-127), which synchronizes the host on every token.
+ */
+hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens, int n, int generate,
+                           const void* embed_weight, const void* lm_head_weight,
+                           const void* final_norm_weight, const void* layer_weights,
+                           const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                           int position, int max_seq_len, float* logits, hipStream_t stream);
+
 /* Device status word of the current device's workspace (0 = healthy; bit 0 = a grid wait timed
- * out, results of that launch are invalid). Synchronizes with the device. No reference
- * counterpart: the reference surfaces errors only through the launch status. */
+ * out, results of that launch are invalid; bit 2 = a device-side input token of mk_decode_steps
+ * was out of range; decoding went on with token 0). A timeout makes later launches drain early
+ * until mk_reset.
+ * Synchronizes with the device. No reference counterpart: the reference surfaces errors only
+ * through the launch status. */
 hipError_t mk_status(uint32_t* status);
 
 /* Clears the status word and the workspace's barrier counters of the current device.

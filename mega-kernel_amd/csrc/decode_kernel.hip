@@ -80,6 +80,8 @@ constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
 constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr uint32_t ERR_TIMEOUT = 1u;
 constexpr uint32_t ERR_PLACEMENT = 2u;
+constexpr uint32_t ERR_TOKEN = 4u;  // a device-side input token was out of range (token 0 used)
+constexpr uint32_t ERR_DRAIN = ~ERR_TOKEN;  // status bits that make the waits give up (a bad token does not)
 #ifndef MK_PF_DIST
 #define MK_PF_DIST 2
 #endif
@@ -120,6 +122,7 @@ struct KArgs {
   uint16_t* v_cache;
   float* logits;
   int32_t* out_token;
+  const int32_t* token_in;  // when set, the input token is read here (written by an earlier launch)
   u64* xw;          // exchange workspace
   uint64_t* trace;  // optional: per-workgroup phase timestamps (TRACE_N per workgroup)
   int token, position, max_seq, num_layers, vocab;
@@ -235,7 +238,7 @@ __device__ __forceinline__ void ll_poll(Comm& c, const uint32_t* base, const int
       for (int i = 0; i < W; ++i) v[W * k + i] = ll_value(r[k][i]);
   };
   auto check = [&](uint32_t it) {
-    if ((it & 62u) == 62u && ld_dev_u32(c.status) != 0) { c.failed = true; return true; }
+    if ((it & 62u) == 62u && (ld_dev_u32(c.status) & ERR_DRAIN) != 0) { c.failed = true; return true; }
     if (it > SPIN_LIMIT) {
       if ((threadIdx.x & 63) == 0) st_dev_u32(c.status, ERR_TIMEOUT);
       c.failed = true;
@@ -993,14 +996,22 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   __builtin_amdgcn_s_setprio(MK_COMM_PRIO);  // the comm wave's instructions issue ahead of math waves'
 #endif
   const uint32_t seq = ld_dev_u32(reinterpret_cast<const uint32_t*>(xw + X_SEQ));
+  const uint32_t st0 = ld_dev_u32(c.status);
   {
-    const uint32_t st0 = ld_dev_u32(c.status);
     c.wt = (st0 & ERR_PLACEMENT) != 0;
     if (lane == 0) { sm.seq = seq; sm.wt = c.wt ? 1u : 0u; }
     if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, st0 | ERR_PLACEMENT);
   }
   {
-    const uint16_t* row = a.embed + (size_t)a.token * H;
+    int token = a.token;
+    if (a.token_in) {  // every workgroup reads the same word, so all take the same branch below
+      token = (int)ld_dev_u32(reinterpret_cast<const uint32_t*>(a.token_in));
+      if (token < 0 || token >= a.vocab) {
+        if (lane == 0) st_dev_u32(c.status, st0 | ERR_TOKEN);  // keeps the bits already set
+        token = 0;
+      }
+    }
+    const uint16_t* row = a.embed + (size_t)token * H;
 #pragma unroll
     for (int k = 0; k < G::E; k += 8) {
       float v[8];
@@ -1221,7 +1232,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
           ok &= __hip_atomic_load(xw + X_DONE + (size_t)(lane * 4 + q) * 16 + 1, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT) == (u64)ep_end;
         if (__ballot(!ok) == 0) break;
-        if ((it & 63u) == 63u && ld_dev_u32(c.status) != 0) c.failed = true;
+        if ((it & 63u) == 63u && (ld_dev_u32(c.status) & ERR_DRAIN) != 0) c.failed = true;
         if (it > SPIN_LIMIT) { if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT); c.failed = true; }
       }
       u64 m = 0;
@@ -1337,27 +1348,19 @@ static hipError_t launch(KArgs& k, hipStream_t stream, bool cooperative) {
   return hipLaunchKernel(f, dim3(NWG), dim3(NT), args, 0, stream);
 }
 
-}  // namespace mk
-
-using namespace mk;
-
-extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const void* embed_weight,
-                                const void* lm_head_weight, const void* final_norm_weight,
-                                const void* layer_weights, const void* cos_table, const void* sin_table,
-                                void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
-                                int32_t* out_token, hipStream_t stream) {
+// Argument checks shared by the entry points (no HIP call); fills the launch arguments of one step
+// at `position` except the token fields.
+static hipError_t prepare(const mk_model_dims* dims, const void* embed_weight, const void* lm_head_weight,
+                          const void* final_norm_weight, const void* layer_weights, const void* cos_table,
+                          const void* sin_table, void* k_cache, void* v_cache, int position, int max_seq_len,
+                          float* logits, KArgs& k, bool& s06) {
   if (!dims || !embed_weight || !lm_head_weight || !final_norm_weight || !layer_weights || !cos_table ||
       !sin_table || !k_cache || !v_cache || !logits)
     return hipErrorInvalidValue;
-  const bool s06 = dims->hidden == 1024 && dims->intermediate == 3072;
+  s06 = dims->hidden == 1024 && dims->intermediate == 3072;
   const bool s17 = dims->hidden == 2048 && dims->intermediate == 6144;
   if (!(s06 || s17) || dims->num_layers < 1 || dims->num_layers > MAX_LAYERS || dims->vocab < NWG) return hipErrorInvalidValue;
-  if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
   if (max_seq_len < 1 || position < 0 || position >= max_seq_len) return hipErrorInvalidValue;
-  DeviceState* st = nullptr;
-  hipError_t e = device_state(&st);
-  if (e != hipSuccess) return e;
-  KArgs k;
   k.embed = (const uint16_t*)embed_weight;
   k.lm_head = (const uint16_t*)lm_head_weight;
   k.final_norm = (const uint16_t*)final_norm_weight;
@@ -1367,15 +1370,65 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.k_cache = (uint16_t*)k_cache;
   k.v_cache = (uint16_t*)v_cache;
   k.logits = logits;
-  k.out_token = out_token;
-  k.xw = (u64*)((char*)st->ws + (s06 ? 0 : WS_BYTES));
-  k.trace = st->trace;
-  k.token = token_id;
+  k.out_token = nullptr;
+  k.token_in = nullptr;
+  k.token = 0;
   k.position = position;
   k.max_seq = max_seq_len;
   k.num_layers = dims->num_layers;
   k.vocab = dims->vocab;
-  return s06 ? launch<1024, 3072>(k, stream, st->cooperative) : launch<2048, 6144>(k, stream, st->cooperative);
+  return hipSuccess;
+}
+
+static hipError_t launch_step(const KArgs& k, bool s06, const DeviceState* st, hipStream_t stream) {
+  KArgs a = k;
+  a.xw = (u64*)((char*)st->ws + (s06 ? 0 : WS_BYTES));
+  a.trace = st->trace;
+  return s06 ? launch<1024, 3072>(a, stream, st->cooperative) : launch<2048, 6144>(a, stream, st->cooperative);
+}
+
+}  // namespace mk
+
+using namespace mk;
+
+extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                                const void* lm_head_weight, const void* final_norm_weight,
+                                const void* layer_weights, const void* cos_table, const void* sin_table,
+                                void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
+                                int32_t* out_token, hipStream_t stream) {
+  KArgs k;
+  bool s06 = false;
+  hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
+                         k_cache, v_cache, position, max_seq_len, logits, k, s06);
+  if (e != hipSuccess) return e;
+  if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  k.token = token_id;
+  k.out_token = out_token;
+  return launch_step(k, s06, st, stream);
+}
+
+extern "C" hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens, int n, int generate,
+                                      const void* embed_weight, const void* lm_head_weight,
+                                      const void* final_norm_weight, const void* layer_weights,
+                                      const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                                      int position, int max_seq_len, float* logits, hipStream_t stream) {
+  KArgs k;
+  bool s06 = false;
+  hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
+                         k_cache, v_cache, position, max_seq_len, logits, k, s06);
+  if (e != hipSuccess) return e;
+  if (!tokens || n < 1 || (long long)position + n > max_seq_len) return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  for (int i = 0; i < n; ++i) {
+    k.position = position + i;
+    k.token_in = tokens + i;
+    k.out_token = (generate || i == n - 1) ? tokens + i + 1 : nullptr;
+    if ((e = launch_step(k, s06, st, stream)) != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 extern "C" hipError_t launch_decode_kernel(int token_id, const void* embed_weight, const void* lm_head_weight,

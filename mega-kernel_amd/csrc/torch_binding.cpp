@@ -162,6 +162,32 @@ std::tuple<torch::Tensor, torch::Tensor> decode_greedy(int64_t token_id, torch::
   return run(token_id, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len, true);
 }
 
+// Device-side multi-token loop (mk_decode_steps): n steps at position .. position + n - 1, each
+// reading its input token from tokens[i] (int32 [n + 1] on the weights' device). generate: step i
+// writes its greedy token to tokens[i + 1] for the next step; otherwise tokens[0..n-1] are inputs
+// and only tokens[n] is written. Returns the last step's logits; nothing synchronizes the host.
+torch::Tensor decode_steps(torch::Tensor tokens, int64_t n, bool generate, torch::Tensor embed, torch::Tensor lm_head,
+                           torch::Tensor final_norm, std::vector<torch::Tensor> lw, torch::Tensor cos,
+                           torch::Tensor sin, torch::Tensor kc, torch::Tensor vc, int64_t position,
+                           int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len);
+  TORCH_CHECK(n >= 1, "megakernel: n must be positive");
+  TORCH_CHECK(position + n <= max_seq_len, "megakernel: position + n (", position + n, ") exceeds max_seq_len (",
+              max_seq_len, ")");
+  TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
+                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) == n + 1,
+              "megakernel: tokens must be a contiguous int32 [n + 1] tensor on ", c.dev);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  const void* table = device_table(lw, c.dev, stream);
+  auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  MK_HIP_CHECK(mk_decode_steps(&c.dims, tokens.data_ptr<int32_t>(), (int)n, generate ? 1 : 0, embed.data_ptr(),
+                               lm_head.data_ptr(), final_norm.data_ptr(), table, cos.data_ptr(), sin.data_ptr(),
+                               kc.data_ptr(), vc.data_ptr(), (int)position, (int)max_seq_len,
+                               logits.data_ptr<float>(), stream));
+  return logits;
+}
+
 int64_t status() {
   uint32_t s = 0;
   MK_HIP_CHECK(mk_status(&s));
@@ -191,6 +217,9 @@ std::tuple<int64_t, int64_t, int64_t, int64_t> check_args(int64_t token_id, torc
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode", &decode, "Qwen3 single-token decode (fp32 logits)");
   m.def("decode_greedy", &decode_greedy, "Qwen3 single-token decode; returns (fp32 logits, int32 greedy token on device)");
+  m.def("decode_steps", &decode_steps,
+        "n decode steps with device-side tokens (int32 [n+1]); generate=True feeds each greedy token to the next "
+        "step without host synchronization; returns the last step's fp32 logits");
   m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
   m.def("reset", &reset, "clear the decode workspace (exchange words, status word) and restart its launch sequence; synchronizes");
   m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");

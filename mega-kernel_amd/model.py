@@ -13,8 +13,13 @@ Mirrors ``/root/reference/model.py`` step for step:
   * greedy loop calling the same ``decode`` entry point (``:95-127``), timed with device events.
     The fused device argmax (``decode_greedy``) replaces the separate ``argmax().item()`` per token;
     the host reads each token back only to feed the next call, as the reference does.
+  * ``--device-loop``: the same greedy generation as one ``decode_steps`` call, which feeds each
+    step's argmax to the next launch on the device; the host reads the tokens once at the end.
+  * ``--native-prefill``: the prompt goes through ``decode_steps`` in teacher mode from an empty
+    cache (one launch per prompt token) instead of the Transformers prefill and cache copy.
 
     python mega-kernel_amd/model.py [--shape qwen3-0.6b] [--prompt 32] [--max-seq 512] [--new 64]
+                                    [--device-loop] [--native-prefill]
 """
 import argparse
 import os
@@ -49,6 +54,9 @@ def main(argv=None):
     ap.add_argument("--prompt", type=int, default=32, help="random prompt length (token ids, seed 1)")
     ap.add_argument("--max-seq", type=int, default=512)
     ap.add_argument("--new", type=int, default=64, help="tokens to generate")
+    ap.add_argument("--device-loop", action="store_true", help="generate with one decode_steps call")
+    ap.add_argument("--native-prefill", action="store_true",
+                    help="fill the cache with decode_steps over the prompt instead of the Transformers prefill")
     a = ap.parse_args(argv)
     import torch
     import megakernel
@@ -62,26 +70,40 @@ def main(argv=None):
     final_norm = model.model.norm.weight.detach().to(dev)
     cos, sin = megakernel.rope_tables(model, a.max_seq, dev)
 
-    with torch.inference_mode():
-        out = model(ids, use_cache=True)
     k_cache, v_cache = megakernel.empty_cache(len(model.model.layers), a.max_seq, dev)
-    position = megakernel.copy_prefill_cache(out.past_key_values, k_cache, v_cache)
-    token = int(out.logits[0, -1].float().argmax())
+    if a.native_prefill:
+        prompt = torch.cat([ids[0], torch.zeros(1, dtype=ids.dtype)]).to(device=dev, dtype=torch.int32)
+        kernel.decode_steps(prompt, a.prompt, False, embed, embed, final_norm, layer_weights, cos, sin, k_cache,
+                            v_cache, 0, a.max_seq)
+        position, token = a.prompt, int(prompt[a.prompt].item())
+    else:
+        with torch.inference_mode():
+            out = model(ids, use_cache=True)
+        position = megakernel.copy_prefill_cache(out.past_key_values, k_cache, v_cache)
+        token = int(out.logits[0, -1].float().argmax())
 
     generated = [token]
     steps = min(a.new, a.max_seq - position)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(steps - 1):
-        _, tok = kernel.decode_greedy(token, embed, embed, final_norm, layer_weights, cos, sin, k_cache, v_cache,
-                                      position, a.max_seq)
-        token = int(tok.item())
-        generated.append(token)
-        position += 1
+    if a.device_loop and steps > 1:
+        tokens = torch.zeros(steps, dtype=torch.int32, device=dev)
+        tokens[0] = token
+        kernel.decode_steps(tokens, steps - 1, True, embed, embed, final_norm, layer_weights, cos, sin, k_cache,
+                            v_cache, position, a.max_seq)
+    else:
+        for _ in range(steps - 1):
+            _, tok = kernel.decode_greedy(token, embed, embed, final_norm, layer_weights, cos, sin, k_cache,
+                                          v_cache, position, a.max_seq)
+            token = int(tok.item())
+            generated.append(token)
+            position += 1
     end.record()
     end.synchronize()
     wall = time.perf_counter() - t0
+    if a.device_loop and steps > 1:
+        generated = tokens.tolist()
     n = max(steps - 1, 1)
     print(f"generated {len(generated)} tokens: {generated[:16]}{' ...' if len(generated) > 16 else ''}")
     print(f"decode: {start.elapsed_time(end) / n:.3f} ms/token (device events), {n / wall:.1f} tokens/s wall, "

@@ -78,6 +78,22 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib):
     g.argtypes = [ctypes.c_int] + [vp] * 18 + [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
     assert g(1, *([dummy] * 18), 10, 10, 512, None) == HIP_ERROR_INVALID_VALUE  # cache_len must be position + 1
 
+    # the device-side multi-token loop: n >= 1 steps that all fit in the cache, a token array
+    s = lib.mk_decode_steps
+    s.restype = ctypes.c_int
+    s.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int] + [vp] * 8 + [ctypes.c_int, ctypes.c_int, vp, vp]
+
+    def steps(dims=good, tokens=dummy, n=4, position=3, max_seq=512, generate=1):
+        d = ctypes.byref(dims) if dims is not None else None
+        return s(d, tokens, n, generate, *([dummy] * 8), position, max_seq, dummy, None)
+
+    assert steps(dims=None) == HIP_ERROR_INVALID_VALUE
+    assert steps(tokens=None) == HIP_ERROR_INVALID_VALUE
+    assert steps(n=0) == HIP_ERROR_INVALID_VALUE
+    assert steps(position=509, n=4) == HIP_ERROR_INVALID_VALUE  # the last step would write position 512
+    assert steps(position=509, n=4, generate=0) == HIP_ERROR_INVALID_VALUE
+    assert steps(Dims(2048, 3072, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+
 
 # ---------------------------------------------------------------------------------------------
 # the PyTorch operator (reference name and signature)
@@ -103,7 +119,7 @@ def _args(L=2, V=300, max_seq=16, dtype=torch.bfloat16):
 
 
 def test_operator_exports_reference_entry_point(ext):
-    assert callable(ext.decode) and callable(ext.decode_greedy)
+    assert callable(ext.decode) and callable(ext.decode_greedy) and callable(ext.decode_steps)
     assert ext.version().startswith("megakernel_amd")
 
 

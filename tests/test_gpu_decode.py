@@ -128,6 +128,94 @@ def test_mini_1_7b_shape_matches_fp32_restatement(mini17):
         tok = int(dev_tok.item())
 
 
+def _decode_steps(sess, tokens, n, generate, kd, vd, position):
+    return sess.kernel.decode_steps(tokens, n, generate, sess.embed, sess.lm_head, sess.final_norm, sess.layers,
+                                    sess.cos, sess.sin, kd, vd, position, sess.max_seq)
+
+
+def test_device_loop_matches_per_step_calls(mini):
+    """The device-side multi-token loop (``decode_steps``, C ABI ``mk_decode_steps``) in both modes
+    against a host loop of ``decode_greedy`` calls that reads each token back: the same kernel on the
+    same inputs, so the tokens, the last logits and the whole cache agree bit for bit. The 32 steps
+    from prompt 240 cross context 256, where the launches switch to two register K/V rows per
+    group."""
+    P, n = 240, 32
+    _, last, _, kc, vc = mini.prefill(P)
+    t0 = int(last.float().argmax())
+    ka, va = kc.to(DEV), vc.to(DEV)
+    toks, tok = [], t0
+    for i in range(n):
+        logits_a, dev_tok = mini.decode(tok, ka, va, P + i, greedy=True)
+        tok = int(dev_tok.item())
+        toks.append(tok)
+    print(f"[device-loop] host loop tokens {toks[:8]} ...", flush=True)
+
+    kb, vb = kc.to(DEV), vc.to(DEV)
+    tokens = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
+    tokens[0] = t0
+    logits_b = _decode_steps(mini, tokens, n, True, kb, vb, P)
+    assert tokens[1:].tolist() == toks
+    assert torch.equal(logits_b, logits_a)
+    assert torch.equal(kb, ka) and torch.equal(vb, va)
+    print("[device-loop] generate mode matches", flush=True)
+
+    # teacher mode on the same input tokens: same cache and logits, only tokens[n] written
+    kt, vt = kc.to(DEV), vc.to(DEV)
+    inputs = [t0] + toks[:-1]
+    teach = torch.tensor(inputs + [-5], dtype=torch.int32, device=DEV)
+    logits_c = _decode_steps(mini, teach, n, False, kt, vt, P)
+    assert teach[:n].tolist() == inputs and int(teach[n].item()) == toks[-1]
+    assert torch.equal(logits_c, logits_a)
+    assert torch.equal(kt, ka) and torch.equal(vt, va)
+    assert kt[:, :, P + n:].abs().sum().item() == 0
+    assert mini.kernel.status() == 0
+    print("[device-loop] teacher mode matches", flush=True)
+
+
+def test_native_prefill_through_decode_steps(mini):
+    """Prefill without Transformers: the prompt fed through ``decode_steps`` in teacher mode from an
+    empty cache writes the ``[L, 8, max_seq, 128]`` cache directly, one position per launch. Checked
+    against the fp32 restatement run the same way (one decode step per prompt token from an empty
+    cache): the cache rows within one bf16 rounding step, the last logits to 5e-3, the same greedy
+    token."""
+    P = 24
+    ids = hf.prompt_ids(P, mini.shape.vocab, seed=3)[0].tolist()
+    L, KV, D = mini.shape.layers, mini.shape.kv_heads, mini.shape.head_dim
+    kc = torch.zeros(L, KV, mini.max_seq, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    for p, tok in enumerate(ids):
+        want, _ = restate.decode_step(mini.W, kc, vc, tok, p, mini.cos_cpu, mini.sin_cpu, numerics="fp32")
+    kd, vd = torch.zeros_like(kc, device=DEV), torch.zeros_like(vc, device=DEV)
+    tokens = torch.tensor(ids + [-1], dtype=torch.int32, device=DEV)
+    got = _decode_steps(mini, tokens, P, False, kd, vd, 0).cpu()
+    maxabs, cos = _stats(got, want)
+    print(f"[native-prefill] P={P}: max|kernel - restatement| {maxabs:.3e}, cos {cos:.8f}", flush=True)
+    assert maxabs < 5e-3 and cos > 0.999999
+    assert int(tokens[P].item()) == restate.argmax_bf16(want)
+    for name, dev_c, ref_c in (("k", kd, kc), ("v", vd, vc)):
+        d = (dev_c[:, :, :P].float().cpu() - ref_c[:, :, :P].float()).abs().max().item()
+        assert d <= 2 ** -6 * max(1.0, ref_c.float().abs().max().item()), (name, d)
+    assert kd[:, :, P:].abs().sum().item() == 0 and vd[:, :, P:].abs().sum().item() == 0
+
+
+def test_device_loop_out_of_range_token_sets_status(mini):
+    """A device-side input token outside [0, vocab) cannot be checked on the host: the kernel decodes
+    token 0 instead (a normal launch, nothing drains) and sets status bit 2 until reset."""
+    P = 40
+    _, _, _, kc, vc = mini.prefill(P)
+    ka, va = kc.to(DEV), vc.to(DEV)
+    want = mini.decode(0, ka, va, P)
+    kb, vb = kc.to(DEV), vc.to(DEV)
+    tokens = torch.tensor([mini.shape.vocab + 5, -1], dtype=torch.int32, device=DEV)
+    try:
+        got = _decode_steps(mini, tokens, 1, True, kb, vb, P)
+        assert mini.kernel.status() == 4
+        assert torch.equal(got, want) and torch.equal(kb, ka)
+    finally:
+        mini.kernel.reset()
+    assert mini.kernel.status() == 0
+
+
 def test_decode_writes_only_its_slot(mini):
     """The K/V write touches exactly [layer, head, position, :] and nothing else."""
     P = 40
