@@ -523,7 +523,7 @@ struct Smem {
   uint16_t kvn[2][D];                // new K (normed, rotated) and V, bf16
   float cs[2][D];                    // cos, sin at position
   uint16_t nw[2][Geo<H, I>::NSLOT];  // per-layer norm weights by layer parity
-  float gp[NMW][2][D + 4];           // attention partials of the math waves: acc[128], m, l
+  float gq[MG][2][D + 4];            // attention partials of the 32 math groups: acc[128], m, l
   u64 best[NMW];
   uint32_t seq, wt;                  // launch sequence and write-through mode, set by the comm wave
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
@@ -641,10 +641,11 @@ struct Addr {
   }
 };
 
-// Split-K attention of this workgroup's split for one math wave (4 groups of 16 lanes, one key row
-// per group from registers; longer splits stream the rest), merged over the wave's groups into
-// sm.gp[mw]: per head acc[128], m, l. Online softmax per group for both query heads of the GQA pair,
-// so each K/V row is read once (/root/reference/megakernel.cu:228-370).
+// Split-K attention of this workgroup's split for one math wave (4 groups of 16 lanes, NKV key rows
+// per group from registers; longer splits stream the rest). Online softmax per group for both
+// query heads of the GQA pair, so each K/V row is read once (/root/reference/megakernel.cu:228-370);
+// each group leaves its partial (acc[128], m, l per head) in sm.gq[g] for one merge of all 32
+// groups after the next barrier.
 template <int H, int I, int NKV>
 __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, const Step& st, const Addr<H, I>& ad,
                                                 int layer, int mw, int lane, const uint4 (&kK)[NKV],
@@ -701,26 +702,17 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
       if (pu < st.p1) attend(pu == st.position ? knew : kw[u], pu == st.position ? vnew : vw[u], false);
     }
   }
-  // merge the wave's 4 groups (16-lane rows; lane t holds dims 8t..8t+7 in every row): common max,
-  // rescale, sum across rows. A group without keys has m = -inf, l = 0, acc = 0.
-  auto merge_rows = [&](float& m, float& l, float (&acc)[8]) {
-    float M = xmax32(xmax16(m));
-    const float f = M == -INFINITY ? 0.f : __expf(m - M);
-    l = xsum32(xsum16(l * f));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = xsum32(xsum16(acc[i] * f));
-    m = M;
-  };
+  // the group's partial as it stands (lane t holds dims 8t..8t+7); a group without keys leaves
+  // m = -inf, l = 0, acc = 0
   mark(a, tl + T_M_B_ATT, 64);
-  merge_rows(m0, l0, a0);
-  merge_rows(m1, l1, a1);
-  if (lane < 16) {
 #pragma unroll
-    for (int i = 0; i < 8; i += 4) {
-      *reinterpret_cast<float4*>(&sm.gp[mw][0][8 * t + i]) = make_float4(a0[i], a0[i + 1], a0[i + 2], a0[i + 3]);
-      *reinterpret_cast<float4*>(&sm.gp[mw][1][8 * t + i]) = make_float4(a1[i], a1[i + 1], a1[i + 2], a1[i + 3]);
-    }
-    if (t == 0) { sm.gp[mw][0][D] = m0; sm.gp[mw][0][D + 1] = l0; sm.gp[mw][1][D] = m1; sm.gp[mw][1][D + 1] = l1; }
+  for (int i = 0; i < 8; i += 4) {
+    *reinterpret_cast<float4*>(&sm.gq[g][0][8 * t + i]) = make_float4(a0[i], a0[i + 1], a0[i + 2], a0[i + 3]);
+    *reinterpret_cast<float4*>(&sm.gq[g][1][8 * t + i]) = make_float4(a1[i], a1[i + 1], a1[i + 2], a1[i + 3]);
+  }
+  if (t == 0) {
+    *reinterpret_cast<float2*>(&sm.gq[g][0][D]) = make_float2(m0, l0);
+    *reinterpret_cast<float2*>(&sm.gq[g][1][D]) = make_float2(m1, l1);
   }
 }
 
@@ -907,27 +899,38 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // issued only after this workgroup's attention partial is published: neither the attention nor
     // the publish queues behind them.
     mark(a, tl + T_M_B_END, 64);
-    lds_barrier();  // (B1) every wave's partial in sm.gp
-    {
-      // Publish this split's partial (workgroups without a split publish their unused slot too, so
-      // that every LL word is written at every layer): wave mw merges the 8 wave partials of head
-      // mw / 4, dims 32 (mw % 4) .. +32, lanes 0-7 four dims each. A wave without keys has
-      // m = -inf, l = 0, acc = 0 and weight exp(-inf) = 0.
-      const int h = mw >> 2, d0 = 32 * (mw & 3) + 4 * (lane & 7);
-      float M = -INFINITY;
+    lds_barrier();  // (B1) every group's partial in sm.gq
+    if (att) {
+      // Merge the 32 group partials and publish this split's: wave mw takes head mw / 4, dims
+      // 32 (mw % 4) .. +32. Lane = (subset sub of 4 groups, dim quad q4): each lane merges its 4
+      // groups for 4 dims, then the 8 subsets combine across lanes (xor 8, 16, 32) with a common
+      // max. Lanes 0-7 publish the head's 32 dims; lane 0 of waves 0 and 4 its (m, l).
+      const int h = mw >> 2, sub = lane >> 3, d0 = 32 * (mw & 3) + 4 * (lane & 7);
+      float m[4], l[4];
+      float4 p[4];
 #pragma unroll
-      for (int q = 0; q < NMW; ++q) M = fmaxf(M, sm.gp[q][h][D]);
-      mark(a, tl + T_B_MAX, 64);
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      float Ls = 0.f;
-#pragma unroll
-      for (int q = 0; q < NMW; ++q) {
-        const float f = __expf(sm.gp[q][h][D] - M);
-        const float4 pq = *reinterpret_cast<const float4*>(&sm.gp[q][h][d0]);
-        acc[0] = fmaf(pq.x, f, acc[0]); acc[1] = fmaf(pq.y, f, acc[1]);
-        acc[2] = fmaf(pq.z, f, acc[2]); acc[3] = fmaf(pq.w, f, acc[3]);
-        Ls = fmaf(sm.gp[q][h][D + 1], f, Ls);
+      for (int k = 0; k < 4; ++k) {
+        const float2 ml = *reinterpret_cast<const float2*>(&sm.gq[4 * sub + k][h][D]);
+        m[k] = ml.x; l[k] = ml.y;
+        p[k] = *reinterpret_cast<const float4*>(&sm.gq[4 * sub + k][h][d0]);
       }
+      float M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+      M = fmaxf(M, dpp<0x128>(M));  // row_ror:8 == lane ^ 8 inside a 16-lane row
+      M = xmax32(xmax16(M));        // every split has a key, so M is finite
+      mark(a, tl + T_B_MAX, 64);
+      float Ls = 0.f;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float f = __expf(m[k] - M);  // 0 for a group without keys
+        Ls = fmaf(l[k], f, Ls);
+        acc[0] = fmaf(p[k].x, f, acc[0]); acc[1] = fmaf(p[k].y, f, acc[1]);
+        acc[2] = fmaf(p[k].z, f, acc[2]); acc[3] = fmaf(p[k].w, f, acc[3]);
+      }
+      auto sub_sum = [](float v) { v += dpp<0x128>(v); return xsum32(xsum16(v)); };
+      Ls = sub_sum(Ls);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = sub_sum(acc[i]);
       Comm c;
       c.wt = sm.wt != 0;
       const uint32_t ep = ll_epoch(sm.seq, layer);
