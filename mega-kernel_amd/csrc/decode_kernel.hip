@@ -808,14 +808,22 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     for (int q = lane; q < G::NSL16; q += 64) reinterpret_cast<uint4*>(sm.nw[0])[q] = ld_global16(slot_chunk(0, q));
 
   // Loads of phase Q's registers (A=0: QKV, B=1: K/V rows, C=2: o_proj, D=3: gate/up, E=4: down)
-  // for `layer`; past the last layer they re-read the last one. Every path issues the same loads
-  // in the same order, so the compiler's wait counts stay exact (a load under a data-dependent
-  // condition would make it wait for all outstanding loads). Phase P of layer l issues the loads
+  // for `layer`; past the last layer they re-read the last one. Every path issues the same weight
+  // loads in the same order, so the compiler's wait counts stay exact (a load under a
+  // data-dependent condition makes later waits count it as possibly absent, i.e. stricter). Phase P of layer l issues the loads
   // of phase P + DIST (of layer l, or of layer l + 1 when it wraps): DIST sets how many phases'
   // weights each CU keeps in flight.
   // Past the last layer the loads still issue (same count, so the wait counts stay exact) but every
   // row reads the final norm's 2-4 KB, which stays in L2: no weight traffic for a layer that never
   // runs.
+#ifndef MK_KV_PRED
+#define MK_KV_PRED (H <= 1024)
+#endif
+  // K/V rows: a slot this workgroup's split does not attend to (or a workgroup without a split)
+  // skips its load. The compiler then counts these two loads as possibly absent, which makes a few
+  // later waits one or two loads stricter; worth it at the 0.6B shape (387 vs 395 us per token at
+  // config 2), not at 1.7B (868 vs 864).
+  constexpr bool KV_PRED = MK_KV_PRED;
   auto load_phase = [&](auto qc, int layer) {
     constexpr int Q = decltype(qc)::value;
     const bool past = layer >= L;
@@ -828,8 +836,11 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (Q == 1) {
 #pragma unroll
       for (int r = 0; r < NKV; ++r) {
-        kK[r] = ld_stream(kv_row(a.k_cache, layer, kv_pos(r)));
-        kV[r] = ld_stream(kv_row(a.v_cache, layer, kv_pos(r)));
+        const int pr = st.p0 + g + MG * r;
+        if (!KV_PRED || opaque(att && pr < st.p1 && pr != st.position ? 1 : 0)) {
+          kK[r] = ld_stream(kv_row(a.k_cache, layer, pr));
+          kV[r] = ld_stream(kv_row(a.v_cache, layer, pr));
+        }
       }
     }
     if constexpr (Q == 2) tile_load<TC, TC::PS>(wC, 0, mwq, lq, sel(rows_C(lw)));

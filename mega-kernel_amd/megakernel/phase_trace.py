@@ -114,7 +114,8 @@ def hop_report(t, layers, nxcd=8):
         bpub, bpoll = col(layer, "B pub (partial)"), col(layer, "B poll (merge)")
         att = t[:, TRACE_PER_LAYER * layer + idx["math B scores done"]] != 0
         wb = np.array([bpub[(x == v) & att].max() if ((x == v) & att).any() else bpub[x == v].max() for v in x])
-        add("B  split partials (local)", bpoll - wb, bpoll - bpub)
+        # only the split workgroups publish; `own` is theirs
+        add("B  split partials (local)", bpoll - wb, (bpoll - bpub)[att] if att.any() else bpoll - bpub)
         for ph in "CE":
             pub, cp, lp = col(layer, f"{ph} pub"), col(layer, f"{ph} cross poll"), col(layer, f"{ph} local poll")
             wj = np.array([pub[j == v].max() for v in j])
