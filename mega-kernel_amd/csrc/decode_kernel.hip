@@ -1508,4 +1508,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.8 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.9 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop)"; }
