@@ -109,9 +109,27 @@ hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens, int n, in
                            const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
                            int position, int max_seq_len, float* logits, hipStream_t stream);
 
+/*
+ * mk_decode on a paged K/V cache. k_pages / v_pages are bf16 [num_layers][num_pages][8][page_size][128]:
+ * the rows of positions [i * page_size, (i + 1) * page_size) of every layer and K/V head live in
+ * page block_table[i] (int32 device array of ceil(max_seq_len / page_size) entries; only entries up
+ * to position are read). page_size is a power of two up to 4096, and ceil(max_seq_len / page_size)
+ * at most 2048. The new K/V rows are written at `position`, through the table. An entry outside
+ * [0, num_pages) reads page 0 instead and sets status bit 3 (see mk_status). Other arguments and
+ * errors as mk_decode. No reference counterpart: the reference's cache is contiguous
+ * (/root/reference/model.py:79-87); this serves callers whose cache is a shared pool of pages.
+ */
+hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                           const void* lm_head_weight, const void* final_norm_weight,
+                           const void* layer_weights, const void* cos_table, const void* sin_table,
+                           void* k_pages, void* v_pages, const int32_t* block_table, int num_pages,
+                           int page_size, int position, int max_seq_len, float* logits,
+                           int32_t* out_token, hipStream_t stream);
+
 /* Device status word of the current device's workspace (0 = healthy; bit 0 = a grid wait timed
  * out, results of that launch are invalid; bit 2 = a device-side input token of mk_decode_steps
- * was out of range; decoding went on with token 0). A timeout makes later launches drain early
+ * was out of range; decoding went on with token 0; bit 3 = a block-table entry of
+ * mk_decode_paged was out of range; page 0 was used). A timeout makes later launches drain early
  * until mk_reset.
  * Synchronizes with the device. No reference counterpart: the reference surfaces errors only
  * through the launch status. */

@@ -81,7 +81,9 @@ constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr uint32_t ERR_TIMEOUT = 1u;
 constexpr uint32_t ERR_PLACEMENT = 2u;
 constexpr uint32_t ERR_TOKEN = 4u;  // a device-side input token was out of range (token 0 used)
-constexpr uint32_t ERR_DRAIN = ~ERR_TOKEN;  // status bits that make the waits give up (a bad token does not)
+constexpr uint32_t ERR_PAGE = 8u;   // a block-table entry was out of range (page 0 used)
+constexpr uint32_t ERR_DRAIN = ~(ERR_TOKEN | ERR_PAGE);  // status bits that make the waits give up
+constexpr int MAX_PAGES = 2048;     // block-table entries a paged launch may use (LDS copy)
 #ifndef MK_PF_DIST
 #define MK_PF_DIST 2
 #endif
@@ -123,6 +125,10 @@ struct KArgs {
   float* logits;
   int32_t* out_token;
   const int32_t* token_in;  // when set, the input token is read here (written by an earlier launch)
+  // Paged K/V cache (block_table set): k_cache/v_cache are [L][num_pages][HKV][page][D] and the
+  // rows of positions [i * page, (i + 1) * page) live in page block_table[i]; page = 1 << page_shift.
+  const int32_t* block_table;
+  int num_pages, page_shift;
   u64* xw;          // exchange workspace
   uint64_t* trace;  // optional: per-workgroup phase timestamps (TRACE_N per workgroup)
   int token, position, max_seq, num_layers, vocab;
@@ -527,7 +533,18 @@ struct Smem {
   u64 best[NMW];
   uint32_t seq, wt;                  // launch sequence and write-through mode, set by the comm wave
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
+  int32_t bt[MAX_PAGES];             // block table of a paged launch (entries up to the position)
 };
+
+// Element offset of the K/V row of `head` at position p in layer `layer`: contiguous
+// [L][HKV][max_seq][D] cache, or the paged layout through the block table's LDS copy.
+__device__ __forceinline__ size_t kv_off(const KArgs& a, const int32_t* bt, int layer, int head, int p) {
+  if (a.block_table) {
+    const size_t page = (size_t)bt[p >> a.page_shift];
+    return (((((size_t)layer * a.num_pages + page) * HKV + head) << a.page_shift) + (p & ((1 << a.page_shift) - 1))) * D;
+  }
+  return (((size_t)layer * HKV + head) * a.max_seq + p) * D;
+}
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
 // outstanding global loads (a full __syncthreads fence would also wait for the weight loads that
@@ -621,7 +638,7 @@ struct Addr {
   }
   // first 16-byte chunk of the K/V row of position p of this XCD's head
   __device__ const uint4* kv_row(const uint16_t* cache, int layer, int p) const {
-    return reinterpret_cast<const uint4*>(cache + (((size_t)layer * HKV + st.xcd) * a.max_seq + p) * D);
+    return reinterpret_cast<const uint4*>(cache + kv_off(a, sm.bt, layer, st.xcd, p));
   }
   // position math group g attends to from registers, slot r: p0 + g + MG*r; unused slots re-read p0
   __device__ int kv_pos(int g, int r) const {
@@ -763,13 +780,25 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
   if (lane == 0) sm.best[mw] = best;
 }
 
-// Copies the layer table into LDS (math waves, before the first barrier).
+// Copies the layer table, and for a paged launch the block-table entries up to the position, into
+// LDS (math waves, before the first barrier). An entry outside [0, num_pages) reads page 0 instead
+// and sets the status bit ERR_PAGE, so no access leaves the page pool.
 template <int H, int I>
 __device__ __forceinline__ void copy_layer_table(const KArgs& a, Smem<H, I>& sm) {
   constexpr int TW = (int)(sizeof(mk_layer_weights) / 8);
   const int n = a.num_layers * TW;
   for (int i = threadIdx.x - 64; i < n; i += NT - 64)
     reinterpret_cast<u64*>(sm.layers)[i] = reinterpret_cast<const u64*>(a.layers)[i];
+  if (a.block_table) {
+    const int np = (a.position >> a.page_shift) + 1;
+    bool bad = false;
+    for (int i = threadIdx.x - 64; i < np; i += NT - 64) {
+      const int v = a.block_table[i];
+      bad |= v < 0 || v >= a.num_pages;
+      sm.bt[i] = (v < 0 || v >= a.num_pages) ? 0 : v;
+    }
+    if (bad) st_dev_u32(reinterpret_cast<uint32_t*>(a.xw + X_STATUS), ERR_PAGE);
+  }
 }
 
 // ---- math waves ------------------------------------------------------------------------------
@@ -836,10 +865,15 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (Q == 1) {
 #pragma unroll
       for (int r = 0; r < NKV; ++r) {
-        const int pr = st.p0 + g + MG * r;
-        if (!KV_PRED || opaque(att && pr < st.p1 && pr != st.position ? 1 : 0)) {
-          kK[r] = ld_stream(kv_row(a.k_cache, layer, pr));
-          kV[r] = ld_stream(kv_row(a.v_cache, layer, pr));
+        if constexpr (KV_PRED) {
+          const int pr = st.p0 + g + MG * r;
+          if (opaque(att && pr < st.p1 && pr != st.position ? 1 : 0)) {
+            kK[r] = ld_stream(kv_row(a.k_cache, layer, pr));
+            kV[r] = ld_stream(kv_row(a.v_cache, layer, pr));
+          }
+        } else {  // unconditional: a slot outside the split re-reads its first row (never past position)
+          kK[r] = ld_stream(kv_row(a.k_cache, layer, kv_pos(r)));
+          kV[r] = ld_stream(kv_row(a.v_cache, layer, kv_pos(r)));
         }
       }
     }
@@ -1091,7 +1125,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
         *reinterpret_cast<u4v*>(&sm.kvn[part - 2][8 * tt]) = pk;
         if (j == S - 1) {  // the split that owns `position` stores the new K/V in the cache
           uint16_t* cache = part == 2 ? a.k_cache : a.v_cache;
-          *gpw(reinterpret_cast<u4v*>(cache + (((size_t)layer * HKV + xcd) * a.max_seq + st.position) * D + 8 * tt)) = pk;
+          *gpw(reinterpret_cast<u4v*>(cache + kv_off(a, sm.bt, layer, xcd, st.position) + 8 * tt)) = pk;
         }
       }
     }
@@ -1386,6 +1420,9 @@ static hipError_t prepare(const mk_model_dims* dims, const void* embed_weight, c
   k.logits = logits;
   k.out_token = nullptr;
   k.token_in = nullptr;
+  k.block_table = nullptr;
+  k.num_pages = 0;
+  k.page_shift = 0;
   k.token = 0;
   k.position = position;
   k.max_seq = max_seq_len;
@@ -1420,6 +1457,33 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   if ((e = device_state(&st)) != hipSuccess) return e;
   k.token = token_id;
   k.out_token = out_token;
+  return launch_step(k, s06, st, stream);
+}
+
+extern "C" hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                                      const void* lm_head_weight, const void* final_norm_weight,
+                                      const void* layer_weights, const void* cos_table, const void* sin_table,
+                                      void* k_pages, void* v_pages, const int32_t* block_table, int num_pages,
+                                      int page_size, int position, int max_seq_len, float* logits,
+                                      int32_t* out_token, hipStream_t stream) {
+  KArgs k;
+  bool s06 = false;
+  hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
+                         k_pages, v_pages, position, max_seq_len, logits, k, s06);
+  if (e != hipSuccess) return e;
+  if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
+  int shift = 0;
+  while (shift < 12 && (1 << shift) < page_size) ++shift;
+  if (!block_table || num_pages < 1 || page_size < 1 || (1 << shift) != page_size ||
+      (max_seq_len + page_size - 1) / page_size > MAX_PAGES)
+    return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  k.token = token_id;
+  k.out_token = out_token;
+  k.block_table = block_table;
+  k.num_pages = num_pages;
+  k.page_shift = shift;
   return launch_step(k, s06, st, stream);
 }
 

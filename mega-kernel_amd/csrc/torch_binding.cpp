@@ -58,7 +58,8 @@ struct Checked {
 Checked validate(int64_t token_id, const torch::Tensor& embed, const torch::Tensor& lm_head,
                  const torch::Tensor& final_norm, const std::vector<torch::Tensor>& lw,
                  const torch::Tensor& cos, const torch::Tensor& sin, const torch::Tensor& kc,
-                 const torch::Tensor& vc, int64_t position, int64_t max_seq_len, bool require_gpu = true) {
+                 const torch::Tensor& vc, int64_t position, int64_t max_seq_len, bool require_gpu = true,
+                 bool paged = false) {
   TORCH_CHECK(embed.defined(), "megakernel: embed_weight is undefined");
   TORCH_CHECK(!require_gpu || embed.is_cuda(), "megakernel: embed_weight must be a GPU tensor");
   TORCH_CHECK(embed.dim() == 2, "megakernel: embed_weight must be [vocab, hidden]");
@@ -94,8 +95,10 @@ Checked validate(int64_t token_id, const torch::Tensor& embed, const torch::Tens
   check_bf16(sin, "sin_table", {sin.size(0), kHeadDim}, dev);
   TORCH_CHECK(cos.size(0) >= max_seq_len && sin.size(0) >= max_seq_len,
               "megakernel: cos/sin tables need at least max_seq_len rows");
-  check_bf16(kc, "k_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
-  check_bf16(vc, "v_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
+  if (!paged) {
+    check_bf16(kc, "k_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
+    check_bf16(vc, "v_cache", {L, kKVHeads, max_seq_len, kHeadDim}, dev);
+  }
   TORCH_CHECK(kc.data_ptr() != vc.data_ptr(), "megakernel: k_cache and v_cache must be distinct");
   TORCH_CHECK(position >= 0 && position < max_seq_len, "megakernel: position ", position,
               " out of range [0, ", max_seq_len, ")");
@@ -188,6 +191,38 @@ torch::Tensor decode_steps(torch::Tensor tokens, int64_t n, bool generate, torch
   return logits;
 }
 
+// Paged-cache decode (mk_decode_paged): k_pages / v_pages bf16 [L, num_pages, 8, page_size, 128],
+// block_table int32 [>= ceil(max_seq_len / page_size)] on the same device; page_size a power of two.
+// Returns (fp32 logits [V], int32 greedy token on the device).
+std::tuple<torch::Tensor, torch::Tensor> decode_paged(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
+                                                      torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                      torch::Tensor cos, torch::Tensor sin, torch::Tensor kp,
+                                                      torch::Tensor vp, torch::Tensor block_table, int64_t position,
+                                                      int64_t max_seq_len) {
+  Checked c = validate(token_id, embed, lm_head, final_norm, lw, cos, sin, kp, vp, position, max_seq_len, true, true);
+  TORCH_CHECK(kp.defined() && kp.dim() == 5, "megakernel: k_pages must be [layers, num_pages, 8, page_size, 128]");
+  const int64_t L = c.dims.num_layers, NP = kp.size(1), PS = kp.size(3);
+  TORCH_CHECK(PS >= 1 && PS <= 4096 && (PS & (PS - 1)) == 0, "megakernel: page_size must be a power of two <= 4096");
+  check_bf16(kp, "k_pages", {L, NP, kKVHeads, PS, kHeadDim}, c.dev);
+  check_bf16(vp, "v_pages", {L, NP, kKVHeads, PS, kHeadDim}, c.dev);
+  TORCH_CHECK(kp.data_ptr() != vp.data_ptr(), "megakernel: k_pages and v_pages must be distinct");
+  const int64_t need = (max_seq_len + PS - 1) / PS;
+  TORCH_CHECK(need <= 2048, "megakernel: ceil(max_seq_len / page_size) must be at most 2048");
+  TORCH_CHECK(block_table.defined() && block_table.device() == c.dev && block_table.scalar_type() == torch::kInt32 &&
+                  block_table.is_contiguous() && block_table.dim() == 1 && block_table.size(0) >= need,
+              "megakernel: block_table must be a contiguous int32 tensor of >= ", need, " entries on ", c.dev);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  const void* table = device_table(lw, c.dev, stream);
+  auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  auto tok = torch::empty({1}, embed.options().dtype(torch::kInt32));
+  MK_HIP_CHECK(mk_decode_paged(&c.dims, (int)token_id, embed.data_ptr(), lm_head.data_ptr(), final_norm.data_ptr(),
+                               table, cos.data_ptr(), sin.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                               block_table.data_ptr<int32_t>(), (int)NP, (int)PS, (int)position, (int)max_seq_len,
+                               logits.data_ptr<float>(), tok.data_ptr<int32_t>(), stream));
+  return {logits, tok};
+}
+
 int64_t status() {
   uint32_t s = 0;
   MK_HIP_CHECK(mk_status(&s));
@@ -220,6 +255,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_steps", &decode_steps,
         "n decode steps with device-side tokens (int32 [n+1]); generate=True feeds each greedy token to the next "
         "step without host synchronization; returns the last step's fp32 logits");
+  m.def("decode_paged", &decode_paged,
+        "decode on a paged K/V cache ([L, pages, 8, page_size, 128] + int32 block table); returns (fp32 logits, "
+        "int32 greedy token on device)");
   m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
   m.def("reset", &reset, "clear the decode workspace (exchange words, status word) and restart its launch sequence; synchronizes");
   m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");

@@ -94,6 +94,23 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib):
     assert steps(position=509, n=4, generate=0) == HIP_ERROR_INVALID_VALUE
     assert steps(Dims(2048, 3072, 28, 151936)) == HIP_ERROR_INVALID_VALUE
 
+    # the paged cache: a block table, a power-of-two page size, at most 2048 table entries
+    pg = lib.mk_decode_paged
+    pg.restype = ctypes.c_int
+    pg.argtypes = [vp, ctypes.c_int] + [vp] * 9 + [ctypes.c_int] * 4 + [vp, vp, vp]
+
+    def paged(table=dummy, num_pages=64, page=16, position=3, max_seq=512, token=1):
+        return pg(ctypes.byref(good), token, *([dummy] * 8), table, num_pages, page, position, max_seq, dummy,
+                  None, None)
+
+    assert paged(table=None) == HIP_ERROR_INVALID_VALUE
+    assert paged(num_pages=0) == HIP_ERROR_INVALID_VALUE
+    assert paged(page=24) == HIP_ERROR_INVALID_VALUE
+    assert paged(page=8192) == HIP_ERROR_INVALID_VALUE
+    assert paged(page=1, max_seq=4096) == HIP_ERROR_INVALID_VALUE  # 4096 table entries > 2048
+    assert paged(position=512) == HIP_ERROR_INVALID_VALUE
+    assert paged(token=151936) == HIP_ERROR_INVALID_VALUE
+
 
 # ---------------------------------------------------------------------------------------------
 # the PyTorch operator (reference name and signature)
@@ -120,6 +137,7 @@ def _args(L=2, V=300, max_seq=16, dtype=torch.bfloat16):
 
 def test_operator_exports_reference_entry_point(ext):
     assert callable(ext.decode) and callable(ext.decode_greedy) and callable(ext.decode_steps)
+    assert callable(ext.decode_paged)
     assert ext.version().startswith("megakernel_amd")
 
 

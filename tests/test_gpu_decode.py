@@ -198,6 +198,64 @@ def test_native_prefill_through_decode_steps(mini):
     assert kd[:, :, P:].abs().sum().item() == 0 and vd[:, :, P:].abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("shape_fixture, P", [("mini", 300), ("mini17", 300), ("mini17", 488)])
+def test_paged_cache_matches_contiguous(shape_fixture, P, request):
+    """``decode_paged`` (C ABI ``mk_decode_paged``) on a pool of 16-position pages in shuffled order,
+    with the unused pages filled with NaN, against ``decode_greedy`` on the contiguous cache: the
+    same kernel arithmetic through another address map, so logits and tokens agree bit for bit and
+    the rows written through the table land where the contiguous launch writes them. 24 steps from
+    prompt 300 cross page boundaries and context 256 (two register K/V rows, longer splits); from
+    prompt 488 they end on the cache's last slot (511), where a K/V row read past the split would
+    leave the last page (regression: such reads once took block-table entries past the position)."""
+    from tests.paged_layout import from_pages, to_pages
+    sess = request.getfixturevalue(shape_fixture)
+    n, ps = 24, 16
+    _, last, _, kc, vc = sess.prefill(P)
+    npl = sess.max_seq // ps
+    g = torch.Generator().manual_seed(7)
+    pool = npl + 9
+    table = torch.randperm(pool, generator=g)[:npl].to(torch.int32)
+    kp = to_pages(kc, ps, table.tolist(), pool).to(DEV)
+    vp = to_pages(vc, ps, table.tolist(), pool).to(DEV)
+    table_d = table.to(DEV)
+    ka, va = kc.to(DEV), vc.to(DEV)
+    tok = int(last.float().argmax())
+    for i in range(n):
+        la, ta = sess.decode(tok, ka, va, P + i, greedy=True)
+        lb, tb = sess.kernel.decode_paged(tok, sess.embed, sess.lm_head, sess.final_norm, sess.layers, sess.cos,
+                                          sess.sin, kp, vp, table_d, P + i, sess.max_seq)
+        assert torch.equal(la, lb), f"step {i}: paged logits differ"
+        assert int(ta.item()) == int(tb.item())
+        tok = int(ta.item())
+    print(f"[paged {shape_fixture}] {n} steps from P={P}, page 16: identical logits and tokens", flush=True)
+    assert torch.equal(from_pages(kp, table.tolist()), ka) and torch.equal(from_pages(vp, table.tolist()), va)
+    unused = sorted(set(range(pool)) - set(table.tolist()))
+    assert torch.isnan(kp[:, unused].float()).all() and torch.isnan(vp[:, unused].float()).all()
+    assert sess.kernel.status() == 0
+
+
+def test_paged_cache_bad_table_entry_sets_status(mini):
+    """A block-table entry outside the page pool cannot be checked on the host without a copy: the
+    kernel reads and writes page 0 instead (no access leaves the pool, nothing drains) and sets
+    status bit 3 until reset."""
+    from tests.paged_layout import to_pages
+    P, ps = 40, 16
+    _, _, _, kc, vc = mini.prefill(P)
+    npl = mini.max_seq // ps
+    table = torch.arange(npl, dtype=torch.int32)
+    table[P // ps] = npl + 5  # the page holding the position being written
+    kp = to_pages(kc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
+    vp = to_pages(vc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
+    try:
+        logits, _ = mini.kernel.decode_paged(7, mini.embed, mini.lm_head, mini.final_norm, mini.layers, mini.cos,
+                                             mini.sin, kp, vp, table.to(DEV), P, mini.max_seq)
+        assert mini.kernel.status() == 8
+        assert torch.isfinite(logits).all()
+    finally:
+        mini.kernel.reset()
+    assert mini.kernel.status() == 0
+
+
 def test_device_loop_out_of_range_token_sets_status(mini):
     """A device-side input token outside [0, vocab) cannot be checked on the host: the kernel decodes
     token 0 instead (a normal launch, nothing drains) and sets status bit 2 until reset."""

@@ -233,3 +233,17 @@ def test_weight_bytes_per_token(name, expected):
     assert counted == expected
     assert s.kv_bytes_per_position() == 114_688
     assert s.bytes_per_token(288) == expected + 114_688 * 289 + 512
+
+
+def test_paged_layout_helpers():
+    """The page layout used by the paged-cache GPU tests: position p of layer l, head h sits at
+    pages[l, table[p // page], h, p % page]; scatter then gather is the identity."""
+    from tests.paged_layout import from_pages, to_pages
+    L, KV, S, D, ps = 2, 8, 64, 4, 16
+    cache = torch.arange(L * KV * S * D, dtype=torch.float32).view(L, KV, S, D)
+    table = [3, 0, 5, 1]
+    pages = to_pages(cache, ps, table, num_pages=7)
+    for l, h, p in ((0, 0, 0), (1, 7, 63), (0, 3, 17), (1, 2, 40)):
+        assert torch.equal(pages[l, table[p // ps], h, p % ps], cache[l, h, p])
+    assert torch.isnan(pages[:, 2]).all() and torch.isnan(pages[:, 4]).all() and torch.isnan(pages[:, 6]).all()
+    assert torch.equal(from_pages(pages, table), cache)
