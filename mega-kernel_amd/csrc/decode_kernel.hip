@@ -1040,9 +1040,6 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   float res[G::E];
 
   lds_barrier();  // (P0)
-#ifdef MK_COMM_PRIO
-  __builtin_amdgcn_s_setprio(MK_COMM_PRIO);  // the comm wave's instructions issue ahead of math waves'
-#endif
   const uint32_t seq = ld_dev_u32(reinterpret_cast<const uint32_t*>(xw + X_SEQ));
   const uint32_t st0 = ld_dev_u32(c.status);
   {
@@ -1572,4 +1569,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.9 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.10 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop, paged cache)"; }
