@@ -126,6 +126,16 @@ hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, const void* 
                            int page_size, int position, int max_seq_len, float* logits,
                            int32_t* out_token, hipStream_t stream);
 
+/* mk_decode_steps on a paged K/V cache (layout, table and limits as mk_decode_paged): the
+ * device-side multi-token loop for callers that keep their cache in pages. No reference
+ * counterpart (see mk_decode_steps and mk_decode_paged). */
+hipError_t mk_decode_steps_paged(const mk_model_dims* dims, int32_t* tokens, int n, int generate,
+                                 const void* embed_weight, const void* lm_head_weight,
+                                 const void* final_norm_weight, const void* layer_weights,
+                                 const void* cos_table, const void* sin_table, void* k_pages, void* v_pages,
+                                 const int32_t* block_table, int num_pages, int page_size, int position,
+                                 int max_seq_len, float* logits, hipStream_t stream);
+
 /* Device status word of the current device's workspace (0 = healthy; bit 0 = a grid wait timed
  * out, results of that launch are invalid; bit 2 = a device-side input token of mk_decode_steps
  * was out of range; decoding went on with token 0; bit 3 = a block-table entry of

@@ -1457,6 +1457,36 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   return launch_step(k, s06, st, stream);
 }
 
+// Page-table checks and fields of a paged launch (page size a power of two up to 4096, at most
+// MAX_PAGES table entries for max_seq_len positions).
+static hipError_t set_paged(KArgs& k, const int32_t* block_table, int num_pages, int page_size, int max_seq_len) {
+  int shift = 0;
+  while (shift < 12 && (1 << shift) < page_size) ++shift;
+  if (!block_table || num_pages < 1 || page_size < 1 || (1 << shift) != page_size ||
+      (max_seq_len + page_size - 1) / page_size > MAX_PAGES)
+    return hipErrorInvalidValue;
+  k.block_table = block_table;
+  k.num_pages = num_pages;
+  k.page_shift = shift;
+  return hipSuccess;
+}
+
+// n launches at positions position .. position + n - 1 with device-side tokens (see mk_decode_steps).
+static hipError_t run_steps(KArgs& k, bool s06, int32_t* tokens, int n, int generate, int position,
+                            int max_seq_len, hipStream_t stream) {
+  if (!tokens || n < 1 || (long long)position + n > max_seq_len) return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  hipError_t e = device_state(&st);
+  if (e != hipSuccess) return e;
+  for (int i = 0; i < n; ++i) {
+    k.position = position + i;
+    k.token_in = tokens + i;
+    k.out_token = (generate || i == n - 1) ? tokens + i + 1 : nullptr;
+    if ((e = launch_step(k, s06, st, stream)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 extern "C" hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, const void* embed_weight,
                                       const void* lm_head_weight, const void* final_norm_weight,
                                       const void* layer_weights, const void* cos_table, const void* sin_table,
@@ -1469,18 +1499,11 @@ extern "C" hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, c
                          k_pages, v_pages, position, max_seq_len, logits, k, s06);
   if (e != hipSuccess) return e;
   if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
-  int shift = 0;
-  while (shift < 12 && (1 << shift) < page_size) ++shift;
-  if (!block_table || num_pages < 1 || page_size < 1 || (1 << shift) != page_size ||
-      (max_seq_len + page_size - 1) / page_size > MAX_PAGES)
-    return hipErrorInvalidValue;
+  if ((e = set_paged(k, block_table, num_pages, page_size, max_seq_len)) != hipSuccess) return e;
   DeviceState* st = nullptr;
   if ((e = device_state(&st)) != hipSuccess) return e;
   k.token = token_id;
   k.out_token = out_token;
-  k.block_table = block_table;
-  k.num_pages = num_pages;
-  k.page_shift = shift;
   return launch_step(k, s06, st, stream);
 }
 
@@ -1494,16 +1517,22 @@ extern "C" hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens
   hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
                          k_cache, v_cache, position, max_seq_len, logits, k, s06);
   if (e != hipSuccess) return e;
-  if (!tokens || n < 1 || (long long)position + n > max_seq_len) return hipErrorInvalidValue;
-  DeviceState* st = nullptr;
-  if ((e = device_state(&st)) != hipSuccess) return e;
-  for (int i = 0; i < n; ++i) {
-    k.position = position + i;
-    k.token_in = tokens + i;
-    k.out_token = (generate || i == n - 1) ? tokens + i + 1 : nullptr;
-    if ((e = launch_step(k, s06, st, stream)) != hipSuccess) return e;
-  }
-  return hipSuccess;
+  return run_steps(k, s06, tokens, n, generate, position, max_seq_len, stream);
+}
+
+extern "C" hipError_t mk_decode_steps_paged(const mk_model_dims* dims, int32_t* tokens, int n, int generate,
+                                            const void* embed_weight, const void* lm_head_weight,
+                                            const void* final_norm_weight, const void* layer_weights,
+                                            const void* cos_table, const void* sin_table, void* k_pages,
+                                            void* v_pages, const int32_t* block_table, int num_pages, int page_size,
+                                            int position, int max_seq_len, float* logits, hipStream_t stream) {
+  KArgs k;
+  bool s06 = false;
+  hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
+                         k_pages, v_pages, position, max_seq_len, logits, k, s06);
+  if (e != hipSuccess) return e;
+  if ((e = set_paged(k, block_table, num_pages, page_size, max_seq_len)) != hipSuccess) return e;
+  return run_steps(k, s06, tokens, n, generate, position, max_seq_len, stream);
 }
 
 extern "C" hipError_t launch_decode_kernel(int token_id, const void* embed_weight, const void* lm_head_weight,

@@ -191,15 +191,15 @@ torch::Tensor decode_steps(torch::Tensor tokens, int64_t n, bool generate, torch
   return logits;
 }
 
-// Paged-cache decode (mk_decode_paged): k_pages / v_pages bf16 [L, num_pages, 8, page_size, 128],
-// block_table int32 [>= ceil(max_seq_len / page_size)] on the same device; page_size a power of two.
-// Returns (fp32 logits [V], int32 greedy token on the device).
-std::tuple<torch::Tensor, torch::Tensor> decode_paged(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
-                                                      torch::Tensor final_norm, std::vector<torch::Tensor> lw,
-                                                      torch::Tensor cos, torch::Tensor sin, torch::Tensor kp,
-                                                      torch::Tensor vp, torch::Tensor block_table, int64_t position,
-                                                      int64_t max_seq_len) {
-  Checked c = validate(token_id, embed, lm_head, final_norm, lw, cos, sin, kp, vp, position, max_seq_len, true, true);
+struct Paged {
+  int num_pages, page_size;
+};
+
+// Shapes of a paged cache: k_pages / v_pages bf16 [L, num_pages, 8, page_size, 128] on the weights'
+// device, page_size a power of two <= 4096, and an int32 block table of ceil(max_seq_len /
+// page_size) <= 2048 entries or more.
+Paged check_paged(const Checked& c, const torch::Tensor& kp, const torch::Tensor& vp, const torch::Tensor& block_table,
+                  int64_t max_seq_len) {
   TORCH_CHECK(kp.defined() && kp.dim() == 5, "megakernel: k_pages must be [layers, num_pages, 8, page_size, 128]");
   const int64_t L = c.dims.num_layers, NP = kp.size(1), PS = kp.size(3);
   TORCH_CHECK(PS >= 1 && PS <= 4096 && (PS & (PS - 1)) == 0, "megakernel: page_size must be a power of two <= 4096");
@@ -211,6 +211,19 @@ std::tuple<torch::Tensor, torch::Tensor> decode_paged(int64_t token_id, torch::T
   TORCH_CHECK(block_table.defined() && block_table.device() == c.dev && block_table.scalar_type() == torch::kInt32 &&
                   block_table.is_contiguous() && block_table.dim() == 1 && block_table.size(0) >= need,
               "megakernel: block_table must be a contiguous int32 tensor of >= ", need, " entries on ", c.dev);
+  return {(int)NP, (int)PS};
+}
+
+// Paged-cache decode (mk_decode_paged): k_pages / v_pages bf16 [L, num_pages, 8, page_size, 128],
+// block_table int32 [>= ceil(max_seq_len / page_size)] on the same device; page_size a power of two.
+// Returns (fp32 logits [V], int32 greedy token on the device).
+std::tuple<torch::Tensor, torch::Tensor> decode_paged(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
+                                                      torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                      torch::Tensor cos, torch::Tensor sin, torch::Tensor kp,
+                                                      torch::Tensor vp, torch::Tensor block_table, int64_t position,
+                                                      int64_t max_seq_len) {
+  Checked c = validate(token_id, embed, lm_head, final_norm, lw, cos, sin, kp, vp, position, max_seq_len, true, true);
+  const Paged pg = check_paged(c, kp, vp, block_table, max_seq_len);
   c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
   const void* table = device_table(lw, c.dev, stream);
@@ -218,9 +231,33 @@ std::tuple<torch::Tensor, torch::Tensor> decode_paged(int64_t token_id, torch::T
   auto tok = torch::empty({1}, embed.options().dtype(torch::kInt32));
   MK_HIP_CHECK(mk_decode_paged(&c.dims, (int)token_id, embed.data_ptr(), lm_head.data_ptr(), final_norm.data_ptr(),
                                table, cos.data_ptr(), sin.data_ptr(), kp.data_ptr(), vp.data_ptr(),
-                               block_table.data_ptr<int32_t>(), (int)NP, (int)PS, (int)position, (int)max_seq_len,
+                               block_table.data_ptr<int32_t>(), pg.num_pages, pg.page_size, (int)position, (int)max_seq_len,
                                logits.data_ptr<float>(), tok.data_ptr<int32_t>(), stream));
   return {logits, tok};
+}
+
+// decode_steps on a paged cache (tensors as decode_paged); returns the last step's fp32 logits.
+torch::Tensor decode_steps_paged(torch::Tensor tokens, int64_t n, bool generate, torch::Tensor embed,
+                                 torch::Tensor lm_head, torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                 torch::Tensor cos, torch::Tensor sin, torch::Tensor kp, torch::Tensor vp,
+                                 torch::Tensor block_table, int64_t position, int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kp, vp, position, max_seq_len, true, true);
+  const Paged pg = check_paged(c, kp, vp, block_table, max_seq_len);
+  TORCH_CHECK(n >= 1, "megakernel: n must be positive");
+  TORCH_CHECK(position + n <= max_seq_len, "megakernel: position + n (", position + n, ") exceeds max_seq_len (",
+              max_seq_len, ")");
+  TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
+                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) == n + 1,
+              "megakernel: tokens must be a contiguous int32 [n + 1] tensor on ", c.dev);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  const void* table = device_table(lw, c.dev, stream);
+  auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  MK_HIP_CHECK(mk_decode_steps_paged(&c.dims, tokens.data_ptr<int32_t>(), (int)n, generate ? 1 : 0, embed.data_ptr(),
+                                     lm_head.data_ptr(), final_norm.data_ptr(), table, cos.data_ptr(), sin.data_ptr(),
+                                     kp.data_ptr(), vp.data_ptr(), block_table.data_ptr<int32_t>(), pg.num_pages,
+                                     pg.page_size, (int)position, (int)max_seq_len, logits.data_ptr<float>(), stream));
+  return logits;
 }
 
 int64_t status() {
@@ -258,6 +295,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_paged", &decode_paged,
         "decode on a paged K/V cache ([L, pages, 8, page_size, 128] + int32 block table); returns (fp32 logits, "
         "int32 greedy token on device)");
+  m.def("decode_steps_paged", &decode_steps_paged,
+        "decode_steps on a paged K/V cache (tensors as decode_paged); returns the last step's fp32 logits");
   m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
   m.def("reset", &reset, "clear the decode workspace (exchange words, status word) and restart its launch sequence; synchronizes");
   m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");

@@ -111,6 +111,19 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib):
     assert paged(position=512) == HIP_ERROR_INVALID_VALUE
     assert paged(token=151936) == HIP_ERROR_INVALID_VALUE
 
+    sp = lib.mk_decode_steps_paged
+    sp.restype = ctypes.c_int
+    sp.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int] + [vp] * 9 + [ctypes.c_int] * 4 + [vp, vp]
+
+    def steps_paged(tokens=dummy, n=4, table=dummy, page=16, position=3, max_seq=512):
+        return sp(ctypes.byref(good), tokens, n, 1, *([dummy] * 8), table, 64, page, position, max_seq, dummy, None)
+
+    assert steps_paged(tokens=None) == HIP_ERROR_INVALID_VALUE
+    assert steps_paged(n=0) == HIP_ERROR_INVALID_VALUE
+    assert steps_paged(table=None) == HIP_ERROR_INVALID_VALUE
+    assert steps_paged(page=12) == HIP_ERROR_INVALID_VALUE
+    assert steps_paged(position=509) == HIP_ERROR_INVALID_VALUE
+
 
 # ---------------------------------------------------------------------------------------------
 # the PyTorch operator (reference name and signature)
@@ -137,7 +150,7 @@ def _args(L=2, V=300, max_seq=16, dtype=torch.bfloat16):
 
 def test_operator_exports_reference_entry_point(ext):
     assert callable(ext.decode) and callable(ext.decode_greedy) and callable(ext.decode_steps)
-    assert callable(ext.decode_paged)
+    assert callable(ext.decode_paged) and callable(ext.decode_steps_paged)
     assert ext.version().startswith("megakernel_amd")
 
 

@@ -234,6 +234,33 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
     assert sess.kernel.status() == 0
 
 
+def test_device_loop_on_paged_cache(mini):
+    """``decode_steps_paged``: greedy generation on the device over a paged cache (shuffled pages,
+    NaN in the unused ones) against ``decode_steps`` on the contiguous cache -- the same tokens, the
+    same last logits, and the same rows written."""
+    from tests.paged_layout import from_pages, to_pages
+    P, n, ps = 250, 20, 32
+    _, last, _, kc, vc = mini.prefill(P)
+    npl = mini.max_seq // ps
+    table = torch.randperm(npl + 5, generator=torch.Generator().manual_seed(11))[:npl].to(torch.int32)
+    kp = to_pages(kc, ps, table.tolist(), npl + 5).to(DEV)
+    vp = to_pages(vc, ps, table.tolist(), npl + 5).to(DEV)
+    t0 = int(last.float().argmax())
+    ka, va = kc.to(DEV), vc.to(DEV)
+    tok_a = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
+    tok_a[0] = t0
+    la = _decode_steps(mini, tok_a, n, True, ka, va, P)
+    tok_b = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
+    tok_b[0] = t0
+    lb = mini.kernel.decode_steps_paged(tok_b, n, True, mini.embed, mini.lm_head, mini.final_norm, mini.layers,
+                                        mini.cos, mini.sin, kp, vp, table.to(DEV), P, mini.max_seq)
+    assert tok_b.tolist() == tok_a.tolist()
+    assert torch.equal(lb, la)
+    assert torch.equal(from_pages(kp, table.tolist()), ka) and torch.equal(from_pages(vp, table.tolist()), va)
+    assert mini.kernel.status() == 0
+    print(f"[paged device loop] {n} steps from P={P}, page {ps}: tokens {tok_b[1:9].tolist()} ... identical", flush=True)
+
+
 def test_paged_cache_bad_table_entry_sets_status(mini):
     """A block-table entry outside the page pool cannot be checked on the host without a copy: the
     kernel reads and writes page 0 instead (no access leaves the pool, nothing drains) and sets
