@@ -945,37 +945,42 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // the publish queues behind them.
     mark(a, tl + T_M_B_END, 64);
     lds_barrier();  // (B1) every group's partial in sm.gq
-    if (att) {
+    {
       // Merge the 32 group partials and publish this split's: wave mw takes head mw / 4, dims
       // 32 (mw % 4) .. +32. Lane = (subset sub of 4 groups, dim quad q4): each lane merges its 4
       // groups for 4 dims, then the 8 subsets combine across lanes (xor 8, 16, 32) with a common
       // max. Lanes 0-7 publish the head's 32 dims; lane 0 of waves 0 and 4 its (m, l).
+      // A workgroup without a split publishes zeros into its slot: every exchange word is written
+      // at every layer, which is what keeps a stale word's epoch from ever matching (the epochs
+      // of consecutive writes of a word are then 1 to 64 apart, never equal mod 255).
       const int h = mw >> 2, sub = lane >> 3, d0 = 32 * (mw & 3) + 4 * (lane & 7);
-      float m[4], l[4];
-      float4 p[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float2 ml = *reinterpret_cast<const float2*>(&sm.gq[4 * sub + k][h][D]);
-        m[k] = ml.x; l[k] = ml.y;
-        p[k] = *reinterpret_cast<const float4*>(&sm.gq[4 * sub + k][h][d0]);
-      }
-      float M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
-      M = fmaxf(M, dpp<0x128>(M));  // row_ror:8 == lane ^ 8 inside a 16-lane row
-      M = xmax32(xmax16(M));        // every split has a key, so M is finite
-      mark(a, tl + T_B_MAX, 64);
-      float Ls = 0.f;
+      float M = 0.f, Ls = 0.f;
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      if (att) {
+        float m[4], l[4];
+        float4 p[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float f = __expf(m[k] - M);  // 0 for a group without keys
-        Ls = fmaf(l[k], f, Ls);
-        acc[0] = fmaf(p[k].x, f, acc[0]); acc[1] = fmaf(p[k].y, f, acc[1]);
-        acc[2] = fmaf(p[k].z, f, acc[2]); acc[3] = fmaf(p[k].w, f, acc[3]);
+        for (int k = 0; k < 4; ++k) {
+          const float2 ml = *reinterpret_cast<const float2*>(&sm.gq[4 * sub + k][h][D]);
+          m[k] = ml.x; l[k] = ml.y;
+          p[k] = *reinterpret_cast<const float4*>(&sm.gq[4 * sub + k][h][d0]);
+        }
+        M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+        M = fmaxf(M, dpp<0x128>(M));  // row_ror:8 == lane ^ 8 inside a 16-lane row
+        M = xmax32(xmax16(M));        // every split has a key, so M is finite
+        mark(a, tl + T_B_MAX, 64);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float f = __expf(m[k] - M);  // 0 for a group without keys
+          Ls = fmaf(l[k], f, Ls);
+          acc[0] = fmaf(p[k].x, f, acc[0]); acc[1] = fmaf(p[k].y, f, acc[1]);
+          acc[2] = fmaf(p[k].z, f, acc[2]); acc[3] = fmaf(p[k].w, f, acc[3]);
+        }
+        auto sub_sum = [](float v) { v += dpp<0x128>(v); return xsum32(xsum16(v)); };
+        Ls = sub_sum(Ls);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = sub_sum(acc[i]);
       }
-      auto sub_sum = [](float v) { v += dpp<0x128>(v); return xsum32(xsum16(v)); };
-      Ls = sub_sum(Ls);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = sub_sum(acc[i]);
       Comm c;
       c.wt = sm.wt != 0;
       const uint32_t ep = ll_epoch(sm.seq, layer);
@@ -983,7 +988,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
       const float ml[2] = {M, Ls};
       if (lane < 8) ll_store<4>(c, att_x, h * D + d0, acc, ep, false);
       if (lane == 0 && (mw & 3) == 0) ll_store<2>(c, att_x, 2 * D + 2 * h, ml, ep, false);
-      mark(a, tl + T_B_PUB, 64);
+      if (att) mark(a, tl + T_B_PUB, 64);
     }
     lds_barrier();  // (B3) every wave's share of the partial is out before the loads below
     issue_ahead(I1(), layer);

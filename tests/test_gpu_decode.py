@@ -283,6 +283,30 @@ def test_paged_cache_bad_table_entry_sets_status(mini):
     assert mini.kernel.status() == 0
 
 
+def test_split_slots_never_stale_across_launches(mini):
+    """Exchange words carry an 8-bit epoch (launch sequence * 64 + layer, mod 255, + 1); a reader
+    accepts a word once its epoch matches. That is safe only if every word is rewritten at every
+    layer: for this 2-layer model, a word last written at layer 1 of launch k carries the epoch
+    that layer 0 of launch k + 4 expects. So: one launch with 4 attention splits, three with one
+    split (slots 1-3 belong to workgroups without a split), then 4 splits again. If those
+    workgroups skipped their slots, the last launch's merge could take layer-1 partials of the first
+    launch. Its logits must equal the same launch run right after a 4-split launch."""
+    P = 120
+    _, _, _, kc, vc = mini.prefill(P)
+    tok = 11
+    k1, v1 = kc.to(DEV), vc.to(DEV)
+    mini.decode(tok, k1, v1, 100)              # 4 splits (context 101)
+    k2, v2 = kc.to(DEV), vc.to(DEV)
+    for pos in (5, 6, 7):                       # 1 split, on a scratch copy of the cache
+        mini.decode(tok, k2, v2, pos)
+    got = mini.decode(tok, k1, v1, 101)         # 4 splits again, 4 launches after the first
+    k3, v3 = kc.to(DEV), vc.to(DEV)
+    mini.decode(tok, k3, v3, 100)
+    want = mini.decode(tok, k3, v3, 101)
+    assert torch.equal(got, want)
+    assert mini.kernel.status() == 0
+
+
 def test_device_loop_out_of_range_token_sets_status(mini):
     """A device-side input token outside [0, vocab) cannot be checked on the host: the kernel decodes
     token 0 instead (a normal launch, nothing drains) and sets status bit 2 until reset."""
