@@ -323,6 +323,33 @@ __device__ __forceinline__ void comm_norm(const float (&res)[H / 64], const uint
   store_hilo<E>(xh, xl, E * lane, y);
 }
 
+// RMSNorm split in two so that its reduction leaves the critical path: norm_input writes the GEMV
+// input x * w (the math waves start on it at once); norm_scale then computes rsqrt(mean(x^2) + eps),
+// which the comm wave applies to the GEMV's row sums. A GEMV is linear, so (W . (x*w)) * s equals
+// W . (x*w*s) up to rounding.
+template <int H>
+__device__ __forceinline__ void norm_input(const float (&res)[H / 64], const uint16_t* w, uint4* xh, uint4* xl) {
+  constexpr int E = H / 64;
+  const int lane = threadIdx.x & 63;
+  float y[E];
+#pragma unroll
+  for (int k = 0; k < E; k += 8) {
+    float wv[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + lane * E + k), wv);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[k + q] = res[k + q] * wv[q];
+  }
+  store_hilo<E>(xh, xl, E * lane, y);
+}
+template <int H>
+__device__ __forceinline__ float norm_scale(const float (&res)[H / 64]) {
+  constexpr int E = H / 64;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < E; k += 2) { s0 = fmaf(res[k], res[k], s0); s1 = fmaf(res[k + 1], res[k + 1], s1); }
+  return rsqrtf(wave_sum(s0 + s1) / (float)H + EPS);
+}
+
 // Cross-XCD partial sum of one row block, then republish inside the XCD, then read the whole
 // vector and add it to the residual. mine: this workgroup's partial of row HPW*j + lane (lanes <
 // HPW). Block j is rows [HPW*j, HPW*j + HPW).
@@ -1075,8 +1102,10 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     sm.cs[1][lane] = bf16_to_f32(gp(sr)[lane]); sm.cs[1][lane + 64] = bf16_to_f32(gp(sr)[lane + 64]);
   }
   lds_barrier();  // (P1)
-  comm_norm<H>(res, sm.nw[0], sm.xh, sm.xl);
+  norm_input<H>(res, sm.nw[0], sm.xh, sm.xl);
   lds_barrier();  // (P2)
+  float rs_in = norm_scale<H>(res);  // scale of the input norm, applied to the QKV row sums
+  float rs_post = 0.f;               // scale of the post-attention norm, applied to gate/up
 
   for (int layer = 0; layer < L; ++layer) {
     const uint32_t ep = ll_epoch(seq, layer);
@@ -1086,7 +1115,10 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     // ---- A: publish QKV rows; attention workgroups gather q, k, v of the group --------------
     mark(a, tl + T_A_START);
     lds_barrier();  // (A1)
-    if (lane < QKV_WG) ll_store<1>(c, xl + W_QKV, xcd * QKV_X + QKV_WG * j + lane, &sm.up[lane], ep, false);
+    if (lane < QKV_WG) {
+      const float qkv = sm.up[lane] * rs_in;
+      ll_store<1>(c, xl + W_QKV, xcd * QKV_X + QKV_WG * j + lane, &qkv, ep, false);
+    }
     mark(a, tl + T_A_PUB);
     if (st.att_wg) {
       // lane -> 8 values: q head 2x (lanes 0-15), q head 2x+1 (16-31), k head x (32-47), v (48-63)
@@ -1221,9 +1253,10 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
       mark(a, tl + T_C_PUB);
       comm_cross_reduce<H>(c, xl, W_OX, W_OL, xcd, j, mine, ep, res, a, tl + T_C_XPOLL, tl + T_C_LPOLL);
-      comm_norm<H>(res, nw + H, sm.xh, sm.xl);
+      norm_input<H>(res, nw + H, sm.xh, sm.xl);
     }
     lds_barrier();  // (C2)
+    rs_post = norm_scale<H>(res);
 
     // ---- D: silu(gate) * up of this workgroup's rows; gather the XCD's slice ------------------
     mark(a, tl + T_D_START);
@@ -1231,7 +1264,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     {
       uint32_t* m_x = xl + W_M + (size_t)xcd * MAX_IX;
       if (j >= D_FREE && lane < G::DPW) {
-        const float gs = sm.up[lane], us = sm.up[lane + G::DPW];
+        const float gs = sm.up[lane] * rs_post, us = sm.up[lane + G::DPW] * rs_post;
         const float m = gs / (1.f + expf(-gs)) * us;  // silu(g) * u
         ll_store<1>(c, m_x, G::DPW * (j - D_FREE) + lane, &m, ep, false);
       }
@@ -1255,9 +1288,11 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
       mark(a, tl + T_E_PUB);
       comm_cross_reduce<H>(c, xl, W_EX, W_EL, xcd, j, mine, ep, res, a, tl + T_E_XPOLL, tl + T_E_LPOLL);
-      comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm, or the final norm
+      if (layer + 1 < L) norm_input<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm
+      else comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // the final norm, for the LM head
     }
     lds_barrier();  // (E2)
+    if (layer + 1 < L) rs_in = norm_scale<H>(res);
   }
 
   mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 1);
