@@ -1638,4 +1638,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.10 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.11 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop, paged cache)"; }
