@@ -1,4 +1,4 @@
-// Persistent cooperative decode kernel for Qwen3-shaped models on MI355X (gfx950), plus its C ABI.
+// Persistent decode kernel for Qwen3-shaped models on MI355X (gfx950), plus its C ABI.
 //
 // One launch = one decode step for batch 1: embedding -> L x {RMSNorm, QKV, per-head norm + RoPE,
 // K/V cache write, split-K GQA attention, O-proj + residual, RMSNorm, gate/up + SiLU, down +
@@ -27,10 +27,15 @@
 // words live in that XCD's L2 (plain stores, device-scope loads); across XCDs they are written
 // through to memory (device-scope stores). Cross-XCD partial sums go in two hops: workgroup j of
 // each XCD gathers row block j from the 8 XCDs, sums it in XCD order and republishes it inside its
-// own XCD; then every workgroup reads the whole vector from its L2. Every buffer is written once
-// per layer and read before any writer can reach the next layer's write; consecutive writes of a
-// word carry epochs 1 to 64 apart (never 0 mod 255), so no buffer needs clearing. Each model shape
-// has its own workspace, so that every word of it is written by every layer of every launch.
+// own XCD; then every workgroup reads the whole vector from its L2. Every word is written once
+// per layer of every launch (also by workgroups that have nothing to put in it) and read before any
+// writer can reach the next layer's write; consecutive writes of a word therefore carry epochs at
+// most 127 apart (never 0 mod 255), so no buffer needs clearing and no stale word can pass for a
+// fresh one. Each model shape has its own workspace.
+//
+// Variants chosen per launch on the host: one or two K/V rows per math group held in registers
+// (template NKV), a contiguous or a paged K/V cache (block table in LDS), and a token read from
+// the arguments or from device memory (the device-side multi-token loop).
 //
 // Numerics follow the reference kernel's fp32 design: bf16 weights and cache, fp32 activations and
 // accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to bf16 as stored. Logits are fp32;
