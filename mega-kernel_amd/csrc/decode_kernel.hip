@@ -477,8 +477,42 @@ __device__ __forceinline__ void tile_consume(const uint4 (&pf)[T::PS][T::CPL], i
     xh[k] = xh_lds[k * T::SPAN + lane % T::SPAN];
     xl[k] = xl_lds[k * T::SPAN + lane % T::SPAN];
   }
+#ifndef MK_JOINT_RED
+#define MK_JOINT_RED 1
+#endif
+  if constexpr (MK_JOINT_RED && T::SPAN == 64 && (T::PS == 2 || T::PS == 4) && T::PS == T::STEPS) {
+    // whole-wave rows, all prefetched: reduce the PS row sums together. Each lane-swap step halves
+    // the values a lane carries (gfx950 v_permlane32/16_swap: lanes 0-31 keep the first operand's
+    // pair sums, lanes 32-63 the second's; likewise per 16-lane row pair), so PS rows cost one
+    // 16-lane reduction instead of PS full-wave ones.
+    float v[T::PS];
 #pragma unroll
-  for (int s = 0; s < T::PS; ++s) tile_dot_step<T>(pf[s], xh, xl, s, mw, lane, s_up);
+    for (int s = 0; s < T::PS; ++s) v[s] = dot_chunks<T::CPL>(pf[s], xh, xl);
+    auto swap_add32 = [](float a, float b) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    auto swap_add16 = [](float a, float b) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    float z;
+    int s;
+    if constexpr (T::PS == 4) {
+      // rows of the 16-lane row groups: step 0 (lanes 0-15), 2 (16-31), 1 (32-47), 3 (48-63)
+      z = row16_sum(swap_add16(swap_add32(v[0], v[1]), swap_add32(v[2], v[3])));
+      s = ((lane >> 5) & 1) | (((lane >> 4) & 1) << 1);
+    } else {
+      // step 0 in lanes 0-31, step 1 in lanes 32-63
+      z = row16_sum(xsum16(swap_add32(v[0], v[1])));
+      s = (lane >> 5) & 1;
+    }
+    const int r = tile_row<T>(s, mw, 0);
+    if ((lane & 15) == 0 && r < T::ROWS) s_up[r] = z;
+  } else {
+#pragma unroll
+    for (int s = 0; s < T::PS; ++s) tile_dot_step<T>(pf[s], xh, xl, s, mw, lane, s_up);
+  }
   after();
 #pragma unroll
   for (int s = T::PS; s < T::STEPS; ++s) {
@@ -885,6 +919,15 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // later waits one or two loads stricter; worth it at the 0.6B shape (387 vs 395 us per token at
   // config 2), not at 1.7B (868 vs 864).
   constexpr bool KV_PRED = MK_KV_PRED;
+#ifndef MK_A_FIRST
+#define MK_A_FIRST 1
+#endif
+  // QKV register steps issued at phase D (the rest at phase E). A burst of weight loads delays every
+  // exchange poll the CU issues after it until the burst has drained (~1.3 us for all QKV rows
+  // chip-wide), so the QKV burst is split between the D and E hops, each of which it fits. Measured
+  // on MI355X at config 2: 381 -> 365 us per token.
+  constexpr int A_FIRST = MK_A_FIRST < TA::PS ? (MK_A_FIRST < 1 ? 1 : MK_A_FIRST) : TA::PS;
+
   auto load_phase = [&](auto qc, int layer) {
     constexpr int Q = decltype(qc)::value;
     const bool past = layer >= L;
@@ -893,7 +936,14 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     const int mwq = opaque(mw), lq = opaque(lane);
     const uint4* hot = reinterpret_cast<const uint4*>(a.final_norm);
     auto sel = [&](auto rp) { return [=](int r) { return past ? hot : rp(r); }; };
-    if constexpr (Q == 0) tile_load<TA, TA::PS>(wA, 0, mwq, lq, sel(rows_A(lw)));
+    if constexpr (Q == 0) {  // QKV: the first A_FIRST steps (all of them when A_FIRST == PS)
+      typedef uint4 First[A_FIRST][TA::CPL];
+      tile_load<TA, A_FIRST>(*reinterpret_cast<First*>(&wA[0]), 0, mwq, lq, sel(rows_A(lw)));
+    }
+    if constexpr (Q == 6 && A_FIRST < TA::PS) {  // QKV: the remaining steps, issued a phase later
+      typedef uint4 Rest[TA::PS - A_FIRST][TA::CPL];
+      tile_load<TA, TA::PS - A_FIRST>(*reinterpret_cast<Rest*>(&wA[A_FIRST]), A_FIRST, mwq, lq, sel(rows_A(lw)));
+    }
     if constexpr (Q == 1) {
 #pragma unroll
       for (int r = 0; r < NKV; ++r) {
@@ -950,6 +1000,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     for (int k = 0; k < G::NSL_L; ++k) nsl[k] = ld_global16(slot_chunk(layer + 1, q0 + 64 * NMW * k));
   };
   if constexpr (DIST > 0) load_phase(I0(), 0);
+  if constexpr (DIST > 0 && A_FIRST < TA::PS) load_phase(std::integral_constant<int, 6>(), 0);
   load_phase(I1(), 0);
   if constexpr (DIST > 2) load_phase(I2(), 0);
   if constexpr ((DIST > 3 && D_AT < 0) || D_AT == 4) load_phase(I3(), 0);
@@ -1046,6 +1097,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // E: down_proj partial over slice x's columns
     if constexpr (!MID) issue_ahead(I4(), layer);
     if constexpr (D_AT == 4) load_phase(I3(), layer + 1);
+    if constexpr (A_FIRST < TA::PS) load_phase(std::integral_constant<int, 6>(), layer + 1);
     tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
     {
       // the next layer's norm weights (or the final norm) into the other LDS slot
@@ -1643,4 +1695,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.11 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.12 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, plain launch, device-side token loop, paged cache)"; }
