@@ -69,7 +69,7 @@ constexpr int QKV_X = 4 * D;  // q (2 heads) + k + v rows owned by one XCD
 constexpr int QKV_WG = QKV_X / WPX;  // 16
 constexpr int D_FREE = 8;            // local workgroups without gate/up rows (see Geo::DPW)
 // K/V rows per math group held in registers (loaded a layer ahead) is a kernel template parameter
-// NKV: 1 while every split is at most MG positions long, 2 beyond (kv_rows_for()).
+// NKV: 1 or 2, from split_plan().
 constexpr int SPLIT_POS = MG;        // positions per split while the split count is below its cap
 // Attention split merge: up to SB0 splits are polled with their (m, l) words in one round; beyond
 // that the comm wave polls SB1 splits per round (as many as its registers hold).
@@ -92,8 +92,8 @@ constexpr int MAX_PAGES = 2048;     // block-table entries a paged launch may us
 #ifndef MK_PF_DIST
 #define MK_PF_DIST 2
 #endif
-constexpr int PF_DIST = MK_PF_DIST;  // phases of weights each math lane keeps in flight (0..5)
-static_assert(PF_DIST >= 0 && PF_DIST <= 5, "prefetch distance");
+constexpr int PF_DIST = MK_PF_DIST;  // phases of weights each math lane keeps in flight (0..4)
+static_assert(PF_DIST >= 0 && PF_DIST <= 4, "prefetch distance");
 constexpr int MAX_LAYERS = 62;  // epoch = seq << 6 | layer; 63 marks the final exchange
 
 // Exchange workspace of one model shape. LL regions in 32-bit words (W_*), then the done flags,
@@ -628,6 +628,25 @@ struct Step {
   bool att_wg;
 };
 
+// Attention split plan of a context: S splits on local workgroups 0..S-1, NKV register K/V rows
+// per math group (the kernel's template parameter, chosen by the host from the same plan). One
+// split per SPLIT_POS positions, capped at what one merge round takes (two rounds' worth for long
+// contexts): a merge round costs more than a longer split. One register row while the splits are
+// at most SPLIT_POS long (a second would only re-read a row), two once they are longer, so that
+// contexts up to 512 (2048 at two merge rounds) stream no K/V inside the attention phase.
+// (Measured on MI355X: packing two rows per group earlier, to keep S within one merge poll up to
+// context 256, costs 3-4 us per token at the 0.6B shape and ~4 at 1.7B for short contexts.)
+struct SplitPlan {
+  int S, nkv;
+};
+template <int H>
+__host__ __device__ constexpr SplitPlan split_plan(int ctx) {
+  const int cap = ctx > S_LONG_CTX ? 2 * SB1 : SB1;
+  const int S = (ctx + SPLIT_POS - 1) / SPLIT_POS;
+  return {S < cap ? S : cap, ctx > cap * SPLIT_POS ? 2 : 1};
+}
+
+template <int H>
 __device__ __forceinline__ Step make_step(const KArgs& a) {
   Step s;
   s.xcd = blockIdx.x % NXCD;
@@ -635,13 +654,9 @@ __device__ __forceinline__ Step make_step(const KArgs& a) {
   s.position = a.position;
   s.ctx = a.position + 1;
   s.L = a.num_layers;
-  // Split-K attention: the context is cut into S splits handled by local workgroups 0..S-1.
-  // Up to MG * NKV positions per split come from registers loaded a layer ahead, the rest stream
-  // in phase B. One split per SPLIT_POS positions, capped at what one merge round takes (two
-  // rounds' worth for long contexts): a merge round costs more than a longer split.
-  const int cap = s.ctx > S_LONG_CTX ? 2 * SB1 : SB1;
-  const int S = (s.ctx + SPLIT_POS - 1) / SPLIT_POS;
-  s.S = S < cap ? S : cap;
+  // Split-K attention (split_plan): up to MG * NKV positions per split come from registers
+  // loaded a layer ahead, the rest stream in phase B.
+  s.S = split_plan<H>(s.ctx).S;
   s.att_wg = s.j < s.S;
   s.p0 = s.att_wg ? (int)(((long long)s.ctx * s.j) / s.S) : 0;
   s.p1 = s.att_wg ? (int)(((long long)s.ctx * (s.j + 1)) / s.S) : 0;
@@ -963,19 +978,13 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, sel(rows_D(lw)));
     if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, sel(rows_E(lw)));
   };
-#ifndef MK_D_AT
-#define MK_D_AT -1
-#endif
-  // gate/up weights: -1 = on the DIST schedule; 4 = at the start of the previous layer's E;
-  // 2 = in C after C1
-  constexpr int D_AT = MK_D_AT;
-  // at the start of phase P (DIST < 5) or after its consumption (DIST == 5). The K/V rows of layer
+  // at the start of phase P. The K/V rows of layer
   // l + 1 are not on this schedule: phase C of layer l issues them (after its own loads), four
   // phases ahead, so that at B they wait on nothing newer than themselves but the A weights.
   auto issue_ahead = [&](auto pc, int layer) {
     constexpr int P = decltype(pc)::value;
     constexpr int Q = P + DIST;
-    if constexpr (Q % 5 != 1 && !(Q % 5 == 3 && D_AT >= 0)) {
+    if constexpr (Q % 5 != 1) {
       if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
       else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
     }
@@ -986,13 +995,6 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
   using I4 = std::integral_constant<int, 4>;
-#ifndef MK_ISSUE_MID
-#define MK_ISSUE_MID 0
-#endif
-  // MID: a phase issues its loads after handing its results to the comm wave (between the phase's
-  // two barriers, while the comm wave exchanges), not before its own compute; required for
-  // DIST == 5, where a phase reloads its own registers
-  constexpr bool MID = DIST == 5 || MK_ISSUE_MID;
   auto load_norms = [&](int layer) {
     // the next layer's norm weights (or the final norm), one chunk per math lane
     const int q0 = mw * 64 + lane;
@@ -1003,8 +1005,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   if constexpr (DIST > 0 && A_FIRST < TA::PS) load_phase(std::integral_constant<int, 6>(), 0);
   load_phase(I1(), 0);
   if constexpr (DIST > 2) load_phase(I2(), 0);
-  if constexpr ((DIST > 3 && D_AT < 0) || D_AT == 4) load_phase(I3(), 0);
-  if constexpr (DIST > 4) load_phase(I4(), 0);
+  if constexpr (DIST > 3) load_phase(I3(), 0);
   lds_barrier();  // (P1) norm weights of layer 0 in LDS
   lds_barrier();  // (P2) comm: x = RMSNorm(embedding)
 
@@ -1013,11 +1014,11 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
 
     // A: QKV rows
-    if constexpr (!MID) { issue_ahead(I0(), layer); load_norms(layer); }
+    issue_ahead(I0(), layer);
+    load_norms(layer);
     tile_consume<TA>(wA, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_A(lw), [&]() { mark(a, tl + T_M_A_DOT, 64); });
     mark(a, tl + T_M_A_END, 64);
     lds_barrier();  // (A1)
-    if constexpr (MID) { issue_ahead(I0(), layer); load_norms(layer); }
     lds_barrier();  // (A2) comm: q, new K/V in LDS
     mark(a, tl + T_M_B_START, 64);
 
@@ -1079,24 +1080,20 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     lds_barrier();  // (B2) comm: attention output in x[0, 256)
 
     // C: o_proj partial over this group's 256 columns
-    if constexpr (!MID) issue_ahead(I2(), layer);
+    issue_ahead(I2(), layer);
     tile_consume<TC>(wC, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_C(lw), NoOp());
     lds_barrier();  // (C1)
-    if constexpr (MID) issue_ahead(I2(), layer);
-    if constexpr (D_AT == 2) load_phase(I3(), layer);
     lds_barrier();  // (C2) comm: x = RMSNorm(residual) * post-attention norm
 
     // D: gate/up rows of MLP slice x
-    if constexpr (!MID) issue_ahead(I3(), layer);
+    issue_ahead(I3(), layer);
     mark(a, tl + T_M_D_ISSUED, 64);
     tile_consume<TD>(wD, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_D(lw), [&]() { mark(a, tl + T_M_D_DOT, 64); });
     lds_barrier();  // (D1)
-    if constexpr (MID) issue_ahead(I3(), layer);
     lds_barrier();  // (D2) comm: x[0, IX) = silu(gate) * up of the slice
 
     // E: down_proj partial over slice x's columns
-    if constexpr (!MID) issue_ahead(I4(), layer);
-    if constexpr (D_AT == 4) load_phase(I3(), layer + 1);
+    issue_ahead(I4(), layer);
     if constexpr (A_FIRST < TA::PS) load_phase(std::integral_constant<int, 6>(), layer + 1);
     tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
     {
@@ -1108,7 +1105,6 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         if (q0 + 64 * NMW * k < G::NSL16) dst[q0 + 64 * NMW * k] = nsl[k];
     }
     lds_barrier();  // (E1)
-    if constexpr (MID) issue_ahead(I4(), layer);
     lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
   }
 
@@ -1395,7 +1391,7 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
 template <int H, int I, int NKV>
 __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<H, I> sm;
-  const Step st = make_step(a);
+  const Step st = make_step<H>(a);
   mark(a, TRACE_LAYERS * TRACE_PER_LAYER + 0);
   if (threadIdx.x < 64) comm_role<H, I>(a, sm, st);
   else math_role<H, I, PF_DIST, NKV>(a, sm, st);
@@ -1473,18 +1469,10 @@ static hipError_t device_state(DeviceState** out) {
 // start wait for the rest with bounded spins; past the bound the launch ends with the status
 // timeout bit set instead of hanging. mk_set_launch_mode(1) selects hipLaunchCooperativeKernel,
 // whose runtime guarantees co-residency before the grid starts.
-// Register rows per math group for a context: one while the splits are at most SPLIT_POS long (a
-// second would only re-read a row), two once they are longer, so that contexts up to 512 (2048 at
-// two merge rounds) stream no K/V inside the attention phase. The kernel's split rule is the same.
-static int kv_rows_for(int ctx) {
-  const int cap = ctx > S_LONG_CTX ? 2 * SB1 : SB1;
-  return ctx > cap * SPLIT_POS ? 2 : 1;
-}
-
 template <int H, int I>
 static hipError_t launch(KArgs& k, hipStream_t stream, bool cooperative) {
   void* args[] = {(void*)&k};
-  const void* f = kv_rows_for(k.position + 1) == 1 ? (const void*)decode_kernel<H, I, 1>
+  const void* f = split_plan<H>(k.position + 1).nkv == 1 ? (const void*)decode_kernel<H, I, 1>
                                                    : (const void*)decode_kernel<H, I, 2>;
   if (cooperative) return hipLaunchCooperativeKernel(f, dim3(NWG), dim3(NT), args, 0, stream);
   return hipLaunchKernel(f, dim3(NWG), dim3(NT), args, 0, stream);
