@@ -1159,6 +1159,14 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   lds_barrier();  // (P2)
   float rs_in = norm_scale<H>(res);  // scale of the input norm, applied to the QKV row sums
   float rs_post = 0.f;               // scale of the post-attention norm, applied to gate/up
+  // RoPE entries of this lane's 8 dims (d mod 64 of dims 8 (lane % 16) ..), the same at every layer
+  float rc[8], rsn[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = (8 * (lane & 15) + i) & 63;
+    rc[i] = sm.cs[0][d];
+    rsn[i] = sm.cs[1][d];
+  }
 
   for (int layer = 0; layer < L; ++layer) {
     const uint32_t ep = ll_epoch(seq, layer);
@@ -1175,32 +1183,34 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     mark(a, tl + T_A_PUB);
     if (st.att_wg) {
       // lane -> 8 values: q head 2x (lanes 0-15), q head 2x+1 (16-31), k head x (32-47), v (48-63)
+      const int tt = lane & 15, part = lane >> 4;
+      // this lane's 8 q/k-norm weights, read before the poll so that their LDS latency hides in it
+      const u4v hwp = *reinterpret_cast<const u4v*>(nw + 2 * H + (part == 2 ? D : 0) + 8 * tt);
       int off[2];
 #pragma unroll
       for (int k = 0; k < 2; ++k) off[k] = xcd * QKV_X + 8 * lane + 4 * k;
       float v[8];
       ll_poll<2, 4>(c, xl + W_QKV, off, ep, v);
       mark(a, tl + T_A_POLL);
-      const int tt = lane & 15, part = lane >> 4;
       // per-head RMSNorm (/root/reference/megakernel.cu:490-630): a head is one 16-lane row
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
       ss = row16_sum(ss);
       const float rs = rsqrtf(ss / (float)D + EPS);
-      const uint16_t* hw = nw + 2 * H + (part == 2 ? D : 0);
       float u[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) u[i] = v[i] * rs * bf16_to_f32(hw[8 * tt + i]);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t wp = hwp[i >> 1];
+        u[i] = v[i] * rs * __uint_as_float(i & 1 ? wp & 0xFFFF0000u : wp << 16);
+      }
       // rotate-half RoPE with the table entry of dim d mod 64 (/root/reference/megakernel.cu:548-555);
       // dim d's partner d +- 64 sits in lane tt ^ 8 of the same row
       float o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float pr = dpp<0x128>(u[i]);
-        const int d = (8 * tt + i) & 63;
-        const float cv = sm.cs[0][d], sv = sm.cs[1][d];
-        o[i] = tt < 8 ? u[i] * cv - pr * sv : u[i] * cv + pr * sv;
+        o[i] = tt < 8 ? u[i] * rc[i] - pr * rsn[i] : u[i] * rc[i] + pr * rsn[i];
       }
       if (part < 2) {
 #pragma unroll
@@ -1229,70 +1239,92 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       // d0 .. d0+3, plus each split's (m0, l0, m1, l1)). A poll round under load costs ~0.5 us even
       // when its data is ready, so the splits are taken in as few sequential polls as the registers
       // allow: all of them at once up to SB0 splits, otherwise SB1 splits per poll (at most two).
-      float M = -INFINITY, Ls = 0.f;
+      // Max first: each poll's split maxima are reduced before any weight exp(m - max) is taken, so
+      // the weights are independent and the accumulation is plain FMAs, not a chain of rescales
+      // through a running max (which costs ~0.1 us per split on one wave).
+      float Ls = 0.f;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      auto merge_batch = [&](auto nb, int s0) {
+      auto merge_batch = [&](auto nb) {  // all S <= NB splits in one poll
         constexpr int NB = decltype(nb)::value;
         int off[2 * NB];
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
-          const int s = s0 + q < S ? s0 + q : s0;
+          const int s = q < S ? q : 0;
           off[2 * q + 0] = s * APW + h * D + d0;
           off[2 * q + 1] = s * APW + 2 * D;
         }
         float v[8 * NB];
-        ll_poll<2 * NB, 4, 32>(c, att_x, off, ep, v);  // two rounds in flight up to 4 splits, else one
+        ll_poll<2 * NB, 4, 32>(c, att_x, off, ep, v);  // two rounds in flight
+        float M = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < NB; ++q)
+          if (q < S) M = fmaxf(M, h ? v[8 * q + 6] : v[8 * q + 4]);
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
-          if (s0 + q < S) {
+          if (q < S) {
             const float* w = v + 8 * q;
-            const float ms = h ? w[6] : w[4], ls = h ? w[7] : w[5];
-            const float n = fmaxf(M, ms);
-            const float cm = __expf(M - n), cs = __expf(ms - n);
-            Ls = Ls * cm + ls * cs;
-            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
-            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
-            M = n;
+            const float cs = __expf((h ? w[6] : w[4]) - M);
+            Ls = fmaf(h ? w[7] : w[5], cs, Ls);
+            acc.x = fmaf(w[0], cs, acc.x); acc.y = fmaf(w[1], cs, acc.y);
+            acc.z = fmaf(w[2], cs, acc.z); acc.w = fmaf(w[3], cs, acc.w);
           }
         }
       };
       constexpr int SB0 = merge_sb0<H>();
-      static_assert(2 * SB1 <= WPX, "split count");
-      // NB splits from s0 in one poll: each lane's accumulator slice of every split, plus one load
-      // of the splits' (m, l) words (lane q reads split s0 + q's), shared across lanes by readlane
-      auto merge_wide = [&](auto nb, int s0) {
-        constexpr int NB = decltype(nb)::value;
+      static_assert(2 * SB1 <= WPX && SB1 == 8, "split count; one 8-lane group holds a round's (m, l)");
+      // Rounds of SB1 splits from s0: each lane's accumulator slice of every split, plus one load of
+      // the splits' (m0, l0, m1, l1) words on lanes 0..SB1-1 (lane q: split s0 + q). Both heads'
+      // running max and sum are kept wave-uniform (M0, M1, L0, L1) across rounds.
+      float M0 = -INFINITY, M1 = -INFINITY, L0 = 0.f, L1 = 0.f;
+      auto merge_wide = [&](int s0) {
+        constexpr int NB = SB1;
         int off[NB + 1];
 #pragma unroll
         for (int q = 0; q < NB; ++q) off[q] = (s0 + q < S ? s0 + q : s0) * APW + h * D + d0;
-        off[NB] = (lane < NB && s0 + lane < S ? s0 + lane : s0) * APW + 2 * D;
+        const bool own = lane < NB && s0 + lane < S;
+        off[NB] = (own ? s0 + lane : s0) * APW + 2 * D;
         float v[4 * (NB + 1)];
         // one round in flight (two, at the 0.6B width where they fit without spilling, measured
         // no faster on MI355X: -2 to +3 us per token from context 300 to 3584)
         ll_poll<NB + 1, 4, 16>(c, att_x, off, ep, v);
+        auto max8 = [](float x) {  // max over each 8-lane group
+          x = fmaxf(x, dpp<0xB1>(x));   // quad_perm [1,0,3,2]
+          x = fmaxf(x, dpp<0x4E>(x));   // quad_perm [2,3,0,1]
+          return fmaxf(x, dpp<0x141>(x));  // row_half_mirror
+        };
+        auto sum8 = [](float x) {
+          x += dpp<0xB1>(x);
+          x += dpp<0x4E>(x);
+          return x + dpp<0x141>(x);
+        };
+        auto lane0 = [](float x) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)); };
+        const float m0 = own ? v[4 * NB + 0] : -INFINITY, m1 = own ? v[4 * NB + 2] : -INFINITY;
+        const float N0 = fmaxf(M0, lane0(max8(m0))), N1 = fmaxf(M1, lane0(max8(m1)));  // finite
+        const float f0 = own ? __expf(m0 - N0) : 0.f, f1 = own ? __expf(m1 - N1) : 0.f;
+        const float c0 = __expf(M0 - N0), c1 = __expf(M1 - N1);  // 0 on the first round
+        L0 = fmaf(L0, c0, lane0(sum8(own ? v[4 * NB + 1] * f0 : 0.f)));
+        L1 = fmaf(L1, c1, lane0(sum8(own ? v[4 * NB + 3] * f1 : 0.f)));
+        M0 = N0; M1 = N1;
+        const float cm = h ? c1 : c0;
+        acc.x *= cm; acc.y *= cm; acc.z *= cm; acc.w *= cm;
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
           if (s0 + q < S) {
-            float mlq[4];  // lane q's (m0, l0, m1, l1), read before this lane picks its head
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              mlq[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[4 * NB + i]), q));
-            const float ms = h ? mlq[2] : mlq[0], ls = h ? mlq[3] : mlq[1];
-            const float n = fmaxf(M, ms);
-            const float cm = __expf(M - n), cs = __expf(ms - n);
-            Ls = Ls * cm + ls * cs;
+            const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f0), q));
+            const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f1), q));
+            const float cs = h ? g1 : g0;
             const float* w = v + 4 * q;
-            acc.x = acc.x * cm + w[0] * cs; acc.y = acc.y * cm + w[1] * cs;
-            acc.z = acc.z * cm + w[2] * cs; acc.w = acc.w * cm + w[3] * cs;
-            M = n;
+            acc.x = fmaf(w[0], cs, acc.x); acc.y = fmaf(w[1], cs, acc.y);
+            acc.z = fmaf(w[2], cs, acc.z); acc.w = fmaf(w[3], cs, acc.w);
           }
         }
       };
       if (S <= SB0) {
-        merge_batch(std::integral_constant<int, SB0>(), 0);
+        merge_batch(std::integral_constant<int, SB0>());
       } else {
 #pragma unroll 1
-        for (int s0 = 0; s0 < S; s0 += SB1) merge_wide(std::integral_constant<int, SB1>(), s0);
+        for (int s0 = 0; s0 < S; s0 += SB1) merge_wide(s0);
+        Ls = h ? L1 : L0;
       }
       mark(a, tl + T_B_POLL);
       const float inv = 1.f / Ls;
@@ -1685,4 +1717,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.12 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.13 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, plain launch, device-side token loop, paged cache)"; }
