@@ -817,33 +817,50 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
 // Tied LM head over this workgroup's vocabulary rows: wave mw takes row mw of every row group the
 // workgroup owns, one row per step (64 lanes x LCPL chunks), LP rows in flight per wave; fused
 // greedy argmax key of the wave into sm.best[mw].
-template <int H, int I>
-__device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, int lane) {
-  constexpr int LCPL = H / 512;
+template <int H>
+struct LmTile {
+  static constexpr int LCPL = H / 512;  // 16-byte chunks per lane of one row
 #ifndef MK_LP
 #define MK_LP 4
 #endif
-  constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
+  static constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
   // row groups of NMW rows interleaved over the workgroups (step s reads group blockIdx.x + NWG*s),
   // so the grid sweeps the table front to back instead of 256 separate streams
-  const int ngroups = (a.vocab + NMW - 1) / NMW;
-  const int nmine = ((int)blockIdx.x < ngroups) ? (ngroups - (int)blockIdx.x + NWG - 1) / NWG : 0;
-  auto row_of = [&](int s, int m) { return NMW * ((int)blockIdx.x + NWG * s) + m; };
+  __device__ static int nmine(const KArgs& a) {
+    const int ngroups = (a.vocab + NMW - 1) / NMW;
+    return ((int)blockIdx.x < ngroups) ? (ngroups - (int)blockIdx.x + NWG - 1) / NWG : 0;
+  }
+  __device__ static int row_of(int s, int m) { return NMW * ((int)blockIdx.x + NWG * s) + m; }
+  // loads row step s of math wave mw into b; past the end it re-reads the last row (unconditional loads)
+  __device__ static void load(const KArgs& a, int nm, int s, int mw, int lane, uint4 (&b)[LCPL]) {
+    int row = row_of(s, mw);
+    row = (s < nm && row <= a.vocab - 1) ? row : a.vocab - 1;
+    const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lane;
+#pragma unroll
+    for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
+  }
+  // the first LP rows: they depend on nothing the layers compute, so they are issued while the
+  // last layer's exchanges and the final norm are still running
+  __device__ static void first(const KArgs& a, int mw, int lane, uint4 (&buf)[LP][LCPL]) {
+    const int nm = nmine(a);
+#pragma unroll
+    for (int i = 0; i < LP; ++i) load(a, nm, i, opaque(mw), opaque(lane), buf[i]);
+  }
+};
+
+template <int H, int I>
+__device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, int lane,
+                                        uint4 (&buf)[LmTile<H>::LP][LmTile<H>::LCPL]) {
+  typedef LmTile<H> T;
+  constexpr int LCPL = T::LCPL, LP = T::LP;
+  const int nmine = T::nmine(a);
   const int rlast = a.vocab - 1;
   const int lq = opaque(lane), mwq = opaque(mw);
+  auto row_of = [&](int s, int m) { return T::row_of(s, m); };
   uint4 xh[LCPL], xl[LCPL];
 #pragma unroll
   for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
-  auto lm_load = [&](int s, uint4 (&b)[LCPL]) {
-    int row = row_of(s, mwq);
-    row = (s < nmine && row <= rlast) ? row : rlast;  // past the end: re-read the last row (unconditional loads)
-    const uint4* p = reinterpret_cast<const uint4*>(a.lm_head + (size_t)row * H) + lq;
-#pragma unroll
-    for (int k = 0; k < LCPL; ++k) b[k] = ld_stream(p + 64 * k);
-  };
-  uint4 buf[LP][LCPL];
-#pragma unroll
-  for (int i = 0; i < LP; ++i) lm_load(i, buf[i]);
+  auto lm_load = [&](int s, uint4 (&b)[LCPL]) { T::load(a, nmine, s, mwq, lq, b); };
   u64 best = 0;
   for (int s0 = 0; s0 < nmine; s0 += LP) {
 #pragma unroll
@@ -1007,11 +1024,15 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   if constexpr (DIST > 2) load_phase(I2(), 0);
   if constexpr (DIST > 3) load_phase(I3(), 0);
   lds_barrier();  // (P1) norm weights of layer 0 in LDS
-  lds_barrier();  // (P2) comm: x = RMSNorm(embedding)
 
   for (int layer = 0; layer < L; ++layer) {
     const mk_layer_weights& lw = sm.layers[layer];
     const int tl = layer < TRACE_LAYERS ? layer * TRACE_PER_LAYER : -1000000;
+    // (P2) comm: x = RMSNorm(embedding), for layer 0; (E2) of the previous layer otherwise: x =
+    // this layer's normed input. The last layer's E2 follows the loop, after the first LM-head
+    // loads, so that no load sits under a condition inside the loop (which would make the
+    // compiler's wait counts stricter in every layer).
+    lds_barrier();
 
     // A: QKV rows
     issue_ahead(I0(), layer);
@@ -1105,10 +1126,12 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
         if (q0 + 64 * NMW * k < G::NSL16) dst[q0 + 64 * NMW * k] = nsl[k];
     }
     lds_barrier();  // (E1)
-    lds_barrier();  // (E2) comm: x = next layer's normed input, or the final hidden state
   }
 
-  lm_head<H, I>(a, sm, mw, lane);
+  uint4 lm_buf[LmTile<H>::LP][LmTile<H>::LCPL];
+  LmTile<H>::first(a, mw, lane, lm_buf);
+  lds_barrier();  // (E2) of the last layer: comm: x = the final hidden state
+  lm_head<H, I>(a, sm, mw, lane, lm_buf);
   lds_barrier();  // (F) per-wave argmax keys in LDS
 }
 
@@ -1717,4 +1740,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.13 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.14 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
