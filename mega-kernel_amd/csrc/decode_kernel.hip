@@ -995,9 +995,11 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     if constexpr (Q == 3) tile_load<TD, TD::PS>(wD, 0, mwq, lq, sel(rows_D(lw)));
     if constexpr (Q == 4) tile_load<TE, TE::PS>(wE, 0, mwq, lq, sel(rows_E(lw)));
   };
-  // at the start of phase P. The K/V rows of layer
-  // l + 1 are not on this schedule: phase C of layer l issues them (after its own loads), four
-  // phases ahead, so that at B they wait on nothing newer than themselves but the A weights.
+  // at the start of phase P. The K/V rows of layer l + 1 are not on this schedule: phase D of
+  // layer l issues them (after its own loads), three phases ahead, so that at B they wait on nothing
+  // newer than themselves but the rest of the QKV weights. (At phase C they added up to 32 KB per
+  // attention workgroup to the down-projection burst in front of the o_proj exchange: measured on
+  // MI355X, 1-7 us per token slower with two register rows, at both model widths.)
   auto issue_ahead = [&](auto pc, int layer) {
     constexpr int P = decltype(pc)::value;
     constexpr int Q = P + DIST;
@@ -1005,7 +1007,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
       if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
       else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
     }
-    if constexpr (P == 2) load_phase(std::integral_constant<int, 1>(), layer + 1);
+    if constexpr (P == 3) load_phase(std::integral_constant<int, 1>(), layer + 1);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1740,4 +1742,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.14 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.15 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
