@@ -949,7 +949,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // K/V rows: a slot this workgroup's split does not attend to (or a workgroup without a split)
   // skips its load. The compiler then counts these two loads as possibly absent, which makes a few
   // later waits one or two loads stricter; worth it at the 0.6B shape (387 vs 395 us per token at
-  // config 2), not at 1.7B (868 vs 864).
+  // config 2), not at 1.7B (862 vs 848 at config 5, 932 vs 915 from prompt 1800).
   constexpr bool KV_PRED = MK_KV_PRED;
 #ifndef MK_A_FIRST
 #define MK_A_FIRST 1
