@@ -1003,7 +1003,13 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   auto issue_ahead = [&](auto pc, int layer) {
     constexpr int P = decltype(pc)::value;
     constexpr int Q = P + DIST;
-    if constexpr (Q % 5 != 1) {
+    // At the 1.7B width the o_proj rows are issued after this workgroup's attention partial is
+    // published (with the gate/up rows) instead of at phase A start: measured on MI355X, -5.5 us
+    // per token at config 5, but +7 to +8.5 at the 0.6B width, where phase A's QKV poll is not
+    // held up by them and the later burst lands in front of the split merge.
+    constexpr bool C_LATE = H > 1024;
+    if constexpr (C_LATE && P == 1) load_phase(std::integral_constant<int, 2>(), layer);
+    if constexpr (Q % 5 != 1 && !(C_LATE && Q == 2)) {
       if constexpr (Q < 5) load_phase(std::integral_constant<int, Q>(), layer);
       else load_phase(std::integral_constant<int, Q - 5>(), layer + 1);
     }
@@ -1742,4 +1748,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.15 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.16 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
