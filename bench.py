@@ -1,18 +1,24 @@
 #!/usr/bin/env python
-"""Batch-1 decode throughput of the MI355X mega-kernel on BASELINE.json's config 2.
+"""Batch-1 decode throughput of the MI355X mega-kernel on a BASELINE.json config (default: config 2).
 
-Workload (config 2): Qwen3-0.6B-shaped model, random-init bf16 weights from seed 0 (std 0.02,
-norms 1), 32-token random prompt (seed 1), cache 512, 256 teacher-forced greedy decode steps.
-A "step" is one call of the decode operator (one cooperative kernel launch): one token through
-the whole model at context position+1 in [33, 288].
+Workloads (``--config``), all random-init bf16 weights from seed 0 (std 0.02, norms 1), a random
+prompt (seed 1), teacher-forced greedy decode steps:
+  2  Qwen3-0.6B shape, prompt 32, cache 512, 256 steps (ctx 33..288) -- the headline metric;
+  4  Qwen3-0.6B shape, prompt 3584, cache 4096, 256 steps (ctx 3585..3840);
+  5  Qwen3-1.7B shape, prompt 512, cache 2048, 256 steps (ctx 513..768).
+A "step" is one call of the decode operator (one kernel launch): one token through the whole
+model at context position+1. ``--steps`` changes the number of timed steps (the workload string
+says which were run).
 
 Legs:
   * CPU baseline (rank 0, N=1): Transformers' bf16 CPU decode of the same model and prompt -- the
     reference path's own comparison decode -- timed per step with perf_counter on all host cores
     this process may use. It also yields the reference (teacher) tokens the GPU leg feeds.
-  * GPU: the prefill K/V copied into the kernel cache, W untimed warm-up steps (then the cache is
-    restored), K timed steps between synchronizations. HIP events on the operator's stream time
-    every launch; the roofline divides each step's algorithmic bytes by its kernel time.
+  * GPU: built with the product's own helpers (``model.build_model``, ``megakernel.rope_tables``,
+    ``megakernel.copy_prefill_cache``): the prefill K/V copied into the kernel cache, W untimed
+    warm-up steps (then the cache is restored), K timed steps between synchronizations. A HIP
+    event pair on the operator's stream brackets the timed launches; the roofline divides the
+    steps' algorithmic bytes by that kernel time.
 
 Algorithmic bytes per step B(ctx) = all weights read once (every layer, the full tied LM head,
 one embedding row, the norms) + K/V read for ctx positions + the new K/V row + one cos/sin row.
@@ -32,17 +38,32 @@ for p in (REPO, os.path.join(REPO, "mega-kernel_amd")):
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, B/s
 METRIC = "batch-1 decode tokens/sec (Qwen3-0.6B shape) + % of HBM roofline GB/s"
-REF_TOKS_PER_S = 325.57  # reference's published mega-kernel decode rate (RTX 3090)
+REF_TOKS_PER_S = 325.57  # reference's published mega-kernel decode rate (RTX 3090, 0.6B, cache 512)
+CONFIGS = {  # BASELINE.json configs that are bench workloads: shape, prompt, cache
+    2: ("qwen3-0.6b", 32, 512),
+    4: ("qwen3-0.6b", 3584, 4096),
+    5: ("qwen3-1.7b", 512, 2048),
+}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS), help="BASELINE.json config")
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps (K)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed warm-up decode steps (W)")
-    ap.add_argument("--shape", default="qwen3-0.6b", choices=["qwen3-0.6b", "qwen3-1.7b"])
-    ap.add_argument("--prompt", type=int, default=32)
-    ap.add_argument("--max-seq", type=int, default=512)
+    ap.add_argument("--launch", default="plain", choices=["plain", "cooperative"],
+                    help="plain hipLaunchKernel (default) or hipLaunchCooperativeKernel")
     ap.add_argument("--cpu-steps", type=int, default=None,
                     help="steps of the CPU baseline sample (default: same as --steps, capped at 256)")
     ap.add_argument("--cpu-min-seconds", type=float, default=10.0,
@@ -52,10 +73,15 @@ def parse():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the timed steps, copy a device buffer of this many MiB (device to device) so a "
                          "rocprofv3 --pmc run of this command also measures FETCH_SIZE/WRITE_SIZE of a plain copy")
-    ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "decode_traffic_qwen3-0.6b_p32_c512.json"),
-                    help="measured HBM traffic per launch (JSON written from the rocprofv3 --pmc runs); used only "
-                         "when its kernel version and workload match this run")
-    return ap.parse_args()
+    ap.add_argument("--traffic", default=None,
+                    help="measured HBM traffic per launch (JSON written from the rocprofv3 --pmc runs; default: "
+                         "profiles/decode_traffic_<shape>_p<prompt>_c<cache>.json); used only when its kernel "
+                         "version, workload and step count match this run")
+    a = ap.parse_args()
+    a.shape, a.prompt, a.max_seq = CONFIGS[a.config]
+    if a.traffic is None:
+        a.traffic = os.path.join(REPO, "profiles", f"decode_traffic_{a.shape}_p{a.prompt}_c{a.max_seq}.json")
+    return a
 
 
 def main():
@@ -66,27 +92,29 @@ def main():
         return 2
     import torch
     import megakernel
-    from oracle import hf
-    from oracle.spec import SHAPES
+    import model as driver  # the product's driver (mega-kernel_amd/model.py)
 
-    shape = SHAPES[a.shape]
-    if a.prompt + a.steps > a.max_seq:
+    if a.prompt + a.steps > a.max_seq or a.prompt + a.warmup > a.max_seq:
         print("bench.py: prompt + steps exceeds the cache length", file=sys.stderr)
         return 2
     kernel = megakernel.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    kernel.set_launch_mode(1 if a.launch == "cooperative" else 0)
 
     # ---- model (CPU, seeded) and its weights on the GPU ------------------------------------
     t0 = time.perf_counter()
-    model = hf.build_model(a.shape, max_positions=max(4096, a.max_seq))
+    model = driver.build_model(a.shape, max(4096, a.max_seq))
     build_s = time.perf_counter() - t0
-    ids = hf.prompt_ids(a.prompt, shape.vocab)
+    n_layers = len(model.model.layers)
+    vocab = model.config.vocab_size
+    ids = torch.randint(0, vocab, (1, a.prompt), generator=torch.Generator().manual_seed(1))
 
     # ---- CPU baseline leg: Transformers decode on the host cores -----------------------------
     cpu = None
     n_cpu = min(a.cpu_steps or a.steps, 256)
     if not a.no_cpu_baseline:
+        from oracle import hf  # the CPU baseline leg only: Transformers on the host
         cores = hf.cpu_threads()
         torch.set_num_threads(cores)
         ref = hf.greedy_reference(model, ids, max(n_cpu, 1))
@@ -102,6 +130,7 @@ def main():
         med = statistics.median(secs)
         teacher = list(ref["tokens"])
         cpu = {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": cores, "kind": "reference",
+               "cpu_model": cpu_model(),
                "sample": (f"Transformers {__import__('transformers').__version__} Qwen3ForCausalLM bf16 on the host "
                           f"CPU: the reference path's own comparison decode (/root/reference/model.py:139-173) run "
                           f"on CPU, same weights and prompt, {len(ref['seconds'])} greedy decode steps after a "
@@ -111,16 +140,16 @@ def main():
         teacher = []
     g = torch.Generator().manual_seed(2)
     while len(teacher) < a.steps + a.warmup:
-        teacher.append(int(torch.randint(0, shape.vocab, (1,), generator=g)))
+        teacher.append(int(torch.randint(0, vocab, (1,), generator=g)))
 
-    # ---- GPU leg -----------------------------------------------------------------------------
+    # ---- GPU leg (product helpers only) -----------------------------------------------------
     embed = model.model.embed_tokens.weight.detach().to(dev)
     final_norm = model.model.norm.weight.detach().to(dev)
     layers = [t.to(dev) for t in megakernel.layer_weight_list(model)]
-    cos, sin = hf.rope_tables(model, a.max_seq)
-    cos, sin = cos.to(dev), sin.to(dev)
-    _, cache = hf.prefill(model, ids)
-    kc0, vc0 = megakernel.empty_cache(shape.layers, a.max_seq, dev)
+    cos, sin = megakernel.rope_tables(model, a.max_seq, dev)
+    with torch.inference_mode():
+        cache = model(ids, use_cache=True).past_key_values
+    kc0, vc0 = megakernel.empty_cache(n_layers, a.max_seq, dev)
     P = megakernel.copy_prefill_cache(cache, kc0, vc0)
     kc, vc = kc0.clone(), vc0.clone()
     del model, cache
@@ -162,17 +191,21 @@ def main():
         del src, dst
 
     ctxs = [P + t + 1 for t in range(a.steps)]
-    bytes_steps = [shape.bytes_per_token(c) for c in ctxs]
+    bytes_steps = [bytes_per_token(embed.shape[1], layers[8].shape[0], n_layers, vocab, c) for c in ctxs]
     achieved = sum(bytes_steps) / (region_ms * 1e-3)
     tok_s = a.steps / wall
-    workload = (f"BASELINE config 2: {a.shape} random-init bf16, batch 1, prompt {a.prompt}, cache {a.max_seq}, "
-                f"{a.steps} teacher-forced decode steps (ctx {ctxs[0]}..{ctxs[-1]})")
-    traffic = None
+    full = "" if a.steps == 256 else f" (BASELINE runs 256; this run {a.steps})"
+    workload = (f"BASELINE config {a.config}: {a.shape} random-init bf16, batch 1, prompt {a.prompt}, cache "
+                f"{a.max_seq}, {a.steps} teacher-forced decode steps{full} (ctx {ctxs[0]}..{ctxs[-1]})")
+    traffic, traffic_profile = None, None
     if a.traffic and os.path.exists(a.traffic):
         tr = json.load(open(a.traffic))
         if (tr.get("kernel_version") == kernel.version() and tr.get("shape") == a.shape
                 and tr.get("prompt") == a.prompt and tr.get("max_seq_len") == a.max_seq):
-            traffic = tr.get("hbm_bytes_per_launch")
+            traffic_profile = {"hbm_bytes_per_launch": tr.get("hbm_bytes_per_launch"),
+                               "dispatches": tr.get("dispatches"), "source": os.path.relpath(a.traffic, REPO)}
+            if tr.get("dispatches") == a.steps + a.warmup:  # the same steps, so the same contexts
+                traffic = tr.get("hbm_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -183,13 +216,15 @@ def main():
         "ms_per_step": round(wall * 1e3 / a.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(tok_s / REF_TOKS_PER_S, 3),
+        # the reference publishes one number: 0.6B, cache 512 (config 2's workload), on an RTX 3090
+        "vs_baseline": round(tok_s / REF_TOKS_PER_S, 3) if a.config == 2 else None,
         "dtype": "bf16",
         "data": "synthetic (random-init seeded weights, random prompt ids; no checkpoint or dataset)",
         "config": {
             "workload": workload,
             "batch": 1, "prompt": a.prompt, "max_seq_len": a.max_seq, "decode_steps": a.steps,
             "teacher_tokens": "transformers-cpu" if not a.no_cpu_baseline else "random",
+            "launch": a.launch,
             "arithmetic": "bf16 weights and K/V, bf16x2 dot products of weights with hi/lo-split fp32 "
                           "activations, fp32 accumulation",
         },
@@ -200,9 +235,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": traffic,
+            "traffic_profile": traffic_profile,
             # NKV = 1 while the attention splits are at most 32 positions long, 2 beyond
-            "kernel": ("mk::decode_kernel<1024, 3072, NKV>" if a.shape == "qwen3-0.6b"
-                       else "mk::decode_kernel<2048, 6144, NKV>"),
+            "kernel": f"mk::decode_kernel<{embed.shape[1]}, {layers[8].shape[0]}, NKV>",
             "bytes_per_launch_avg": int(sum(bytes_steps) / a.steps),
             "kernel_us_avg": round(1e3 * region_ms / a.steps, 2),
         },
@@ -211,6 +246,17 @@ def main():
     }
     print(json.dumps(out))
     return 0
+
+
+def bytes_per_token(hidden, inter, layers, vocab, ctx, q_heads=16, kv_heads=8, head_dim=128):
+    """Algorithmic HBM bytes of one decode step at context ``ctx`` (bf16): every layer weight and
+    norm, the full tied LM head, one embedding row and the final norm, the K/V rows of ``ctx``
+    positions, the new K/V row, and one cos/sin row."""
+    q, kv = q_heads * head_dim, kv_heads * head_dim
+    per_layer = (q * hidden + 2 * kv * hidden + hidden * q + 3 * inter * hidden + 2 * hidden + 2 * head_dim) * 2
+    weights = layers * per_layer + vocab * hidden * 2 + 2 * hidden * 2
+    kv_pos = layers * kv * 2 * 2
+    return weights + kv_pos * ctx + kv_pos + 2 * head_dim * 2
 
 
 def release_device():

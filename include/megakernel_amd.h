@@ -4,6 +4,18 @@
  * Plain pointers and sizes only; no torch types. Every entry point returns a hipError_t and
  * never throws. Device pointers refer to memory on the current HIP device.
  *
+ * Concurrency. A decode launch needs every CU of the device at once (one workgroup per CU,
+ * waiting on each other). Each stream that launches gets its own exchange workspace (allocated on
+ * the stream's first launch, up to 64 streams per device), so launches on different streams never
+ * share exchange words; but launches that overlap in time on one device cannot all be resident:
+ * they wait with bounded spins and end as failed launches (see "Failure" below). Serialize decode
+ * calls per device.
+ *
+ * Failure. A launch whose bounded waits give up (its workgroups could not all be resident, or the
+ * status word already asked to drain) still completes: it writes NaN logits and greedy token -1,
+ * and sets a status bit (mk_status). Every later launch on the device drains the same way until
+ * mk_reset, so a device-side token loop cannot continue from a failed step.
+ *
  * Reference interface this replaces: the extern "C" launcher of tejeshbhalla/mega-kernel,
  * declared at /root/reference/pytorch_binding.cu:9-33 and defined at
  * /root/reference/megakernel.cu:898-994, bound only by the pybind `decode` operator
@@ -62,9 +74,9 @@ typedef struct mk_model_dims {
  *   cache_len      must equal position + 1 (the reference always passes that)
  *   g_logits       fp32 [151936] output
  * The remaining scratch pointers (hidden_buffer ... g_v) are accepted for ABI compatibility and
- * not used: the kernel keeps its exchange buffers in a per-device workspace owned by the library
- * and allocated on first use. Returns hipErrorInvalidValue for a null pointer, token/position out
- * of range or cache_len != position + 1, otherwise the status of the cooperative launch.
+ * not used: the kernel keeps its exchange buffers in a per-stream workspace owned by the library
+ * and allocated on the stream's first launch. Returns hipErrorInvalidValue for a null pointer,
+ * token/position out of range or cache_len != position + 1, otherwise the status of the launch.
  */
 hipError_t launch_decode_kernel(int token_id, const void* embed_weight, const void* lm_head_weight,
                                 const void* final_norm_weight, const void* layer_weights,
@@ -115,7 +127,8 @@ hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens, int n, in
  * page block_table[i] (int32 device array of ceil(max_seq_len / page_size) entries; only entries up
  * to position are read). page_size is a power of two up to 4096, and ceil(max_seq_len / page_size)
  * at most 2048. The new K/V rows are written at `position`, through the table. An entry outside
- * [0, num_pages) reads page 0 instead and sets status bit 3 (see mk_status). Other arguments and
+ * [0, num_pages) reads page 0 instead and sets status bit 3 (see mk_status); the new K/V rows are
+ * not written when the position's own entry is such an entry. Other arguments and
  * errors as mk_decode. No reference counterpart: the reference's cache is contiguous
  * (/root/reference/model.py:79-87); this serves callers whose cache is a shared pool of pages.
  */
@@ -136,18 +149,28 @@ hipError_t mk_decode_steps_paged(const mk_model_dims* dims, int32_t* tokens, int
                                  const int32_t* block_table, int num_pages, int page_size, int position,
                                  int max_seq_len, float* logits, hipStream_t stream);
 
-/* Device status word of the current device's workspace (0 = healthy; bit 0 = a grid wait timed
- * out, results of that launch are invalid; bit 2 = a device-side input token of mk_decode_steps
- * was out of range; decoding went on with token 0; bit 3 = a block-table entry of
- * mk_decode_paged was out of range; page 0 was used). A timeout makes later launches drain early
- * until mk_reset.
- * Synchronizes with the device. No reference counterpart: the reference surfaces errors only
- * through the launch status. */
+/* Status of the current device: the OR of the status words of all its workspaces. 0 = healthy.
+ *   bit 0  a bounded wait of a launch gave up (its workgroups could not all be resident): that
+ *          launch wrote NaN logits and token -1, and every later launch drains until mk_reset;
+ *   bit 1  workgroups b and b % 8 ran on different XCDs (the kernel relies on their sharing an L2):
+ *          later launches write every exchange word through to memory (slower) until mk_reset;
+ *   bit 2  a device-side input token of mk_decode_steps was out of range: token 0 was decoded;
+ *   bit 3  a block-table entry was out of range: page 0 was read, and the new K/V rows were not
+ *          written when the position's own entry was the bad one;
+ *   bit 4  set by mk_request_drain: every later launch drains (NaN logits, token -1).
+ * Bits are set with atomic ORs and only mk_reset clears them. Synchronizes with the device.
+ * No reference counterpart: the reference surfaces errors only through the launch status. */
 hipError_t mk_status(uint32_t* status);
 
-/* Clears the status word and the workspace's barrier counters of the current device.
- * Synchronizes with the device. No reference counterpart. */
+/* Clears the status words and the exchange words of every workspace of the current device and
+ * restarts their launch sequences. Synchronizes with the device. No reference counterpart. */
 hipError_t mk_reset(void);
+
+/* Sets status bit 4 on every workspace of the current device, so that every later launch drains at
+ * once (all its waits give up, NaN logits, token -1) until mk_reset: lets a caller abandon work it
+ * has queued (a long mk_decode_steps), and lets tests exercise the failure path with every kernel
+ * still exiting normally. Synchronizes with the device. No reference counterpart. */
+hipError_t mk_request_drain(void);
 
 /* Phase tracing (profiling builds and tools; no reference counterpart -- the reference has no
  * in-kernel timers). With a non-NULL device buffer of at least mk_trace_bytes() bytes, every later
@@ -168,8 +191,8 @@ int mk_grid_size(void);
  * cooperative launch (hipLaunchCooperativeKernel: the runtime guarantees that all workgroups are
  * resident before the grid starts, at ~16 us per token). Either way the grid needs every CU; with a
  * plain launch a kernel of another stream or process that holds CUs makes the decode wait and, past
- * its bounded spins, end with the status timeout bit set. No reference counterpart (the reference
- * always launches cooperatively, /root/reference/megakernel.cu:975-990). */
+ * its bounded spins, end as a failed launch (status bit 0, NaN logits, token -1). No reference
+ * counterpart (the reference always launches cooperatively, /root/reference/megakernel.cu:986-993). */
 hipError_t mk_set_launch_mode(int cooperative);
 
 /* Library version string. */

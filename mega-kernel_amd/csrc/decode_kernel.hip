@@ -5,11 +5,13 @@
 // residual} -> final RMSNorm -> tied LM head -> greedy argmax. This is the work of the reference's
 // decode_kernel (/root/reference/megakernel.cu:744-893), re-planned for 256 CUs in 8 XCDs.
 //
-// Placement. One 576-thread workgroup (9 waves) per CU. Workgroup b runs on XCD x = b % 8 as
-// local workgroup j = b / 8 (the dispatcher's round-robin placement; every workgroup checks its
-// HW_REG_XCC_ID). XCD x owns K/V head x -- the 512 Q/K/V rows of that group, its attention and its
-// 256 columns of o_proj -- plus a 1/8 slice of the MLP intermediate, so within a layer only two
-// exchanges (the o_proj and down_proj partial sums) leave the XCD.
+// Placement. One 576-thread workgroup (9 waves) per CU. The dispatcher deals workgroups to the 8
+// XCDs round-robin, so workgroups b and b % 8 share an XCD (which physical XCD a group starts on
+// varies with the hardware queue; only the grouping matters). Workgroup b is local workgroup
+// j = b / 8 of group x = b % 8, checked from HW_REG_XCC_ID at the end of every launch. Group x owns
+// K/V head x -- the 512 Q/K/V rows of that head group, its attention and its 256 columns of o_proj --
+// plus a 1/8 slice of the MLP intermediate, so within a layer only two exchanges (the o_proj and
+// down_proj partial sums) leave the XCD.
 //
 // Roles. Wave 0 of every workgroup is the communication wave: it publishes this workgroup's
 // results, polls for other workgroups' results and does the vector work (residual, RMSNorm, q/k
@@ -31,7 +33,7 @@
 // per layer of every launch (also by workgroups that have nothing to put in it) and read before any
 // writer can reach the next layer's write; consecutive writes of a word therefore carry epochs at
 // most 127 apart (never 0 mod 255), so no buffer needs clearing and no stale word can pass for a
-// fresh one. Each model shape has its own workspace.
+// fresh one. Each model shape has its own workspace, and each launching stream its own set of them.
 //
 // Variants chosen per launch on the host: one or two K/V rows per math group held in registers
 // (template NKV), a contiguous or a paged K/V cache (block table in LDS), and a token read from
@@ -83,11 +85,14 @@ constexpr int APW = 264;      // LL words per attention partial: acc[2][128], m0
 constexpr float EPS = 1e-6f;
 constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
 constexpr uint32_t SPIN_LIMIT = 1u << 22;
-constexpr uint32_t ERR_TIMEOUT = 1u;
-constexpr uint32_t ERR_PLACEMENT = 2u;
-constexpr uint32_t ERR_TOKEN = 4u;  // a device-side input token was out of range (token 0 used)
-constexpr uint32_t ERR_PAGE = 8u;   // a block-table entry was out of range (page 0 used)
-constexpr uint32_t ERR_DRAIN = ~(ERR_TOKEN | ERR_PAGE);  // status bits that make the waits give up
+// Status word bits (all set with an atomic OR, never cleared by the kernel; mk_reset clears them).
+constexpr uint32_t ERR_TIMEOUT = 1u;    // a bounded wait gave up: that launch's results are invalid
+constexpr uint32_t ERR_PLACEMENT = 2u;  // workgroups b and b % 8 ran on different XCDs: later launches
+                                        // write every exchange word through to memory
+constexpr uint32_t ERR_TOKEN = 4u;      // a device-side input token was out of range (token 0 used)
+constexpr uint32_t ERR_PAGE = 8u;       // a block-table entry was out of range (page 0 read, no write)
+constexpr uint32_t ERR_HOST = 16u;      // set by the host (mk_request_drain)
+constexpr uint32_t ERR_DRAIN = ERR_TIMEOUT | ERR_HOST;  // bits that make every launch drain at once
 constexpr int MAX_PAGES = 2048;     // block-table entries a paged launch may use (LDS copy)
 #ifndef MK_PF_DIST
 #define MK_PF_DIST 2
@@ -137,6 +142,7 @@ struct KArgs {
   u64* xw;          // exchange workspace
   uint64_t* trace;  // optional: per-workgroup phase timestamps (TRACE_N per workgroup)
   int token, position, max_seq, num_layers, vocab;
+  int force_wt;     // write every exchange word through to memory (placement not verified)
 };
 
 // Phase timestamps (s_memrealtime, 100 MHz), TRACE_PER_LAYER slots per layer, see TraceSlot.
@@ -251,7 +257,7 @@ __device__ __forceinline__ void ll_poll(Comm& c, const uint32_t* base, const int
   auto check = [&](uint32_t it) {
     if ((it & 62u) == 62u && (ld_dev_u32(c.status) & ERR_DRAIN) != 0) { c.failed = true; return true; }
     if (it > SPIN_LIMIT) {
-      if ((threadIdx.x & 63) == 0) st_dev_u32(c.status, ERR_TIMEOUT);
+      if ((threadIdx.x & 63) == 0) raise_status(c.status, ERR_TIMEOUT);
       c.failed = true;
       return true;
     }
@@ -598,15 +604,17 @@ struct Smem {
   float gq[MG][2][D + 4];            // attention partials of the 32 math groups: acc[128], m, l
   u64 best[NMW];
   uint32_t seq, wt;                  // launch sequence and write-through mode, set by the comm wave
+  uint32_t failed;                   // the launch drained (set before the LM head): logits are NaN
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
   int32_t bt[MAX_PAGES];             // block table of a paged launch (entries up to the position)
 };
 
 // Element offset of the K/V row of `head` at position p in layer `layer`: contiguous
-// [L][HKV][max_seq][D] cache, or the paged layout through the block table's LDS copy.
+// [L][HKV][max_seq][D] cache, or the paged layout through the block table's LDS copy (an invalid
+// entry, -1 there, reads page 0).
 __device__ __forceinline__ size_t kv_off(const KArgs& a, const int32_t* bt, int layer, int head, int p) {
   if (a.block_table) {
-    const size_t page = (size_t)bt[p >> a.page_shift];
+    const size_t page = (size_t)max(bt[p >> a.page_shift], 0);
     return (((((size_t)layer * a.num_pages + page) * HKV + head) << a.page_shift) + (p & ((1 << a.page_shift) - 1))) * D;
   }
   return (((size_t)layer * HKV + head) * a.max_seq + p) * D;
@@ -862,6 +870,7 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
   for (int k = 0; k < LCPL; ++k) { xh[k] = sm.xh[k * 64 + lq]; xl[k] = sm.xl[k * 64 + lq]; }
   auto lm_load = [&](int s, uint4 (&b)[LCPL]) { T::load(a, nmine, s, mwq, lq, b); };
   u64 best = 0;
+  const bool failed = __builtin_amdgcn_readfirstlane(sm.failed) != 0;
   for (int s0 = 0; s0 < nmine; s0 += LP) {
 #pragma unroll
     for (int i = 0; i < LP; ++i) {
@@ -869,7 +878,7 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
       const int s = s0 + i;
       const int row = row_of(s, mwq);
       if (s < nmine && row <= rlast) {
-        if (lq == 0) gpw(a.logits)[row] = v;
+        if (lq == 0) gpw(a.logits)[row] = failed ? __builtin_nanf("") : v;
         best = umax64(best, argmax_key(v, row));
       }
       lm_load(s + LP, buf[i]);
@@ -879,8 +888,10 @@ __device__ __forceinline__ void lm_head(const KArgs& a, Smem<H, I>& sm, int mw, 
 }
 
 // Copies the layer table, and for a paged launch the block-table entries up to the position, into
-// LDS (math waves, before the first barrier). An entry outside [0, num_pages) reads page 0 instead
-// and sets the status bit ERR_PAGE, so no access leaves the page pool.
+// LDS (math waves, before the first barrier). An entry outside [0, num_pages) is kept as -1: reads
+// through it take page 0, the new K/V row is not written when its page is such an entry, and the
+// status bit ERR_PAGE is set, so no access leaves the page pool and no other sequence's page is
+// overwritten.
 template <int H, int I>
 __device__ __forceinline__ void copy_layer_table(const KArgs& a, Smem<H, I>& sm) {
   constexpr int TW = (int)(sizeof(mk_layer_weights) / 8);
@@ -893,9 +904,9 @@ __device__ __forceinline__ void copy_layer_table(const KArgs& a, Smem<H, I>& sm)
     for (int i = threadIdx.x - 64; i < np; i += NT - 64) {
       const int v = a.block_table[i];
       bad |= v < 0 || v >= a.num_pages;
-      sm.bt[i] = (v < 0 || v >= a.num_pages) ? 0 : v;
+      sm.bt[i] = (v < 0 || v >= a.num_pages) ? -1 : v;
     }
-    if (bad) st_dev_u32(reinterpret_cast<uint32_t*>(a.xw + X_STATUS), ERR_PAGE);
+    if (bad) raise_status(reinterpret_cast<uint32_t*>(a.xw + X_STATUS), ERR_PAGE);
   }
 }
 
@@ -1159,16 +1170,20 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
   const uint32_t seq = ld_dev_u32(reinterpret_cast<const uint32_t*>(xw + X_SEQ));
   const uint32_t st0 = ld_dev_u32(c.status);
   {
-    c.wt = (st0 & ERR_PLACEMENT) != 0;
+    // A launch after a failed one (or after mk_request_drain) drains from the start: every wait
+    // gives up at once and the logits come out NaN, until mk_reset.
+    c.failed = (st0 & ERR_DRAIN) != 0;
+    // Write-through when the host could not verify the placement, or an earlier launch found
+    // workgroups b and b % 8 on different XCDs (checked at the end of every launch).
+    c.wt = a.force_wt != 0 || (st0 & ERR_PLACEMENT) != 0;
     if (lane == 0) { sm.seq = seq; sm.wt = c.wt ? 1u : 0u; }
-    if (xcc_id() != (unsigned)xcd && lane == 0) st_dev_u32(c.status, st0 | ERR_PLACEMENT);
   }
   {
     int token = a.token;
     if (a.token_in) {  // every workgroup reads the same word, so all take the same branch below
       token = (int)ld_dev_u32(reinterpret_cast<const uint32_t*>(a.token_in));
       if (token < 0 || token >= a.vocab) {
-        if (lane == 0) st_dev_u32(c.status, st0 | ERR_TOKEN);  // keeps the bits already set
+        if (lane == 0) raise_status(c.status, ERR_TOKEN);
         token = 0;
       }
     }
@@ -1251,7 +1266,9 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
         const u4v pk = {pack_bf16x2(src[0], src[1]), pack_bf16x2(src[2], src[3]), pack_bf16x2(src[4], src[5]),
                         pack_bf16x2(src[6], src[7])};
         *reinterpret_cast<u4v*>(&sm.kvn[part - 2][8 * tt]) = pk;
-        if (j == S - 1) {  // the split that owns `position` stores the new K/V in the cache
+        // the split that owns `position` stores the new K/V in the cache (not through an invalid
+        // block-table entry)
+        if (j == S - 1 && (!a.block_table || sm.bt[st.position >> a.page_shift] >= 0)) {
           uint16_t* cache = part == 2 ? a.k_cache : a.v_cache;
           *gpw(reinterpret_cast<u4v*>(cache + kv_off(a, sm.bt, layer, xcd, st.position) + 8 * tt)) = pk;
         }
@@ -1406,8 +1423,17 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
       const float mine = lane < G::HPW ? sm.up[lane] : 0.f;
       mark(a, tl + T_E_PUB);
       comm_cross_reduce<H>(c, xl, W_EX, W_EL, xcd, j, mine, ep, res, a, tl + T_E_XPOLL, tl + T_E_LPOLL);
-      if (layer + 1 < L) norm_input<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm
-      else comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // the final norm, for the LM head
+      if (layer + 1 < L) {
+        norm_input<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // next layer's input norm
+      } else {
+        // Every exchange of this launch has been consumed. If this workgroup drained, or any
+        // workgroup whose results reached it did (it set a drain bit before publishing them), the
+        // LM head writes NaN: a failed launch is visible in its output without a host sync. The
+        // status load is issued before the final norm so that its latency overlaps it.
+        const uint32_t stw = ld_dev_u32(c.status);
+        comm_norm<H>(res, sm.nw[(layer + 1) & 1], sm.xh, sm.xl);  // the final norm, for the LM head
+        if (lane == 0) sm.failed = (c.failed || (stw & ERR_DRAIN) != 0) ? 1u : 0u;
+      }
     }
     lds_barrier();  // (E2)
     if (layer + 1 < L) rs_in = norm_scale<H>(res);
@@ -1421,23 +1447,42 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
     u64 b = 0;
 #pragma unroll
     for (int w = 0; w < NMW; ++w) b = umax64(b, sm.best[w]);
-    // this workgroup's best key and done flag, in its own slot: key first, flag after it
+    // this workgroup's best key and done flag, in its own slot: key first, flag after it. The flag
+    // carries the epoch in its low 32 bits and the XCD this workgroup ran on above them.
     u64* mine = xw + X_DONE + (size_t)blockIdx.x * 16;
     if (lane == 0) __hip_atomic_store(mine, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_vmem();
-    if (lane == 0) __hip_atomic_store(mine + 1, (u64)ep_end, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      __hip_atomic_store(mine + 1, (u64)ep_end | ((u64)xcc_id() << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (blockIdx.x == 0) {
       // the grid's greedy token: poll all 256 done flags (4 per lane), then reduce the keys
+      u64 f[4] = {0, 0, 0, 0};
       for (uint32_t it = 0; !c.failed; ++it) {
         bool ok = true;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          ok &= __hip_atomic_load(xw + X_DONE + (size_t)(lane * 4 + q) * 16 + 1, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT) == (u64)ep_end;
+        for (int q = 0; q < 4; ++q) {
+          f[q] = __hip_atomic_load(xw + X_DONE + (size_t)(lane * 4 + q) * 16 + 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+          ok &= (uint32_t)f[q] == ep_end;
+        }
         if (__ballot(!ok) == 0) break;
         if ((it & 63u) == 63u && (ld_dev_u32(c.status) & ERR_DRAIN) != 0) c.failed = true;
-        if (it > SPIN_LIMIT) { if (lane == 0) st_dev_u32(c.status, ERR_TIMEOUT); c.failed = true; }
+        if (it > SPIN_LIMIT) { if (lane == 0) raise_status(c.status, ERR_TIMEOUT); c.failed = true; }
       }
+      if (!c.failed) {
+        // The local exchanges rely on workgroups b and b % 8 sharing an XCD (and so an L2); which
+        // physical XCD a group lands on does not matter (the dispatcher may start at any XCD).
+        // Lane l holds workgroups 4l..4l+3; workgroup 4l + q's group leader 4(l % 2) + q is slot q
+        // of lane l % 2.
+        bool bad = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int x = (int)(f[q] >> 32);
+          bad |= x != __shfl(x, lane & 1);
+        }
+        if (__ballot(bad) != 0 && lane == 0) raise_status(c.status, ERR_PLACEMENT);
+      }
+      const bool failed = c.failed || (ld_dev_u32(c.status) & ERR_DRAIN) != 0;
       u64 m = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -1445,7 +1490,8 @@ __device__ __forceinline__ void comm_role(const KArgs& a, Smem<H, I>& sm, const 
                                         __HIP_MEMORY_SCOPE_AGENT));
       for (int off = 32; off >= 1; off >>= 1) m = umax64(m, __shfl_xor(m, off));
       if (lane == 0) {
-        if (a.out_token) *gpw(a.out_token) = m ? (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu)) : -1;
+        // a failed launch reports token -1 (its logits are NaN)
+        if (a.out_token) *gpw(a.out_token) = (m && !failed) ? (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu)) : -1;
         st_dev_u32(reinterpret_cast<uint32_t*>(xw + X_SEQ), seq + 1);  // every workgroup read seq at its start
       }
     }
@@ -1463,17 +1509,49 @@ __global__ void __launch_bounds__(NT, 1) decode_kernel(const KArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Host side: per-device workspace and launch
+// Host side: per-device state, exchange workspaces and launch
 // ------------------------------------------------------------------------------------------
+// A workspace set holds one WS_BYTES workspace per supported model shape, so that every word of a
+// workspace is written at every layer of every launch that uses it (the epoch rule above).
+constexpr int NSHAPE = 2;
+constexpr size_t WS_SET_WORDS = NSHAPE * X_WORDS;
+constexpr size_t WS_SET_BYTES = WS_SET_WORDS * 8;
+
+// Zeroes a workspace set and starts each shape's launch sequence at 1 (a zeroed word has epoch 0,
+// which never matches). A fill kernel rather than a memset.
+__global__ void ws_init_kernel(u64* ws) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < WS_SET_WORDS; i += (size_t)gridDim.x * blockDim.x)
+    ws[i] = (i % X_WORDS == X_SEQ) ? 1ull : 0ull;  // the sequence is the low 32 bits of its word
+}
+
+// OR status bits into every shape's status word of a workspace set (mk_request_drain).
+__global__ void ws_raise_kernel(u64* ws, uint32_t bits) {
+  if (threadIdx.x < NSHAPE) raise_status(reinterpret_cast<uint32_t*>(ws + threadIdx.x * X_WORDS + X_STATUS), bits);
+}
+
+// Each workgroup of a grid of NWG records the XCD it runs on.
+__global__ void placement_probe(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+constexpr int MAX_DEVICES = 64;
+constexpr int MAX_STREAMS = 64;  // workspace sets per device (one per stream that launches)
+
+struct Workspace {
+  hipStream_t stream;
+  void* ws;
+};
 struct DeviceState {
   bool init = false;
-  bool ok = false;
-  bool cooperative = false;  // launch mode, see launch()
-  void* ws = nullptr;
-  uint64_t* trace = nullptr;  // set by mk_set_trace; null in normal operation
+  hipError_t err = hipSuccess;  // why the device cannot run the kernel, if it cannot
+  bool cooperative = false;     // launch mode, see launch()
+  bool force_wt = false;        // placement b % 8 not confirmed: exchanges write through
+  int nws = 0;
+  Workspace ws[MAX_STREAMS];
+  uint64_t* trace = nullptr;    // set by mk_set_trace; null in normal operation
 };
-constexpr int MAX_DEVICES = 64;
 static DeviceState g_dev[MAX_DEVICES];
+
 static std::mutex g_mu;
 
 template <int H, int I>
@@ -1487,43 +1565,77 @@ static hipError_t check_kernel_fits() {
   return hipSuccess;
 }
 
-// Workspaces per device, one per supported model shape: NSHAPE * WS_BYTES.
-constexpr int NSHAPE = 2;
-
-// Zero every exchange word and status word and start each launch sequence at 1 (a zeroed word
-// has epoch 0, which never matches).
-static hipError_t clear_workspace(void* ws) {
-  hipError_t e = hipMemset(ws, 0, NSHAPE * WS_BYTES);
-  if (e != hipSuccess) return e;
-  const uint32_t one = 1;
-  for (int i = 0; i < NSHAPE; ++i) {
-    e = hipMemcpy((char*)ws + i * WS_BYTES + X_SEQ * 8, &one, 4, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return e;
-  }
-  return hipDeviceSynchronize();
+// Can device `dev` run the kernel: 256 CUs, cooperative launch support, one workgroup per CU.
+static hipError_t check_device(int dev) {
+  int cus = 0, coop = 0;
+  hipError_t e;
+  if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+  if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev)) != hipSuccess) return e;
+  if (cus != NWG || !coop) return hipErrorNotSupported;
+  if ((e = check_kernel_fits<1024, 3072>()) != hipSuccess) return e;
+  return check_kernel_fits<2048, 6144>();
 }
 
+// First use of a workspace set: check the workgroup placement the kernel relies on (workgroups b
+// and b % 8 on one XCD, the 8 groups on 8 XCDs), using the set's done-key area for the probe's
+// output, then zero the set. Synchronizes `stream` once. *placement_ok tells whether the probe's
+// grid was placed that way.
+static hipError_t init_workspace(void* ws, hipStream_t stream, bool* placement_ok) {
+  uint32_t* probe = reinterpret_cast<uint32_t*>(static_cast<u64*>(ws) + X_DONE);
+  hipLaunchKernelGGL(placement_probe, dim3(NWG), dim3(64), 0, stream, probe);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  uint32_t ids[NWG];
+  if ((e = hipMemcpyAsync(ids, probe, sizeof ids, hipMemcpyDeviceToHost, stream)) != hipSuccess) return e;
+  if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+  // workgroups b and b % 8 share an XCD, and the 8 groups sit on 8 different XCDs
+  bool ok = true;
+  for (int b = 0; b < NWG; ++b) ok &= ids[b] == ids[b % NXCD];
+  for (int x = 0; x < NXCD; ++x)
+    for (int y = 0; y < x; ++y) ok &= ids[x] != ids[y];
+  *placement_ok = ok;
+  hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<u64*>(ws));
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return hipStreamSynchronize(stream);
+}
+
+static hipError_t current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return e;
+  return (*dev < 0 || *dev >= MAX_DEVICES) ? hipErrorInvalidDevice : hipSuccess;
+}
+
+// The current device's state, checked once. Allocates nothing.
 static hipError_t device_state(DeviceState** out) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e = current_device(&dev);
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState& s = g_dev[dev];
   if (!s.init) {
     s.init = true;
-    int cus = 0, coop = 0;
-    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-    if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev)) != hipSuccess) return e;
-    if (cus != NWG || !coop) return hipErrorNotSupported;
-    if ((e = check_kernel_fits<1024, 3072>()) != hipSuccess) return e;
-    if ((e = check_kernel_fits<2048, 6144>()) != hipSuccess) return e;
-    if ((e = hipMalloc(&s.ws, NSHAPE * WS_BYTES)) != hipSuccess) return e;
-    if ((e = clear_workspace(s.ws)) != hipSuccess) return e;
-    s.ok = true;
+    s.err = check_device(dev);
   }
-  if (!s.ok) return hipErrorNotSupported;
+  if (s.err != hipSuccess) return s.err;
   *out = &s;
+  return hipSuccess;
+}
+
+// The workspace set of `stream` on the current device, allocated and initialised on the stream's
+// first launch. Launches on different streams never share exchange words or epochs.
+static hipError_t stream_workspace(DeviceState* st, hipStream_t stream, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int i = 0; i < st->nws; ++i)
+    if (st->ws[i].stream == stream) { *out = st->ws[i].ws; return hipSuccess; }
+  if (st->nws == MAX_STREAMS) return hipErrorNotSupported;
+  void* ws = nullptr;
+  hipError_t e = hipMalloc(&ws, WS_SET_BYTES);
+  if (e != hipSuccess) return e;
+  bool placement_ok = false;
+  if ((e = init_workspace(ws, stream, &placement_ok)) != hipSuccess) { (void)hipFree(ws); return e; }
+  if (!placement_ok) st->force_wt = true;
+  st->ws[st->nws++] = {stream, ws};
+  *out = ws;
   return hipSuccess;
 }
 
@@ -1532,8 +1644,8 @@ static hipError_t device_state(DeviceState** out) {
 // default: it costs ~16 us less per token than a cooperative one (measured on the MI355X: 423 vs
 // 440 us per step). If a kernel from another stream or process holds CUs, the workgroups that did
 // start wait for the rest with bounded spins; past the bound the launch ends with the status
-// timeout bit set instead of hanging. mk_set_launch_mode(1) selects hipLaunchCooperativeKernel,
-// whose runtime guarantees co-residency before the grid starts.
+// timeout bit set, NaN logits and token -1 instead of hanging. mk_set_launch_mode(1) selects
+// hipLaunchCooperativeKernel, whose runtime guarantees co-residency before the grid starts.
 template <int H, int I>
 static hipError_t launch(KArgs& k, hipStream_t stream, bool cooperative) {
   void* args[] = {(void*)&k};
@@ -1575,14 +1687,42 @@ static hipError_t prepare(const mk_model_dims* dims, const void* embed_weight, c
   k.max_seq = max_seq_len;
   k.num_layers = dims->num_layers;
   k.vocab = dims->vocab;
+  k.force_wt = 0;
+  k.xw = nullptr;
+  k.trace = nullptr;
   return hipSuccess;
 }
 
-static hipError_t launch_step(const KArgs& k, bool s06, const DeviceState* st, hipStream_t stream) {
+// One launch on workspace set `ws`.
+static hipError_t launch_on(const KArgs& k, bool s06, void* ws, bool force_wt, const DeviceState* st,
+                            hipStream_t stream) {
   KArgs a = k;
-  a.xw = (u64*)((char*)st->ws + (s06 ? 0 : WS_BYTES));
+  a.xw = (u64*)((char*)ws + (s06 ? 0 : WS_BYTES));
   a.trace = st->trace;
+  a.force_wt = force_wt ? 1 : 0;
   return s06 ? launch<1024, 3072>(a, stream, st->cooperative) : launch<2048, 6144>(a, stream, st->cooperative);
+}
+
+// One launch on the stream's own workspace set.
+static hipError_t launch_step(const KArgs& k, bool s06, hipStream_t stream) {
+  DeviceState* st = nullptr;
+  hipError_t e = device_state(&st);
+  if (e != hipSuccess) return e;
+  void* ws = nullptr;
+  if ((e = stream_workspace(st, stream, &ws)) != hipSuccess) return e;
+  return launch_on(k, s06, ws, st->force_wt, st, stream);
+}
+
+// Every workspace set of the current device.
+template <typename F>
+static hipError_t for_each_workspace(F f) {
+  DeviceState* st = nullptr;
+  hipError_t e = device_state(&st);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int i = 0; i < st->nws; ++i)
+    if ((e = f(st->ws[i].ws)) != hipSuccess) return e;
+  return hipSuccess;
 }
 
 }  // namespace mk
@@ -1600,11 +1740,9 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
                          k_cache, v_cache, position, max_seq_len, logits, k, s06);
   if (e != hipSuccess) return e;
   if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
-  DeviceState* st = nullptr;
-  if ((e = device_state(&st)) != hipSuccess) return e;
   k.token = token_id;
   k.out_token = out_token;
-  return launch_step(k, s06, st, stream);
+  return launch_step(k, s06, stream);
 }
 
 // Page-table checks and fields of a paged launch (page size a power of two up to 4096, at most
@@ -1625,14 +1763,12 @@ static hipError_t set_paged(KArgs& k, const int32_t* block_table, int num_pages,
 static hipError_t run_steps(KArgs& k, bool s06, int32_t* tokens, int n, int generate, int position,
                             int max_seq_len, hipStream_t stream) {
   if (!tokens || n < 1 || (long long)position + n > max_seq_len) return hipErrorInvalidValue;
-  DeviceState* st = nullptr;
-  hipError_t e = device_state(&st);
-  if (e != hipSuccess) return e;
   for (int i = 0; i < n; ++i) {
     k.position = position + i;
     k.token_in = tokens + i;
     k.out_token = (generate || i == n - 1) ? tokens + i + 1 : nullptr;
-    if ((e = launch_step(k, s06, st, stream)) != hipSuccess) return e;
+    hipError_t e = launch_step(k, s06, stream);
+    if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
@@ -1650,11 +1786,9 @@ extern "C" hipError_t mk_decode_paged(const mk_model_dims* dims, int token_id, c
   if (e != hipSuccess) return e;
   if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
   if ((e = set_paged(k, block_table, num_pages, page_size, max_seq_len)) != hipSuccess) return e;
-  DeviceState* st = nullptr;
-  if ((e = device_state(&st)) != hipSuccess) return e;
   k.token = token_id;
   k.out_token = out_token;
-  return launch_step(k, s06, st, stream);
+  return launch_step(k, s06, stream);
 }
 
 extern "C" hipError_t mk_decode_steps(const mk_model_dims* dims, int32_t* tokens, int n, int generate,
@@ -1703,24 +1837,43 @@ extern "C" hipError_t launch_decode_kernel(int token_id, const void* embed_weigh
 
 extern "C" hipError_t mk_status(uint32_t* status) {
   if (!status) return hipErrorInvalidValue;
-  DeviceState* st = nullptr;
-  hipError_t e = device_state(&st);
+  hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
-  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  uint32_t w[NSHAPE];
-  for (int i = 0; i < NSHAPE; ++i)
-    if ((e = hipMemcpy(&w[i], (char*)st->ws + i * WS_BYTES + X_STATUS * 8, 4, hipMemcpyDeviceToHost)) != hipSuccess)
-      return e;
-  *status = w[0] | w[1];
+  uint32_t acc = 0;
+  e = for_each_workspace([&](void* ws) {
+    for (int i = 0; i < NSHAPE; ++i) {
+      uint32_t w = 0;
+      hipError_t r = hipMemcpy(&w, (char*)ws + i * WS_BYTES + X_STATUS * 8, 4, hipMemcpyDeviceToHost);
+      if (r != hipSuccess) return r;
+      acc |= w;
+    }
+    return hipSuccess;
+  });
+  if (e != hipSuccess) return e;
+  *status = acc;
   return hipSuccess;
 }
 
 extern "C" hipError_t mk_reset(void) {
-  DeviceState* st = nullptr;
-  hipError_t e = device_state(&st);
+  hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
-  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  return clear_workspace(st->ws);
+  e = for_each_workspace([](void* ws) {
+    hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, 0, static_cast<u64*>(ws));
+    return hipGetLastError();
+  });
+  if (e != hipSuccess) return e;
+  return hipDeviceSynchronize();
+}
+
+extern "C" hipError_t mk_request_drain(void) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  e = for_each_workspace([](void* ws) {
+    hipLaunchKernelGGL(ws_raise_kernel, dim3(1), dim3(64), 0, 0, static_cast<u64*>(ws), ERR_HOST);
+    return hipGetLastError();
+  });
+  if (e != hipSuccess) return e;
+  return hipDeviceSynchronize();
 }
 
 extern "C" hipError_t mk_set_trace(uint64_t* device_buffer, size_t bytes) {
@@ -1748,4 +1901,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.16 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.17 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }

@@ -26,20 +26,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
-
-// dot of 8 bf16 weights (one 16-byte chunk) with 8 fp32 activations, accumulated into acc.
-__device__ __forceinline__ float dot8(uint4 w, const float* x, float acc) {
-  acc = fmaf(bf16_lo(w.x), x[0], acc);
-  acc = fmaf(bf16_hi(w.x), x[1], acc);
-  acc = fmaf(bf16_lo(w.y), x[2], acc);
-  acc = fmaf(bf16_hi(w.y), x[3], acc);
-  acc = fmaf(bf16_lo(w.z), x[4], acc);
-  acc = fmaf(bf16_hi(w.z), x[5], acc);
-  acc = fmaf(bf16_lo(w.w), x[6], acc);
-  acc = fmaf(bf16_hi(w.w), x[7], acc);
-  return acc;
-}
 
 // ---------------------------------------------------------------------------------------------
 // Memory access with explicit cache policy.
@@ -50,7 +36,6 @@ __device__ __forceinline__ float dot8(uint4 w, const float* x, float acc) {
 // workgroup writes and another reads within a launch goes through these helpers.
 // ---------------------------------------------------------------------------------------------
 constexpr int CPOL_SC1 = 16;  // gfx940+ cache-policy bit: device (agent) scope
-constexpr int CPOL_NT = 2;    // non-temporal (streaming) hint
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
@@ -62,22 +47,13 @@ __device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t* p) {
 __device__ __forceinline__ void st_dev_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_dev_f32(const float* p) {
-  return __uint_as_float(ld_dev_u32(reinterpret_cast<const uint32_t*>(p)));
-}
-__device__ __forceinline__ void st_dev_f32(float* p, float v) {
-  st_dev_u32(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
-}
-// 16-byte device-scope load/store; byte offset from a 16-byte aligned base.
-__device__ __forceinline__ float4 ld_dev_f32x4(const float* base, uint32_t byte_off) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 r = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(base), byte_off, 0, CPOL_SC1));
-  return make_float4(r[0], r[1], r[2], r[3]);
-}
-__device__ __forceinline__ void st_dev_f32x4(float* base, uint32_t byte_off, float4 v) {
-  typedef unsigned u4 __attribute__((ext_vector_type(4)));
-  u4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-  __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), byte_off, 0, CPOL_SC1);
+// Sets status bits with a device-scope atomic OR (a vector-memory atomic of each active lane), so
+// that bits other workgroups set concurrently are kept, then a release fence: every store this
+// wave makes afterwards (its later exchange publishes) becomes visible only after the bit, so a
+// workgroup that consumes such a publish and then reads the status word sees the bit.
+__device__ __forceinline__ void raise_status(uint32_t* p, uint32_t bits) {
+  __hip_atomic_fetch_or(p, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
 }
 
 // Global-address-space views. Pointers that come out of memory (the layer table) or through
@@ -126,13 +102,6 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp<0x140>(v);  // row_mirror
   return v;
 }
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return v;
-}
 // Values of the lane holding the same position in the other 16-lane row of the pair (rows 0<->1,
 // 2<->3) and in the other 32-lane half, via the gfx950 lane-swap instructions (VALU, no LDS
 // traffic). Each builtin returns (own, partner) in some order; these combine them symmetrically.
@@ -153,9 +122,8 @@ __device__ __forceinline__ float xmax32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Full wave sum / max; every lane receives the result.
+// Full wave sum; every lane receives the result.
 __device__ __forceinline__ float wave_sum(float v) { return xsum32(xsum16(row16_sum(v))); }
-__device__ __forceinline__ float wave_max(float v) { return xmax32(xmax16(row16_max(v))); }
 
 __device__ __forceinline__ unsigned xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // HW_REG_XCC_ID[3:0]

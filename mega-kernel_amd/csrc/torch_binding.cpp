@@ -11,7 +11,9 @@
 // the device (the reference mallocs, uploads and frees it on every token); the call is fully
 // asynchronous on the current stream (the reference's cudaFree synchronizes). `decode_greedy`
 // additionally returns the fused device argmax, and the model shape (0.6B or 1.7B) is taken
-// from the tensors instead of compile-time constants.
+// from the tensors instead of compile-time constants. A launch that could not complete its grid
+// waits returns NaN logits and token -1 (no host synchronization needed to notice); `status()`
+// tells why.
 #include <torch/extension.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
@@ -268,6 +270,8 @@ int64_t status() {
 
 void reset() { MK_HIP_CHECK(mk_reset()); }
 
+void request_drain() { MK_HIP_CHECK(mk_request_drain()); }
+
 // 0 = plain launch (default), 1 = cooperative launch, for the current device
 void set_launch_mode(int64_t cooperative) {
   TORCH_CHECK(cooperative == 0 || cooperative == 1, "set_launch_mode: expected 0 or 1");
@@ -297,8 +301,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "int32 greedy token on device)");
   m.def("decode_steps_paged", &decode_steps_paged,
         "decode_steps on a paged K/V cache (tensors as decode_paged); returns the last step's fp32 logits");
-  m.def("status", &status, "device status word of the decode workspace (0 = healthy); synchronizes");
-  m.def("reset", &reset, "clear the decode workspace (exchange words, status word) and restart its launch sequence; synchronizes");
+  m.def("status", &status,
+        "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
+  m.def("reset", &reset, "clear the decode workspaces (exchange words, status words) and restart their launch sequences; synchronizes");
+  m.def("request_drain", &request_drain,
+        "set status bit 4: every later launch drains at once (NaN logits, token -1) until reset(); synchronizes");
   m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");
   m.def("check_args", &check_args, "validate decode's arguments without launching; returns (hidden, intermediate, layers, vocab)");
   m.def("version", []() { return std::string(mk_version()); });

@@ -2,11 +2,14 @@
 
 Two oracles (see ``oracle/``):
   * the fp32 restatement (``oracle.restate``, numerics="fp32"), which computes what the kernel
-    computes up to fp32 summation order -- the tight check (max-abs 5e-3, identical greedy token);
-  * Transformers itself on the CPU (the reference path), teacher-forced -- the north-star check:
-    identical greedy token on >= 99% of steps and cosine >= 0.9999 (float64) against its bf16
-    logits. Its max-abs difference is reported next to the noise floor of bf16 itself (the
-    Transformers fp32 model against the bf16 model differs by ~4e-2 on these weights).
+    computes up to fp32 summation order -- the tight check (max-abs 5e-3, identical greedy token),
+    run on the cache the kernel itself wrote;
+  * Transformers itself on the CPU (the reference path), teacher-forced. Its bf16 decode is noisy on
+    these random-init weights, so the kernel is held to a floor measured in the same run: the fp32
+    restatement teacher-forced on the same tokens from the same prefill (its own cache), compared
+    with the same Transformers logits. The kernel must be no further from Transformers than that
+    (tokens, per-step cosine, max-abs), and must meet the north-star bar (>= 99% identical tokens,
+    max-abs <= 2e-2, cosine >= 0.9999 per step) wherever the restatement meets it.
 """
 import math
 
@@ -14,49 +17,11 @@ import pytest
 import torch
 
 from oracle import hf, restate
-from oracle.spec import SHAPES
+from tests.gpu_common import DEV, Session, c_library, stats, stream_handle, Dims
 
 pytestmark = pytest.mark.gpu
 
-DEV = "cuda:0"
-
-
-class Session:
-    """One model on CPU (oracle) and its bf16 weights on the GPU (kernel)."""
-
-    def __init__(self, shape_name, max_seq):
-        self.shape = SHAPES[shape_name]
-        self.max_seq = max_seq
-        self.model = hf.build_model(shape_name, max_positions=max(max_seq, 4096))
-        import megakernel
-        self.kernel = megakernel.load()
-        self.embed = self.model.model.embed_tokens.weight.detach().to(DEV)
-        self.lm_head = self.embed  # tied
-        self.final_norm = self.model.model.norm.weight.detach().to(DEV)
-        self.layers = [t.to(DEV) for t in megakernel.layer_weight_list(self.model)]
-        self.cos_cpu, self.sin_cpu = hf.rope_tables(self.model, max_seq)
-        self.cos, self.sin = self.cos_cpu.to(DEV), self.sin_cpu.to(DEV)
-        self._W = None
-
-    @property
-    def W(self):
-        if self._W is None:
-            self._W = restate.Weights.from_model(self.model, self.shape)
-        return self._W
-
-    def prefill(self, prompt_len, seed=1):
-        ids = hf.prompt_ids(prompt_len, self.shape.vocab, seed)
-        last, cache = hf.prefill(self.model, ids)
-        kc, vc = hf.cache_to_kernel_layout(cache, self.shape.layers, self.shape.kv_heads, self.max_seq,
-                                           self.shape.head_dim)
-        return ids, last, cache, kc, vc
-
-    def decode(self, token, k_dev, v_dev, position, greedy=False):
-        args = (int(token), self.embed, self.lm_head, self.final_norm, self.layers, self.cos, self.sin,
-                k_dev, v_dev, int(position), self.max_seq)
-        if greedy:
-            return self.kernel.decode_greedy(*args)
-        return self.kernel.decode(*args)
+NS_TOKENS, NS_MAXABS, NS_COS = 0.99, 2e-2, 0.9999
 
 
 @pytest.fixture(scope="module")
@@ -74,12 +39,6 @@ def q06():
     return Session("qwen3-0.6b", 512)
 
 
-def _stats(ours, ref):
-    ours, ref = ours.double(), ref.double()
-    cos = torch.nn.functional.cosine_similarity(ours, ref, dim=0).item()
-    return (ours - ref).abs().max().item(), cos
-
-
 def test_mini_matches_fp32_restatement(mini):
     """2-layer model with the kernel's real head geometry: every step's logits and the K/V written
     to the cache agree with the fp32 restatement."""
@@ -92,10 +51,10 @@ def test_mini_matches_fp32_restatement(mini):
         tok = ref["tokens"][t]
         print(f"[mini] step {t} pos {pos} token {tok}", flush=True)
         logits, dev_tok = mini.decode(tok, kd, vd, pos, greedy=True)
-        want, _ = restate.decode_step(mini.W, kc, vc, tok, pos, mini.cos_cpu, mini.sin_cpu, numerics="fp32")
+        want = mini.oracle_step(kc, vc, tok, pos)
         got = logits.cpu()
         assert torch.isfinite(got).all()
-        maxabs, cos = _stats(got, want)
+        maxabs, cos = stats(got, want)
         assert maxabs < 5e-3, f"step {t}: max|kernel - restatement| = {maxabs}"
         assert cos > 0.999999
         assert int(dev_tok.item()) == restate.argmax_bf16(got), "device argmax != argmax of returned logits"
@@ -120,17 +79,12 @@ def test_mini_1_7b_shape_matches_fp32_restatement(mini17):
         pos = P + t
         print(f"[mini-1.7b] step {t} pos {pos} token {tok}", flush=True)
         logits, dev_tok = mini17.decode(tok, kd, vd, pos, greedy=True)
-        want, _ = restate.decode_step(mini17.W, kc, vc, tok, pos, mini17.cos_cpu, mini17.sin_cpu, numerics="fp32")
+        want = mini17.oracle_step(kc, vc, tok, pos)
         got = logits.cpu()
-        maxabs, cos = _stats(got, want)
+        maxabs, cos = stats(got, want)
         assert maxabs < 5e-3, f"step {t}: max|kernel - restatement| = {maxabs}"
         assert int(dev_tok.item()) == restate.argmax_bf16(got)
         tok = int(dev_tok.item())
-
-
-def _decode_steps(sess, tokens, n, generate, kd, vd, position):
-    return sess.kernel.decode_steps(tokens, n, generate, sess.embed, sess.lm_head, sess.final_norm, sess.layers,
-                                    sess.cos, sess.sin, kd, vd, position, sess.max_seq)
 
 
 def test_device_loop_matches_per_step_calls(mini):
@@ -138,7 +92,8 @@ def test_device_loop_matches_per_step_calls(mini):
     against a host loop of ``decode_greedy`` calls that reads each token back: the same kernel on the
     same inputs, so the tokens, the last logits and the whole cache agree bit for bit. The 32 steps
     from prompt 240 cross context 256, where the launches switch to two register K/V rows per
-    group."""
+    group. (The tokens are checked against the oracle's own greedy chain in
+    ``test_device_loop_generates_the_oracle_greedy_chain``.)"""
     P, n = 240, 32
     _, last, _, kc, vc = mini.prefill(P)
     t0 = int(last.float().argmax())
@@ -153,7 +108,7 @@ def test_device_loop_matches_per_step_calls(mini):
     kb, vb = kc.to(DEV), vc.to(DEV)
     tokens = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
     tokens[0] = t0
-    logits_b = _decode_steps(mini, tokens, n, True, kb, vb, P)
+    logits_b = mini.decode_steps(tokens, n, True, kb, vb, P)
     assert tokens[1:].tolist() == toks
     assert torch.equal(logits_b, logits_a)
     assert torch.equal(kb, ka) and torch.equal(vb, va)
@@ -163,13 +118,58 @@ def test_device_loop_matches_per_step_calls(mini):
     kt, vt = kc.to(DEV), vc.to(DEV)
     inputs = [t0] + toks[:-1]
     teach = torch.tensor(inputs + [-5], dtype=torch.int32, device=DEV)
-    logits_c = _decode_steps(mini, teach, n, False, kt, vt, P)
+    logits_c = mini.decode_steps(teach, n, False, kt, vt, P)
     assert teach[:n].tolist() == inputs and int(teach[n].item()) == toks[-1]
     assert torch.equal(logits_c, logits_a)
     assert torch.equal(kt, ka) and torch.equal(vt, va)
     assert kt[:, :, P + n:].abs().sum().item() == 0
     assert mini.kernel.status() == 0
     print("[device-loop] teacher mode matches", flush=True)
+
+
+def _top2_gap(logits):
+    v = restate.bf16(logits).topk(2).values
+    return (v[0] - v[1]).item()
+
+
+@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 240, 32), ("mini17", 100, 12)])
+def test_device_loop_generates_the_oracle_greedy_chain(shape_fixture, P, n, request):
+    """``decode_steps(generate=True)``: the tokens the device feeds itself are the fp32 restatement's
+    own greedy chain (the restatement run step by step on its own cache, each step's argmax fed to
+    the next), and the last logits agree with the restatement's last step. A greedy chain can only
+    be compared up to a near-tie of the restatement's top two logits (below 1e-3, where fp32
+    summation order may pick either); the test reports such a step and compares up to it."""
+    sess = request.getfixturevalue(shape_fixture)
+    _, last, _, kc, vc = sess.prefill(P)
+    t0 = int(last.float().argmax())
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    tokens = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
+    tokens[0] = t0
+    got_last = sess.decode_steps(tokens, n, True, kd, vd, P).cpu()
+    got = tokens.tolist()
+    want, tok, ok_steps, want_last = [t0], t0, 0, None
+    for i in range(n):
+        lg = sess.oracle_step(kc, vc, tok, P + i)
+        tok = restate.argmax_bf16(lg)
+        want.append(tok)
+        if got[i + 1] != tok:
+            gap = _top2_gap(lg)
+            print(f"[{shape_fixture} chain] step {i}: kernel {got[i + 1]} oracle {tok}, oracle top-2 gap {gap:.2e}",
+                  flush=True)
+            assert gap < 1e-3, f"step {i}: tokens differ without a near-tie"
+            break
+        ok_steps += 1
+        want_last = lg
+    print(f"[{shape_fixture} chain] {ok_steps}/{n} greedy tokens equal the oracle's: {got[1:9]} ...", flush=True)
+    assert ok_steps >= n // 2
+    if ok_steps == n:
+        maxabs, _ = stats(got_last, want_last)
+        assert maxabs < 5e-3, maxabs
+        # the cache the device loop wrote holds the restatement's rows (one bf16 rounding step)
+        for dev_c, ref_c in ((kd, kc), (vd, vc)):
+            d = (dev_c[:, :, P:P + n].float().cpu() - ref_c[:, :, P:P + n].float()).abs().max().item()
+            assert d <= 2 ** -6 * max(1.0, ref_c[:, :, P:P + n].float().abs().max().item()), d
+    assert sess.kernel.status() == 0
 
 
 def test_native_prefill_through_decode_steps(mini):
@@ -184,11 +184,11 @@ def test_native_prefill_through_decode_steps(mini):
     kc = torch.zeros(L, KV, mini.max_seq, D, dtype=torch.bfloat16)
     vc = torch.zeros_like(kc)
     for p, tok in enumerate(ids):
-        want, _ = restate.decode_step(mini.W, kc, vc, tok, p, mini.cos_cpu, mini.sin_cpu, numerics="fp32")
+        want = mini.oracle_step(kc, vc, tok, p)
     kd, vd = torch.zeros_like(kc, device=DEV), torch.zeros_like(vc, device=DEV)
     tokens = torch.tensor(ids + [-1], dtype=torch.int32, device=DEV)
-    got = _decode_steps(mini, tokens, P, False, kd, vd, 0).cpu()
-    maxabs, cos = _stats(got, want)
+    got = mini.decode_steps(tokens, P, False, kd, vd, 0).cpu()
+    maxabs, cos = stats(got, want)
     print(f"[native-prefill] P={P}: max|kernel - restatement| {maxabs:.3e}, cos {cos:.8f}", flush=True)
     assert maxabs < 5e-3 and cos > 0.999999
     assert int(tokens[P].item()) == restate.argmax_bf16(want)
@@ -196,6 +196,16 @@ def test_native_prefill_through_decode_steps(mini):
         d = (dev_c[:, :, :P].float().cpu() - ref_c[:, :, :P].float()).abs().max().item()
         assert d <= 2 ** -6 * max(1.0, ref_c.float().abs().max().item()), (name, d)
     assert kd[:, :, P:].abs().sum().item() == 0 and vd[:, :, P:].abs().sum().item() == 0
+
+
+def _paged_pool(sess, kc, vc, ps, extra, seed):
+    from tests.paged_layout import to_pages
+    npl = sess.max_seq // ps
+    pool = npl + extra
+    table = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))[:npl].to(torch.int32)
+    kp = to_pages(kc, ps, table.tolist(), pool).to(DEV)
+    vp = to_pages(vc, ps, table.tolist(), pool).to(DEV)
+    return table, kp, vp, pool
 
 
 @pytest.mark.parametrize("shape_fixture, P", [("mini", 300), ("mini17", 300), ("mini17", 488)])
@@ -206,17 +216,13 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
     the rows written through the table land where the contiguous launch writes them. 24 steps from
     prompt 300 cross page boundaries and context 256 (two register K/V rows, longer splits); from
     prompt 488 they end on the cache's last slot (511), where a K/V row read past the split would
-    leave the last page (regression: such reads once took block-table entries past the position)."""
-    from tests.paged_layout import from_pages, to_pages
+    leave the last page (regression: such reads once took block-table entries past the position).
+    (The paged path against the oracle: ``test_paged_cache_matches_oracle``.)"""
+    from tests.paged_layout import from_pages
     sess = request.getfixturevalue(shape_fixture)
     n, ps = 24, 16
     _, last, _, kc, vc = sess.prefill(P)
-    npl = sess.max_seq // ps
-    g = torch.Generator().manual_seed(7)
-    pool = npl + 9
-    table = torch.randperm(pool, generator=g)[:npl].to(torch.int32)
-    kp = to_pages(kc, ps, table.tolist(), pool).to(DEV)
-    vp = to_pages(vc, ps, table.tolist(), pool).to(DEV)
+    table, kp, vp, pool = _paged_pool(sess, kc, vc, ps, 9, 7)
     table_d = table.to(DEV)
     ka, va = kc.to(DEV), vc.to(DEV)
     tok = int(last.float().argmax())
@@ -234,22 +240,72 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
     assert sess.kernel.status() == 0
 
 
+@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6)])
+def test_paged_cache_matches_oracle(shape_fixture, P, n, request):
+    """``decode_paged`` against the fp32 restatement on the gathered cache: every step, the cache the
+    kernel has written through the block table is gathered back to ``[L, 8, max_seq, 128]`` and the
+    restatement decodes the same token at the same position on it -- logits to 5e-3, the same
+    greedy token, and the row the kernel wrote within one bf16 rounding step of the restatement's.
+    Then ``decode_steps_paged`` (teacher mode) continues for n steps and its last logits and rows are
+    checked against the restatement run step by step on its own cache."""
+    from tests.paged_layout import from_pages
+    sess = request.getfixturevalue(shape_fixture)
+    ps = 32
+    _, last, _, kc, vc = sess.prefill(P)
+    table, kp, vp, _ = _paged_pool(sess, kc, vc, ps, 5, 13)
+    table_d = table.to(DEV)
+    tok = int(last.float().argmax())
+    for i in range(n):
+        pos = P + i
+        kg, vg = from_pages(kp, table.tolist()).cpu(), from_pages(vp, table.tolist()).cpu()
+        got, dev_tok = sess.kernel.decode_paged(tok, sess.embed, sess.lm_head, sess.final_norm, sess.layers,
+                                                sess.cos, sess.sin, kp, vp, table_d, pos, sess.max_seq)
+        want = sess.oracle_step(kg, vg, tok, pos)
+        maxabs, _ = stats(got.cpu(), want)
+        assert maxabs < 5e-3, f"step {i}: max|paged kernel - restatement| {maxabs}"
+        assert int(dev_tok.item()) == restate.argmax_bf16(want)
+        for dev_c, ref_c in ((kp, kg), (vp, vg)):
+            row = from_pages(dev_c, table.tolist())[:, :, pos].float().cpu()
+            d = (row - ref_c[:, :, pos].float()).abs().max().item()
+            assert d <= 2 ** -6 * max(1.0, ref_c[:, :, pos].float().abs().max().item()), d
+        tok = int(dev_tok.item())
+    print(f"[paged oracle {shape_fixture}] {n} decode_paged steps from P={P} match the restatement", flush=True)
+
+    # decode_steps_paged, teacher-forced on the restatement's greedy chain
+    p0 = P + n
+    kc2, vc2 = from_pages(kp, table.tolist()).cpu(), from_pages(vp, table.tolist()).cpu()
+    feed, t = [], tok
+    for i in range(n):
+        feed.append(t)
+        want = sess.oracle_step(kc2, vc2, t, p0 + i)
+        t = restate.argmax_bf16(want)
+    tokens = torch.tensor(feed + [-1], dtype=torch.int32, device=DEV)
+    got = sess.kernel.decode_steps_paged(tokens, n, False, sess.embed, sess.lm_head, sess.final_norm, sess.layers,
+                                         sess.cos, sess.sin, kp, vp, table_d, p0, sess.max_seq).cpu()
+    maxabs, _ = stats(got, want)
+    assert maxabs < 5e-3, maxabs
+    assert int(tokens[n].item()) == t
+    for dev_c, ref_c in ((kp, kc2), (vp, vc2)):
+        rows = from_pages(dev_c, table.tolist())[:, :, p0:p0 + n].float().cpu()
+        d = (rows - ref_c[:, :, p0:p0 + n].float()).abs().max().item()
+        assert d <= 2 ** -6 * max(1.0, ref_c[:, :, p0:p0 + n].float().abs().max().item()), d
+    assert sess.kernel.status() == 0
+    print(f"[paged oracle {shape_fixture}] {n} decode_steps_paged steps match the restatement", flush=True)
+
+
 def test_device_loop_on_paged_cache(mini):
     """``decode_steps_paged``: greedy generation on the device over a paged cache (shuffled pages,
     NaN in the unused ones) against ``decode_steps`` on the contiguous cache -- the same tokens, the
     same last logits, and the same rows written."""
-    from tests.paged_layout import from_pages, to_pages
+    from tests.paged_layout import from_pages
     P, n, ps = 250, 20, 32
     _, last, _, kc, vc = mini.prefill(P)
-    npl = mini.max_seq // ps
-    table = torch.randperm(npl + 5, generator=torch.Generator().manual_seed(11))[:npl].to(torch.int32)
-    kp = to_pages(kc, ps, table.tolist(), npl + 5).to(DEV)
-    vp = to_pages(vc, ps, table.tolist(), npl + 5).to(DEV)
+    table, kp, vp, _ = _paged_pool(mini, kc, vc, ps, 5, 11)
     t0 = int(last.float().argmax())
     ka, va = kc.to(DEV), vc.to(DEV)
     tok_a = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
     tok_a[0] = t0
-    la = _decode_steps(mini, tok_a, n, True, ka, va, P)
+    la = mini.decode_steps(tok_a, n, True, ka, va, P)
     tok_b = torch.zeros(n + 1, dtype=torch.int32, device=DEV)
     tok_b[0] = t0
     lb = mini.kernel.decode_steps_paged(tok_b, n, True, mini.embed, mini.lm_head, mini.final_norm, mini.layers,
@@ -263,8 +319,9 @@ def test_device_loop_on_paged_cache(mini):
 
 def test_paged_cache_bad_table_entry_sets_status(mini):
     """A block-table entry outside the page pool cannot be checked on the host without a copy: the
-    kernel reads and writes page 0 instead (no access leaves the pool, nothing drains) and sets
-    status bit 3 until reset."""
+    kernel reads page 0 instead (no access leaves the pool, nothing drains), does not write the new
+    K/V rows when the bad entry is the position's own page (no other sequence's page 0 is
+    overwritten), and sets status bit 3 until reset."""
     from tests.paged_layout import to_pages
     P, ps = 40, 16
     _, _, _, kc, vc = mini.prefill(P)
@@ -273,14 +330,73 @@ def test_paged_cache_bad_table_entry_sets_status(mini):
     table[P // ps] = npl + 5  # the page holding the position being written
     kp = to_pages(kc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
     vp = to_pages(vc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
+    kp0, vp0 = kp.clone(), vp.clone()
     try:
         logits, _ = mini.kernel.decode_paged(7, mini.embed, mini.lm_head, mini.final_norm, mini.layers, mini.cos,
                                              mini.sin, kp, vp, table.to(DEV), P, mini.max_seq)
         assert mini.kernel.status() == 8
         assert torch.isfinite(logits).all()
+        assert torch.equal(kp, kp0) and torch.equal(vp, vp0), "a K/V row was written through a bad table entry"
     finally:
         mini.kernel.reset()
     assert mini.kernel.status() == 0
+
+
+def test_status_bits_accumulate(mini):
+    """Status bits are ORed in, never overwritten: one device-loop step with an out-of-range input
+    token (bit 2) on a paged cache with an out-of-range table entry (bit 3) reports 12."""
+    from tests.paged_layout import to_pages
+    P, ps = 40, 16
+    _, _, _, kc, vc = mini.prefill(P)
+    npl = mini.max_seq // ps
+    table = torch.arange(npl, dtype=torch.int32)
+    table[1] = -3
+    kp = to_pages(kc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
+    vp = to_pages(vc, ps, list(range(npl)), npl, fill=0.0).to(DEV)
+    tokens = torch.tensor([mini.shape.vocab + 1, 0], dtype=torch.int32, device=DEV)
+    try:
+        logits = mini.kernel.decode_steps_paged(tokens, 1, True, mini.embed, mini.lm_head, mini.final_norm,
+                                                mini.layers, mini.cos, mini.sin, kp, vp, table.to(DEV), P,
+                                                mini.max_seq)
+        assert torch.isfinite(logits).all()
+        assert mini.kernel.status() == 12
+    finally:
+        mini.kernel.reset()
+    assert mini.kernel.status() == 0
+
+
+def test_failed_launch_is_visible_in_band(mini):
+    """A launch whose waits give up completes normally but reports itself: NaN logits and token -1,
+    with no host synchronization needed to notice. The drain is forced from the host (status bit 4,
+    ``request_drain``), so every bounded wait gives up at once and every kernel exits normally.
+    A device-side loop cannot run on from a failed step: every later step drains too. After
+    ``reset`` the same decode is healthy again and equals a decode that never saw the drain."""
+    P = 60
+    _, last, _, kc, vc = mini.prefill(P)
+    tok = int(last.float().argmax())
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    want, want_tok = mini.decode(tok, kd, vd, P, greedy=True)
+    want_tok = int(want_tok.item())
+    assert torch.isfinite(want).all()
+    try:
+        mini.kernel.request_drain()
+        assert mini.kernel.status() == 16
+        kb, vb = kc.to(DEV), vc.to(DEV)
+        logits, dev_tok = mini.decode(tok, kb, vb, P, greedy=True)
+        assert torch.isnan(logits).all(), "a drained launch must not return finite logits"
+        assert int(dev_tok.item()) == -1
+        tokens = torch.zeros(5, dtype=torch.int32, device=DEV)
+        tokens[0] = tok
+        last_logits = mini.decode_steps(tokens, 4, True, kb, vb, P + 1)
+        assert tokens[1:].tolist() == [-1, -1, -1, -1]
+        assert torch.isnan(last_logits).all()
+        assert mini.kernel.status() & 16
+    finally:
+        mini.kernel.reset()
+    assert mini.kernel.status() == 0
+    kc2, vc2 = kc.to(DEV), vc.to(DEV)
+    again, again_tok = mini.decode(tok, kc2, vc2, P, greedy=True)
+    assert torch.equal(again, want) and int(again_tok.item()) == want_tok
 
 
 def test_split_slots_never_stale_across_launches(mini):
@@ -317,7 +433,7 @@ def test_device_loop_out_of_range_token_sets_status(mini):
     kb, vb = kc.to(DEV), vc.to(DEV)
     tokens = torch.tensor([mini.shape.vocab + 5, -1], dtype=torch.int32, device=DEV)
     try:
-        got = _decode_steps(mini, tokens, 1, True, kb, vb, P)
+        got = mini.decode_steps(tokens, 1, True, kb, vb, P)
         assert mini.kernel.status() == 4
         assert torch.equal(got, want) and torch.equal(kb, ka)
     finally:
@@ -339,150 +455,156 @@ def test_decode_writes_only_its_slot(mini):
     assert ((vd != before_v).any(dim=-1)[:, :, :P]).sum() == 0
 
 
-def _bf16_ulp(x):
-    return 2.0 ** (math.floor(math.log2(abs(x))) - 7)
-
-
-def test_qwen06_config1_one_step(q06):
-    """prompt 64, cache 512, one greedy step -- logits and argmax vs Transformers.
-
-    One step cannot demand the identical token: when the top two logits are within Transformers'
-    own bf16 noise, its choice differs between host CPUs (this step's top two differ by 6e-4 in
-    fp32 and Transformers picks different winners on different machines). The token must be a
-    Transformers near-argmax (within 2 bf16 ulps of its max) and identical to the fp32
-    restatement's; exact agreement is the >= 99%-of-steps statistic of config 2."""
+def test_reference_launcher_through_the_c_abi(q06):
+    """The drop-in C launcher ``launch_decode_kernel`` (the reference's extern "C" entry,
+    /root/reference/pytorch_binding.cu:9-33), called through ctypes exactly as the reference's
+    binding calls it: a device ``LayerWeights[28]`` table the caller filled, the 9 scratch pointers
+    (here NULL: the library keeps its own), ``cache_len = position + 1``, the caller's stream. Its
+    logits and cache row equal the PyTorch operator's bit for bit on the same inputs."""
+    lib = c_library()
     P = 64
-    ids, last, cache, kc, vc = q06.prefill(P)
-    kd, vd = kc.to(DEV), vc.to(DEV)
+    _, last, _, kc, vc = q06.prefill(P)
     tok = int(last.float().argmax())
-    ref_logits, _ = hf.decode_step(q06.model, tok, cache)
-    logits, dev_tok = q06.decode(tok, kd, vd, P, greedy=True)
-    got = logits.cpu()
-    r = ref_logits.float()
-    maxabs, cos = _stats(got, r)
-    ours = int(dev_tok.item())
-    print(f"[config1] max|d| {maxabs:.4e} cos {cos:.8f} token kernel {ours} hf {int(r.argmax())}")
-    assert cos >= 0.9999
-    assert r[ours] >= r.max() - 2 * _bf16_ulp(r.max().item())
-    want, _ = restate.decode_step(q06.W, kc, vc, tok, P, q06.cos_cpu, q06.sin_cpu, numerics="fp32")
-    assert _stats(got, want)[0] < 5e-3
-    assert ours == restate.argmax_bf16(want)
+    table = q06.device_layer_table()
+    ka, va = kc.to(DEV), vc.to(DEV)
+    logits = torch.empty(q06.shape.vocab, dtype=torch.float32, device=DEV)
+    nul = None
+    rc = lib.launch_decode_kernel(tok, q06.embed.data_ptr(), q06.lm_head.data_ptr(), q06.final_norm.data_ptr(),
+                                  table.data_ptr(), q06.cos.data_ptr(), q06.sin.data_ptr(), ka.data_ptr(),
+                                  va.data_ptr(), nul, nul, nul, nul, nul, nul, logits.data_ptr(), nul, nul, nul,
+                                  P, P + 1, q06.max_seq, stream_handle())
+    assert rc == 0, f"launch_decode_kernel returned hipError {rc}"
+    kb, vb = kc.to(DEV), vc.to(DEV)
+    want = q06.decode(tok, kb, vb, P)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, want)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert q06.kernel.status() == 0
+    print(f"[launcher] launch_decode_kernel == decode bit for bit; token {restate.argmax_bf16(logits.cpu())}")
 
 
-def test_qwen06_config2_teacher_forced(q06):
-    """prompt 32, cache 512, 256 teacher-forced steps.
-
-    Tight gate: the kernel reproduces the fp32 restatement (same greedy token on every step but
-    at most one fp32 near-tie, max-abs < 5e-3).
-    Reference gate: against Transformers' bf16 logits the north-star targets are >= 99% identical
-    tokens and cosine >= 0.9999. Both sit at the bf16 noise floor of this random-init model:
-    over 1024 teacher-forced steps Transformers' own fp32 model agrees with its bf16 model on
-    98.5-98.7% of tokens with min cosine 0.99989, and which near-tie Transformers resolves which
-    way depends on the host CPU's GEMM kernels. The test therefore asserts the floor (>= 97.5%
-    tokens, mean cosine >= 0.9999, min >= 0.9998) and prints the measured numbers."""
-    P, steps = 32, 256
-    ids, last, cache, kc, vc = q06.prefill(P)
-    kd, vd = kc.to(DEV), vc.to(DEV)
-    ref = hf.greedy_reference(q06.model, ids, steps)
-    agree, same_as_restate, coss, worst_abs, worst_restate = 0, 0, [], 0.0, 0.0
-    for t in range(steps):
-        tok = ref["tokens"][t]
-        logits, dev_tok = q06.decode(tok, kd, vd, P + t, greedy=True)
-        logits = logits.cpu()
-        r = ref["logits"][t].float()
-        ours = int(dev_tok.item())
-        assert ours == restate.argmax_bf16(logits)
-        agree += ours == int(r.argmax())
-        m, c = _stats(logits, r)
-        worst_abs = max(worst_abs, m)
-        coss.append(c)
-        want, _ = restate.decode_step(q06.W, kc, vc, tok, P + t, q06.cos_cpu, q06.sin_cpu, numerics="fp32")
-        worst_restate = max(worst_restate, _stats(logits, want)[0])
-        same_as_restate += ours == restate.argmax_bf16(want)
-    mean_cos = sum(coss) / len(coss)
-    print(f"[config2] vs Transformers: tokens {agree}/{steps} ({100.0 * agree / steps:.2f}%), "
-          f"cos mean {mean_cos:.8f} min {min(coss):.8f}, max|d| {worst_abs:.4e}; "
-          f"vs fp32 restatement: tokens {same_as_restate}/{steps}, max|d| {worst_restate:.3e}")
-    assert same_as_restate >= steps - 1
-    assert worst_restate < 5e-3
-    assert agree >= math.ceil(0.975 * steps)
-    assert mean_cos >= 0.9999 and min(coss) >= 0.9998
-
-
-def _teacher_forced(sess, P, steps, restate_every, tag, seed=1):
-    """Teacher-forced decode of ``steps`` tokens after a ``P``-token prompt: Transformers (CPU) feeds
-    the tokens (its greedy choice at every step, as ``hf.greedy_reference``); the kernel's logits are
-    compared with Transformers' on every step and, on every ``restate_every``-th step, with the fp32
-    restatement run on the cache the kernel has written so far. Returns the counts the config tests
-    assert on."""
+# ------------------------------------------------------------------------------------------------
+# BASELINE configs against Transformers (the reference path), with a same-run fp32-oracle floor
+# ------------------------------------------------------------------------------------------------
+def _parity_run(sess, P, steps, tight_every, tag, seed=1):
+    """Teacher-forced decode of ``steps`` tokens after a ``P``-token prompt, Transformers' greedy
+    token fed at every step (as /root/reference/model.py:139-173 feeds its own). Per step:
+      * Transformers' bf16 logits (CPU, the reference path);
+      * the kernel's fp32 logits (GPU);
+      * the fp32 restatement teacher-forced the same way on its own cache (CPU): the floor;
+      * every ``tight_every``-th step, the restatement on the cache the kernel has written: the
+        tight check."""
     ids = hf.prompt_ids(P, sess.shape.vocab, seed)
     last, cache = hf.prefill(sess.model, ids)
-    kc, vc = hf.cache_to_kernel_layout(cache, sess.shape.layers, sess.shape.kv_heads, sess.max_seq,
+    ko, vo = hf.cache_to_kernel_layout(cache, sess.shape.layers, sess.shape.kv_heads, sess.max_seq,
                                        sess.shape.head_dim)
-    kd, vd = kc.to(DEV), vc.to(DEV)
-    del kc, vc
-    out = {"agree": 0, "steps": steps, "coss": [], "restate_steps": 0, "restate_same": 0, "restate_abs": 0.0,
-           "sampled_agree": 0, "restate_agree": 0, "sampled_coss": [], "restate_coss": []}
+    kd, vd = ko.to(DEV), vo.to(DEV)
+    rec = {"steps": steps, "k_agree": 0, "o_agree": 0, "k_o_same": 0, "k_cos": [], "o_cos": [], "k_abs": [],
+           "o_abs": [], "k_o_rel": [], "tight_steps": 0, "tight_same": 0, "tight_abs": 0.0}
     tok = int(last.float().argmax())
     for t in range(steps):
         pos = P + t
         r, cache = hf.decode_step(sess.model, tok, cache)
         r = r.float()
-        if t % restate_every == 0:
+        if t % tight_every == 0:
             kc_now, vc_now = kd.cpu(), vd.cpu()  # positions [0, pos) as the kernel wrote them
         logits, dev_tok = sess.decode(tok, kd, vd, pos, greedy=True)
         logits = logits.cpu()
         ours = int(dev_tok.item())
         assert torch.isfinite(logits).all(), f"[{tag}] step {t}: non-finite logits"
         assert ours == restate.argmax_bf16(logits), f"[{tag}] step {t}: device argmax != argmax of logits"
-        out["agree"] += ours == int(r.argmax())
-        out["coss"].append(_stats(logits, r)[1])
-        if t % restate_every == 0:
-            want, _ = restate.decode_step(sess.W, kc_now, vc_now, tok, pos, sess.cos_cpu, sess.sin_cpu,
-                                          numerics="fp32")
+        o = sess.oracle_step(ko, vo, tok, pos)
+        ref_tok = int(r.argmax())
+        rec["k_agree"] += ours == ref_tok
+        rec["o_agree"] += restate.argmax_bf16(o) == ref_tok
+        rec["k_o_same"] += ours == restate.argmax_bf16(o)
+        m, c = stats(logits, r)
+        rec["k_abs"].append(m)
+        rec["k_cos"].append(c)
+        m, c = stats(o, r)
+        rec["o_abs"].append(m)
+        rec["o_cos"].append(c)
+        rec["k_o_rel"].append(((logits.double() - o.double()).norm() / o.double().norm()).item())
+        if t % tight_every == 0:
+            want = sess.oracle_step(kc_now, vc_now, tok, pos)
             del kc_now, vc_now
-            out["restate_steps"] += 1
-            out["restate_same"] += ours == restate.argmax_bf16(want)
-            out["restate_abs"] = max(out["restate_abs"], _stats(logits, want)[0])
-            # the same comparison with Transformers for the restatement: its distance to Transformers'
-            # bf16 logits is the bf16 noise floor the kernel's distance is judged against
-            out["sampled_agree"] += ours == int(r.argmax())
-            out["restate_agree"] += restate.argmax_bf16(want) == int(r.argmax())
-            out["sampled_coss"].append(out["coss"][-1])
-            out["restate_coss"].append(_stats(want, r)[1])
-        tok = int(r.argmax())
-    c = out["coss"]
-    print(f"[{tag}] P={P} steps={steps}: vs Transformers tokens {out['agree']}/{steps}, cos mean "
-          f"{sum(c) / len(c):.8f} min {min(c):.8f}; vs fp32 restatement ({out['restate_steps']} steps) "
-          f"tokens {out['restate_same']}/{out['restate_steps']}, max|d| {out['restate_abs']:.3e}; on those steps "
-          f"Transformers agreement kernel {out['sampled_agree']} restatement {out['restate_agree']}, cos mean "
-          f"kernel {sum(out['sampled_coss']) / len(out['sampled_coss']):.8f} restatement "
-          f"{sum(out['restate_coss']) / len(out['restate_coss']):.8f}", flush=True)
+            rec["tight_steps"] += 1
+            rec["tight_same"] += ours == restate.argmax_bf16(want)
+            rec["tight_abs"] = max(rec["tight_abs"], stats(logits, want)[0])
+        if t % 64 == 63:
+            print(f"[{tag}] step {t + 1}/{steps}: tokens kernel {rec['k_agree']} oracle {rec['o_agree']}", flush=True)
+        tok = ref_tok
+    n = steps
+    print(f"[{tag}] P={P} steps={n} vs Transformers: tokens kernel {rec['k_agree']}/{n} oracle {rec['o_agree']}/{n}; "
+          f"cos min kernel {min(rec['k_cos']):.8f} oracle {min(rec['o_cos']):.8f}, mean kernel "
+          f"{sum(rec['k_cos']) / n:.8f} oracle {sum(rec['o_cos']) / n:.8f}; max-abs kernel {max(rec['k_abs']):.4e} "
+          f"oracle {max(rec['o_abs']):.4e}; kernel vs oracle tokens {rec['k_o_same']}/{n}, relative distance max "
+          f"{max(rec['k_o_rel']):.2e}; tight "
+          f"({rec['tight_steps']} steps on the kernel's cache): tokens {rec['tight_same']}/{rec['tight_steps']}, "
+          f"max-abs {rec['tight_abs']:.3e}", flush=True)
+    return rec
+
+
+def _merge(recs):
+    out = {"steps": 0, "k_agree": 0, "o_agree": 0, "k_o_same": 0, "k_cos": [], "o_cos": [], "k_abs": [], "o_abs": [],
+           "k_o_rel": [], "tight_steps": 0, "tight_same": 0, "tight_abs": 0.0}
+    for r in recs:
+        for k in ("steps", "k_agree", "o_agree", "k_o_same", "tight_steps", "tight_same"):
+            out[k] += r[k]
+        for k in ("k_cos", "o_cos", "k_abs", "o_abs", "k_o_rel"):
+            out[k] += r[k]
+        out["tight_abs"] = max(out["tight_abs"], r["tight_abs"])
     return out
 
 
-def _assert_config(res, floor):
-    assert res["restate_abs"] < 5e-3
-    assert res["restate_same"] >= res["restate_steps"] - 1
-    c = res["coss"]
-    assert sum(c) / len(c) >= 0.9999 and min(c) >= 0.9998
-    assert res["agree"] >= math.floor(floor * res["steps"])
+def _assert_parity(rec):
+    """The gates every BASELINE config passes.
+
+    Cosine floor: the mean over steps of the kernel's cosine to Transformers is within 1e-6 of the
+    oracle's. Per step, the kernel and the oracle run on their own caches, so their logits differ by
+    a small relative distance r = |k - o| / |o| (fp32 summation order, compounded over the steps);
+    to first order that can move the cosine to Transformers' logits h by at most
+    r * sqrt(1 - cos(o, h)^2) (the component of the unit gradient of cos(., h) orthogonal to o), so
+    each step's kernel cosine must be within that bound (plus r^2) of the oracle's."""
+    n = rec["steps"]
+    # tight: the kernel computes what the fp32 restatement computes (on the kernel's own cache);
+    # at most one greedy token may differ, at an fp32 near-tie
+    assert rec["tight_abs"] < 5e-3
+    assert rec["tight_same"] >= rec["tight_steps"] - 1
+    # floor: no further from Transformers than the fp32 restatement run the same way
+    assert rec["k_agree"] >= rec["o_agree"], (rec["k_agree"], rec["o_agree"])
+    assert sum(rec["k_cos"]) / n >= sum(rec["o_cos"]) / n - 1e-6
+    for t, (kc_, oc_, r) in enumerate(zip(rec["k_cos"], rec["o_cos"], rec["k_o_rel"])):
+        slack = r * math.sqrt(max(0.0, 1.0 - oc_ * oc_)) + r * r
+        assert kc_ >= oc_ - slack, f"step {t}: cosine to Transformers {kc_} below the oracle's {oc_} - {slack:.2e}"
+    assert max(rec["k_abs"]) <= max(rec["o_abs"]) + 1e-3
+    # the north-star bar, wherever the same-run oracle meets it
+    if rec["o_agree"] >= math.ceil(NS_TOKENS * n):
+        assert rec["k_agree"] >= math.ceil(NS_TOKENS * n)
+    if max(rec["o_abs"]) <= NS_MAXABS:
+        assert max(rec["k_abs"]) <= NS_MAXABS
+    for t, (kc_, oc_) in enumerate(zip(rec["k_cos"], rec["o_cos"])):
+        if oc_ >= NS_COS:
+            assert kc_ >= NS_COS, f"step {t}: cosine {kc_} below {NS_COS} where the oracle meets it"
+
+
+def test_qwen06_config1_one_step(q06):
+    """prompt 64, cache 512, one greedy step -- logits and argmax against
+    Transformers, with the same-run fp32-oracle floor."""
+    _assert_parity(_parity_run(q06, 64, 1, 1, "config1"))
+
+
+def test_qwen06_config2_teacher_forced(q06):
+    """prompt 32, cache 512, 256 teacher-forced steps (ctx 33-288; past 256 the
+    launches hold two K/V rows per group in registers). Tight check on every 4th step."""
+    _assert_parity(_parity_run(q06, 32, 256, 4, "config2"))
 
 
 def test_qwen06_config3_prompt_sweep(q06):
     """Config 3: prompts of 16, 128, 256 and 480 tokens, cache 512, 32 teacher-forced steps each --
     the attention split count S = min(ceil(ctx / 32), 8) runs from 1 to 8 and the last step writes the
-    cache's final slot (position 511). Tight gate against the fp32 restatement on every 8th step;
-    token agreement with Transformers pooled over the 128 steps (the bf16 noise floor, as in
-    config 2)."""
-    pooled = {"agree": 0, "steps": 0, "coss": [], "restate_steps": 0, "restate_same": 0, "restate_abs": 0.0}
-    for P in (16, 128, 256, 480):
-        r = _teacher_forced(q06, P, 32, 8, "config3")
-        for k in ("agree", "steps", "restate_steps", "restate_same"):
-            pooled[k] += r[k]
-        pooled["coss"] += r["coss"]
-        pooled["restate_abs"] = max(pooled["restate_abs"], r["restate_abs"])
-    _assert_config(pooled, 0.96)
+    cache's final slot (position 511). Gates pooled over the 128 steps."""
+    _assert_parity(_merge([_parity_run(q06, P, 32, 8, "config3") for P in (16, 128, 256, 480)]))
 
 
 @pytest.fixture(scope="module")
@@ -493,29 +615,14 @@ def q06_4k():
 def test_qwen06_config4_long_context(q06_4k):
     """Config 4: prompt 3584, cache 4096, 256 teacher-forced steps (ctx 3585-3840): 16 attention
     splits of ~230 keys merged in two poll rounds, most keys streamed inside the attention phase
-    rather than held in registers. fp32 restatement on every 32nd step."""
-    _assert_config(_teacher_forced(q06_4k, 3584, 256, 32, "config4"), 0.96)
+    rather than held in registers. Tight check on every 32nd step."""
+    _assert_parity(_parity_run(q06_4k, 3584, 256, 32, "config4"))
 
 
 def test_qwen17_config5():
     """Config 5: the Qwen3-1.7B shape (H 2048, I 6144, 28 layers, full vocabulary), prompt 512,
-    cache 2048, 256 teacher-forced steps; fp32 restatement on every 8th step.
-
-    At this width the bf16 noise of Transformers' own CPU decode is larger than at 0.6B: the fp32
-    restatement (the reference kernel's arithmetic) itself agrees with Transformers' bf16 greedy
-    token on only ~92% of steps, with mean cosine ~0.9995. The kernel is therefore held to the
-    restatement tightly (max-abs < 5e-3, same token) and to Transformers relative to that floor:
-    on the sampled steps its cosine to Transformers is within 1e-5 of the restatement's and its
-    token agreement within one step of the restatement's."""
-    sess = Session("qwen3-1.7b", 2048)
-    res = _teacher_forced(sess, 512, 256, 8, "config5")
-    assert res["restate_abs"] < 5e-3
-    assert res["restate_same"] >= res["restate_steps"] - 1
-    for ck, cr in zip(res["sampled_coss"], res["restate_coss"]):
-        assert ck >= cr - 1e-5, (ck, cr)
-    assert res["sampled_agree"] >= res["restate_agree"] - 1
-    c = res["coss"]
-    assert sum(c) / len(c) >= 0.999 and res["agree"] >= math.floor(0.88 * res["steps"])
+    cache 2048, 256 teacher-forced steps; tight check on every 8th step."""
+    _assert_parity(_parity_run(Session("qwen3-1.7b", 2048), 512, 256, 8, "config5"))
 
 
 def test_launch_modes_agree(mini):
@@ -535,3 +642,22 @@ def test_launch_modes_agree(mini):
     assert mini.kernel.status() == 0
     assert torch.equal(outs[0][0], outs[1][0]) and outs[0][1] == outs[1][1]
     assert torch.equal(outs[0][2], outs[1][2])
+
+
+def test_two_streams_have_separate_workspaces(mini):
+    """Decodes issued on two streams (one after the other) use separate exchange workspaces and give
+    the same result as on the default stream."""
+    P = 70
+    _, last, _, kc, vc = mini.prefill(P)
+    tok = int(last.float().argmax())
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    want = mini.decode(tok, kd, vd, P)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            kb, vb = kc.to(DEV), vc.to(DEV)
+            got = mini.decode(tok, kb, vb, P)
+        s.synchronize()
+        assert torch.equal(got, want)
+    assert mini.kernel.status() == 0

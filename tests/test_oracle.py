@@ -247,3 +247,40 @@ def test_paged_layout_helpers():
         assert torch.equal(pages[l, table[p // ps], h, p % ps], cache[l, h, p])
     assert torch.isnan(pages[:, 2]).all() and torch.isnan(pages[:, 4]).all() and torch.isnan(pages[:, 6]).all()
     assert torch.equal(from_pages(pages, table), cache)
+
+
+@pytest.mark.slow
+def test_bf16_emulation_is_no_closer_to_transformers_than_fp32():
+    """Why the GPU parity gate against Transformers is a same-run fp32 floor and not exact bf16
+    agreement: at the full 0.6B shape, the restatement that reproduces every bf16 rounding point of
+    Transformers' decode (``numerics="hf"``, bit-exact on the tiny golden model) agrees with
+    Transformers' own greedy tokens no better, and its logits sit further from Transformers' than
+    the fp32 restatement's. One-ulp GEMV differences from a different summation order compound
+    through 28 layers, so exact emulation buys nothing; both modes are teacher-forced with
+    Transformers' tokens from the same prefill, 64 steps."""
+    name, P, steps, max_seq = "qwen3-0.6b", 32, 64, 512
+    shape = SHAPES[name]
+    model = hf.build_model(name, max_positions=max_seq)
+    ids = hf.prompt_ids(P, shape.vocab)
+    ref = hf.greedy_reference(model, ids, steps)
+    _, cache = hf.prefill(model, ids)
+    kh, vh = hf.cache_to_kernel_layout(cache, shape.layers, shape.kv_heads, max_seq, shape.head_dim)
+    k3, v3 = kh.clone(), vh.clone()
+    cos, sin = hf.rope_tables(model, max_seq)
+    W = restate.Weights.from_model(model, shape)
+    agree_hf = agree_fp32 = 0
+    rms_hf, rms_fp32 = [], []
+    for t in range(steps):
+        tok, r = ref["tokens"][t], ref["logits"][t].float()
+        a, _ = restate.decode_step(W, kh, vh, tok, P + t, cos, sin, numerics="hf", lanes=_lanes())
+        b, _ = restate.decode_step(W, k3, v3, tok, P + t, cos, sin, numerics="fp32")
+        a = restate.bf16(a)
+        agree_hf += restate.argmax_bf16(a) == int(r.argmax())
+        agree_fp32 += restate.argmax_bf16(b) == int(r.argmax())
+        rms_hf.append(((a - r) ** 2).mean().sqrt().item())
+        rms_fp32.append(((b - r) ** 2).mean().sqrt().item())
+    mean_hf, mean_fp32 = sum(rms_hf) / steps, sum(rms_fp32) / steps
+    print(f"tokens agreeing with Transformers: bf16 emulation {agree_hf}/{steps}, fp32 {agree_fp32}/{steps}; "
+          f"mean rms logit distance: bf16 emulation {mean_hf:.5f}, fp32 {mean_fp32:.5f}")
+    assert agree_hf <= agree_fp32
+    assert mean_hf > mean_fp32
