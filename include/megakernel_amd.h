@@ -101,6 +101,25 @@ hipError_t mk_decode(const mk_model_dims* dims, int token_id, const void* embed_
                      int32_t* out_token, hipStream_t stream);
 
 /*
+ * mk_decode with no allocation on any call. No counterpart in the reference: it is for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation). Same arguments, results and errors as mk_decode, and the same kernels; the
+ * exchange workspace is a file-scope device array of mk_workspace_bytes() bytes (1.2 MB) that each
+ * device running the library holds until the process ends, instead of a per-stream allocation.
+ * Limits, rejected with hipErrorInvalidValue before anything is launched: (hidden, intermediate)
+ * one of the two supported shapes, 1..62 layers, vocab >= 256, position < max_seq_len.
+ * The first call on a device initialises the array (a placement probe and a fill kernel on
+ * `stream`, then a synchronization of `stream`), so make it outside graph capture. Every call on
+ * one device shares that one array and keeps its state (launch sequence, status word) for the
+ * next call: calls on one device must not overlap in time, on any stream, or they race.
+ */
+hipError_t mk_decode_noalloc(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                             const void* lm_head_weight, const void* final_norm_weight,
+                             const void* layer_weights, const void* cos_table, const void* sin_table,
+                             void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
+                             int32_t* out_token, hipStream_t stream);
+
+/*
  * Several decode steps in one call, with no host synchronization between them: the device-side
  * multi-token loop. Step i (0 <= i < n) runs at position + i and reads its input token from device
  * memory, tokens[i] (int32, device array of n + 1 entries, tokens[0] set by the caller).
@@ -171,6 +190,10 @@ hipError_t mk_reset(void);
  * has queued (a long mk_decode_steps), and lets tests exercise the failure path with every kernel
  * still exiting normally. Synchronizes with the device. No reference counterpart. */
 hipError_t mk_request_drain(void);
+
+/* Bytes of one exchange workspace set (the static array of mk_decode_noalloc has this size; each
+ * stream's allocated workspace too). */
+size_t mk_workspace_bytes(void);
 
 /* Phase tracing (profiling builds and tools; no reference counterpart -- the reference has no
  * in-kernel timers). With a non-NULL device buffer of at least mk_trace_bytes() bytes, every later

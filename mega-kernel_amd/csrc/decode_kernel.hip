@@ -1552,6 +1552,17 @@ struct DeviceState {
 };
 static DeviceState g_dev[MAX_DEVICES];
 
+// The no-allocation entry point's workspace set: a file-scope device array (each device that runs
+// the library holds its own copy until the process ends). Host code never uses the name `scratch`
+// as an address: its per-device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) u64 scratch[WS_SET_WORDS];
+struct StaticState {
+  bool init = false;
+  hipError_t err = hipSuccess;
+  bool force_wt = false;
+  void* ptr = nullptr;  // this device's address of `scratch`
+};
+static StaticState g_static[MAX_DEVICES];
 static std::mutex g_mu;
 
 template <int H, int I>
@@ -1639,6 +1650,29 @@ static hipError_t stream_workspace(DeviceState* st, hipStream_t stream, void** o
   return hipSuccess;
 }
 
+// The static workspace set of the current device: its address via hipGetSymbolAddress and its
+// initialisation, once per device. Calls no allocating routine.
+static hipError_t static_workspace(hipStream_t stream, void** out, bool* force_wt) {
+  int dev = 0;
+  hipError_t e = current_device(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(g_mu);
+  StaticState& s = g_static[dev];
+  if (!s.init) {
+    s.init = true;
+    s.err = check_device(dev);
+    if (s.err == hipSuccess) s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch));
+    if (s.err == hipSuccess && s.ptr == nullptr) s.err = hipErrorInvalidSymbol;
+    bool placement_ok = false;
+    if (s.err == hipSuccess) s.err = init_workspace(s.ptr, stream, &placement_ok);
+    s.force_wt = !placement_ok;
+  }
+  if (s.err != hipSuccess) return s.err;
+  *out = s.ptr;
+  *force_wt = s.force_wt;
+  return hipSuccess;
+}
+
 // The grid's workgroups wait on each other, so all 256 must be resident at once: one per CU, which
 // check_kernel_fits() verified, and kernels on one stream never overlap. A plain launch is the
 // default: it costs ~16 us less per token than a cooperative one (measured on the MI355X: 423 vs
@@ -1713,15 +1747,18 @@ static hipError_t launch_step(const KArgs& k, bool s06, hipStream_t stream) {
   return launch_on(k, s06, ws, st->force_wt, st, stream);
 }
 
-// Every workspace set of the current device.
+// Every workspace set of the current device (allocated ones, and the static one once initialised).
 template <typename F>
 static hipError_t for_each_workspace(F f) {
   DeviceState* st = nullptr;
   hipError_t e = device_state(&st);
   if (e != hipSuccess) return e;
+  int dev = 0;
+  if ((e = current_device(&dev)) != hipSuccess) return e;
   std::lock_guard<std::mutex> lk(g_mu);
   for (int i = 0; i < st->nws; ++i)
     if ((e = f(st->ws[i].ws)) != hipSuccess) return e;
+  if (g_static[dev].init && g_static[dev].err == hipSuccess && (e = f(g_static[dev].ptr)) != hipSuccess) return e;
   return hipSuccess;
 }
 
@@ -1743,6 +1780,27 @@ extern "C" hipError_t mk_decode(const mk_model_dims* dims, int token_id, const v
   k.token = token_id;
   k.out_token = out_token;
   return launch_step(k, s06, stream);
+}
+
+extern "C" hipError_t mk_decode_noalloc(const mk_model_dims* dims, int token_id, const void* embed_weight,
+                                        const void* lm_head_weight, const void* final_norm_weight,
+                                        const void* layer_weights, const void* cos_table, const void* sin_table,
+                                        void* k_cache, void* v_cache, int position, int max_seq_len, float* logits,
+                                        int32_t* out_token, hipStream_t stream) {
+  KArgs k;
+  bool s06 = false;
+  hipError_t e = prepare(dims, embed_weight, lm_head_weight, final_norm_weight, layer_weights, cos_table, sin_table,
+                         k_cache, v_cache, position, max_seq_len, logits, k, s06);
+  if (e != hipSuccess) return e;
+  if (token_id < 0 || token_id >= dims->vocab) return hipErrorInvalidValue;
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  void* ws = nullptr;
+  bool force_wt = false;
+  if ((e = static_workspace(stream, &ws, &force_wt)) != hipSuccess) return e;
+  k.token = token_id;
+  k.out_token = out_token;
+  return launch_on(k, s06, ws, force_wt, st, stream);
 }
 
 // Page-table checks and fields of a paged launch (page size a power of two up to 4096, at most
@@ -1895,6 +1953,8 @@ extern "C" hipError_t mk_set_launch_mode(int cooperative) {
 }
 
 extern "C" size_t mk_trace_bytes(void) { return (size_t)NWG * TRACE_N * sizeof(uint64_t); }
+
+extern "C" size_t mk_workspace_bytes(void) { return WS_SET_BYTES; }
 
 extern "C" int mk_grid_size(void) {
   DeviceState* st = nullptr;

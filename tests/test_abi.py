@@ -191,3 +191,29 @@ def test_unsupported_shape_is_rejected(ext):
             a[4][i] = torch.zeros(4096, 1024, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="supported"):
         ext.check_args(*a)
+
+
+def test_noalloc_entry_point_rejects_out_of_limit_arguments_before_launch(lib):
+    """``mk_decode_noalloc`` checks its limits (supported shape, layers, vocabulary, position) before
+    any HIP call, like ``mk_decode``; ``mk_workspace_bytes`` reports the static array's size."""
+    f = lib.mk_decode_noalloc
+    f.restype = ctypes.c_int
+    vp = ctypes.c_void_p
+    f.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    dummy = vp(16)
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                    ("num_layers", ctypes.c_int32), ("vocab", ctypes.c_int32)]
+
+    def call(dims, token=1, position=3, max_seq=512):
+        return f(ctypes.byref(dims), token, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, position,
+                 max_seq, dummy, None, None)
+
+    assert call(Dims(4096, 12288, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 63, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 28, 255)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 28, 151936), position=512) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 28, 151936), token=151936) == HIP_ERROR_INVALID_VALUE
+    lib.mk_workspace_bytes.restype = ctypes.c_size_t
+    assert 1 << 20 <= lib.mk_workspace_bytes() <= 2 << 20
