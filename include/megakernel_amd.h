@@ -120,6 +120,34 @@ hipError_t mk_decode_noalloc(const mk_model_dims* dims, int token_id, const void
                              int32_t* out_token, hipStream_t stream);
 
 /*
+ * Batched prefill: tokens[0..num_tokens-1] (int32 device array) at positions position ..
+ * position + num_tokens - 1 go through the whole model in one pass -- every layer's products on
+ * the matrix cores over all the tokens at once, causal attention over the cache -- writing each
+ * token's K/V rows into k_cache/v_cache ([num_layers, 8, max_seq_len, 128] bf16, the decode
+ * layout), and the last token's fp32 logits [vocab] to `logits` and, when out_token is not NULL,
+ * its greedy token (argmax of the bf16-rounded logits, lowest index on ties). Rows before
+ * `position` must already hold the earlier tokens (position 0 for a fresh prompt; larger for a
+ * prompt fed in chunks). Numerics are mk_decode's (fp32 activations and accumulation, K/V
+ * rounded to bf16), so a decode after the prefill continues exactly as after decode steps.
+ *   layer_weights     HOST array of mk_layer_weights[num_layers] (device pointers inside)
+ *   workspace         device memory of at least mk_prefill_workspace_bytes(dims, num_tokens)
+ *                     bytes, 256-byte aligned, owned by the caller, not used after the call's work
+ *                     completes on `stream`
+ * A token outside [0, vocab) is embedded as token 0 and the call reports itself as failed in-band
+ * (NaN logits, token -1). Asynchronous on `stream`. Argument errors (null pointers, unsupported
+ * shape, position + num_tokens > max_seq_len, workspace too small or not 256-byte aligned) return
+ * hipErrorInvalidValue before any launch.
+ * Replaces the reference's Transformers prefill and the copy of its cache into the kernel layout
+ * (/root/reference/model.py:72-87), which the reference runs before its decode loop.
+ */
+size_t mk_prefill_workspace_bytes(const mk_model_dims* dims, int num_tokens);
+hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                      const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                      const void* layer_weights, const void* cos_table, const void* sin_table,
+                      void* k_cache, void* v_cache, int max_seq_len, float* logits, int32_t* out_token,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Several decode steps in one call, with no host synchronization between them: the device-side
  * multi-token loop. Step i (0 <= i < n) runs at position + i and reads its input token from device
  * memory, tokens[i] (int32, device array of n + 1 entries, tokens[0] set by the caller).

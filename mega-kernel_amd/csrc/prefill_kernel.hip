@@ -1,0 +1,779 @@
+// Batched prefill of a Qwen3-shaped model on MI355X (gfx950): all prompt tokens at once, layer by
+// layer, writing the decode kernel's K/V cache layout [L][8][max_seq][128] directly.
+//
+// The reference prefills with Transformers on the GPU and copies its cache into the kernel's
+// layout (/root/reference/model.py:72-87); the decode kernel of this library could also prefill by
+// one decode launch per prompt token. Here the prompt's tokens are the M rows of skinny-to-square
+// GEMMs on the matrix cores (v_mfma_f32_16x16x32_bf16), with the elementwise work fused into the
+// GEMM epilogues:
+//   x = embed[tokens]                                  (fp32 residual rows, workspace)
+//   per layer:  a = RMSNorm(x)                         (norm_kernel, as bf16 hi/lo pair)
+//               q, k, v = a . [Wq; Wk; Wv]^T           (gemm, EPI_QKV: per-head RMSNorm + RoPE on q and k,
+//                                                       k and v rounded to bf16 into the cache, q kept)
+//               o = causal attention(q, cache)         (attn_kernel: flash-style, online softmax)
+//               x += o . Wo^T                          (gemm, EPI_RESID)
+//               a = RMSNorm(x)
+//               m = silu(a . Wg^T) * (a . Wu^T)        (gemm, EPI_SILU: gate and up rows in one tile)
+//               x += m . Wd^T                          (gemm, EPI_RESID)
+//   logits of the last row = RMSNorm(x) . E^T, greedy token (lm_head_kernel, fused argmax)
+//
+// Numerics are the decode kernel's (the reference kernel's fp32 design, /root/reference/
+// megakernel.cu): fp32 residual and accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to
+// bf16. The matrix cores take bf16 operands, so every fp32 activation operand is split into
+// hi = bf16(x) and lo = bf16(x - hi) and multiplied twice (weights and cache rows are bf16
+// already): a product then matches fp32 to ~2^-17 relative.
+//
+// MFMA operand layout (16x16x32 bf16; lane l, i = l % 16, g = l / 16): A[i][8g + j] and
+// B[8g + j][i] for j = 0..7 (8 bf16 = 16 bytes per lane), accumulator C[4g + j][i] for j = 0..3.
+// Both A (activation rows) and B (weight rows, C = A . W^T) are read as 16-byte chunks of rows.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mk_device.h"
+#include "../../include/megakernel_amd.h"
+
+namespace mkp {
+using namespace mk;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned long long u64;
+
+constexpr int D = 128, HQ = 16, HKV = 8;
+constexpr float EPS = 1e-6f;
+constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
+
+__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// hi = bf16(v), lo = bf16(v - hi) of 8 values, as two 16-byte chunks
+__device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+    l[q] = pack_bf16x2(v[2 * q] - bf16_lo(h[q]), v[2 * q + 1] - bf16_hi(h[q]));
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+__device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
+  v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x); v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
+  v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
+}
+
+// ------------------------------------------------------------------------------------------------
+// RMSNorm of rows of x (fp32 [M][H]) into a bf16 hi/lo pair [M][lda]: y = x * w * rsqrt(mean(x^2) +
+// eps) (/root/reference/megakernel.cu:704-739). With `tokens`, x is first filled with the
+// embedding rows (fp32 copies of bf16 embed[tokens[m]]); a token outside [0, vocab) reads row 0
+// instead and sets *bad, which makes the call's logits NaN and its token -1. One wave per row.
+// ------------------------------------------------------------------------------------------------
+template <int H>
+__global__ void __launch_bounds__(256) norm_kernel(float* x, const int32_t* tokens, const uint16_t* embed, int vocab,
+                                                   int32_t* bad, const uint16_t* w, uint16_t* ah, uint16_t* al, int lda,
+                                                   int M) {
+  constexpr int E = H / 64;  // contiguous elements per lane
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  float v[E];
+  float* xr = x + (size_t)m * H + E * lane;
+  if (tokens) {
+    int tok = tokens[m];
+    if (tok < 0 || tok >= vocab) {
+      if (lane == 0) *bad = 1;
+      tok = 0;
+    }
+    const uint16_t* er = embed + (size_t)tok * H + E * lane;
+#pragma unroll
+    for (int k = 0; k < E; k += 8) {
+      float t[8];
+      unpack8(*reinterpret_cast<const uint4*>(er + k), t);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[k + q] = t[q];
+    }
+#pragma unroll
+    for (int k = 0; k < E; k += 4) *reinterpret_cast<float4*>(xr + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; k += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(xr + k);
+      v[k] = t.x; v[k + 1] = t.y; v[k + 2] = t.z; v[k + 3] = t.w;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < E; ++k) ss = fmaf(v[k], v[k], ss);
+  const float rs = rsqrtf(wave_sum(ss) / (float)H + EPS);
+  const uint16_t* wr = w + E * lane;
+#pragma unroll
+  for (int k = 0; k < E; k += 8) {
+    float wv[8], y[8];
+    unpack8(*reinterpret_cast<const uint4*>(wr + k), wv);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
+    uint4 hi, lo;
+    split8(y, hi, lo);
+    *reinterpret_cast<uint4*>(ah + (size_t)m * lda + E * lane + k) = hi;
+    *reinterpret_cast<uint4*>(al + (size_t)m * lda + E * lane + k) = lo;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// GEMM C[M][N] = A[M][K] . W[N][K]^T on the matrix cores, A given as a bf16 hi/lo pair, W bf16
+// row-major (nn.Linear layout, read in place). Tile 128 x 128 per workgroup of 4 waves (2 x 2, 64 x
+// 64 each), K in steps of 64 staged through LDS, the next step's global loads in flight during the
+// current step's MFMAs. The epilogue takes the tile's fp32 sums.
+// ------------------------------------------------------------------------------------------------
+constexpr int MT = 128, NT = 128, KT = 64, KP = KT + 8;  // KP: padded LDS row (144 B)
+constexpr int CP = NT + 4;                              // padded fp32 row of the epilogue tile
+
+enum Epi { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2 };
+
+struct GemmArgs {
+  const uint16_t* ah;
+  const uint16_t* al;
+  int lda;
+  int M, N, K;
+  // weights: EPI_RESID: w0 [N][K]; EPI_QKV: w0 = Wq, w1 = Wk, w2 = Wv; EPI_SILU: w0 = Wg, w1 = Wu
+  const uint16_t* w0;
+  const uint16_t* w1;
+  const uint16_t* w2;
+  // EPI_RESID: x[M][ldx] += C
+  float* x;
+  int ldx;
+  // EPI_SILU: m = silu(gate) * up into bh/bl [M][ldb]
+  uint16_t* bh;
+  uint16_t* bl;
+  int ldb;
+  // EPI_QKV
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const uint16_t* cos_tab;
+  const uint16_t* sin_tab;
+  uint16_t* qh;  // [M][16 * 128] normed, rotated queries, bf16 hi/lo
+  uint16_t* ql;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int layer, position, max_seq;
+};
+
+// first element of weight row r (0..127) of N-tile t
+template <int EPI>
+__device__ __forceinline__ const uint16_t* weight_row(const GemmArgs& g, int t, int r) {
+  if constexpr (EPI == EPI_QKV) {
+    if (t < HQ) return g.w0 + (size_t)(t * D + r) * g.K;
+    if (t < HQ + HKV) return g.w1 + (size_t)((t - HQ) * D + r) * g.K;
+    return g.w2 + (size_t)((t - HQ - HKV) * D + r) * g.K;
+  } else if constexpr (EPI == EPI_SILU) {  // gate rows then up rows of intermediates [64 t, 64 t + 64)
+    return r < NT / 2 ? g.w0 + (size_t)(t * (NT / 2) + r) * g.K : g.w1 + (size_t)(t * (NT / 2) + r - NT / 2) * g.K;
+  } else {
+    return g.w0 + (size_t)(t * NT + r) * g.K;
+  }
+}
+
+struct GemmSmem {
+  union {
+    struct {
+      uint16_t a[2][MT][KP];  // hi, lo
+      uint16_t w[NT][KP];
+    } t;
+    float c[MT][CP];
+  };
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) GemmSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tn = blockIdx.x, m0 = blockIdx.y * MT;
+  const int li = lane & 15, lg = lane >> 4;
+
+  // global -> register staging: 4 chunks of 16 bytes per thread per matrix (row c / 8, chunk c % 8)
+  uint4 ra[2][4], rw[4];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int m = m0 + row;
+      if (m < g.M) {
+        ra[0][i] = *reinterpret_cast<const uint4*>(g.ah + (size_t)m * g.lda + k0 + 8 * ch);
+        ra[1][i] = *reinterpret_cast<const uint4*>(g.al + (size_t)m * g.lda + k0 + 8 * ch);
+      } else {
+        ra[0][i] = make_uint4(0, 0, 0, 0);
+        ra[1][i] = make_uint4(0, 0, 0, 0);
+      }
+      rw[i] = ld_stream(reinterpret_cast<const uint4*>(weight_row<EPI>(g, tn, row) + k0 + 8 * ch));
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<uint4*>(&sm.t.a[0][row][8 * ch]) = ra[0][i];
+      *reinterpret_cast<uint4*>(&sm.t.a[1][row][8 * ch]) = ra[1][i];
+      *reinterpret_cast<uint4*>(&sm.t.w[row][8 * ch]) = rw[i];
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  load(0);
+  for (int k0 = 0; k0 < g.K; k0 += KT) {
+    __syncthreads();  // every wave is done with the previous step's tile
+    store();
+    __syncthreads();
+    if (k0 + KT < g.K) load(k0 + KT);
+#pragma unroll
+    for (int s = 0; s < KT / 32; ++s) {
+      uint4 fa[2][4], fw[4];
+#pragma unroll
+      for (int bm = 0; bm < 4; ++bm) {
+        const int r = wm * 64 + bm * 16 + li;
+        fa[0][bm] = *reinterpret_cast<const uint4*>(&sm.t.a[0][r][32 * s + 8 * lg]);
+        fa[1][bm] = *reinterpret_cast<const uint4*>(&sm.t.a[1][r][32 * s + 8 * lg]);
+      }
+#pragma unroll
+      for (int bn = 0; bn < 4; ++bn)
+        fw[bn] = *reinterpret_cast<const uint4*>(&sm.t.w[wn * 64 + bn * 16 + li][32 * s + 8 * lg]);
+#pragma unroll
+      for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < 4; ++bn) {
+          acc[bm][bn] = mfma(fa[0][bm], fw[bn], acc[bm][bn]);
+          acc[bm][bn] = mfma(fa[1][bm], fw[bn], acc[bm][bn]);
+        }
+    }
+  }
+
+  if constexpr (EPI == EPI_RESID) {
+    // x += C, each element owned by one lane
+#pragma unroll
+    for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 64 + bm * 16 + 4 * lg + j;
+        if (m < g.M) {
+#pragma unroll
+          for (int bn = 0; bn < 4; ++bn) {
+            float* p = g.x + (size_t)m * g.ldx + tn * NT + wn * 64 + bn * 16 + li;
+            *p += acc[bm][bn][j];
+          }
+        }
+      }
+    return;
+  }
+
+  // QKV and SILU need whole rows of the tile: through LDS
+  __syncthreads();
+#pragma unroll
+  for (int bm = 0; bm < 4; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 4; ++bn)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sm.c[wm * 64 + bm * 16 + 4 * lg + j][wn * 64 + bn * 16 + li] = acc[bm][bn][j];
+  __syncthreads();
+  const int r = tid >> 1, half = tid & 1;  // two threads per row
+  const int m = m0 + r;
+  if (m >= g.M) return;
+
+  if constexpr (EPI == EPI_SILU) {
+    // columns 0..63 gate, 64..127 up of intermediates [64 tn, 64 tn + 64); this thread: 32 of them
+    const int c0 = 32 * half;
+#pragma unroll
+    for (int c = 0; c < 32; c += 8) {
+      float mv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float gt = sm.c[r][c0 + c + q], up = sm.c[r][NT / 2 + c0 + c + q];
+        mv[q] = gt / (1.f + expf(-gt)) * up;  // silu(gate) * up (/root/reference/megakernel.cu:659-665)
+      }
+      uint4 hi, lo;
+      split8(mv, hi, lo);
+      const size_t o = (size_t)m * g.ldb + tn * (NT / 2) + c0 + c;
+      *reinterpret_cast<uint4*>(g.bh + o) = hi;
+      *reinterpret_cast<uint4*>(g.bl + o) = lo;
+    }
+    return;
+  }
+
+  if constexpr (EPI == EPI_QKV) {
+    // tile tn is one head: q head tn (< 16), k head tn - 16 (< 24) or v head tn - 24
+    const int pos = g.position + m;
+    const int d0 = 64 * half;  // this thread's dims [d0, d0 + 64); the RoPE partner of d is d ^ 64
+    if (tn >= HQ + HKV) {      // v: rounded to bf16 into the cache as is
+      uint16_t* dst = g.v_cache + (((size_t)g.layer * HKV + (tn - HQ - HKV)) * g.max_seq + pos) * D + d0;
+#pragma unroll
+      for (int c = 0; c < 64; c += 8) {
+        uint32_t p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(sm.c[r][d0 + c + 2 * q], sm.c[r][d0 + c + 2 * q + 1]);
+        *reinterpret_cast<uint4*>(dst + c) = make_uint4(p[0], p[1], p[2], p[3]);
+      }
+      return;
+    }
+    // per-head RMSNorm over the 128 dims (/root/reference/megakernel.cu:490-630), then rotate-half
+    // RoPE with the table entry of dim d mod 64 (/root/reference/megakernel.cu:548-555)
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 64; ++c) ss = fmaf(sm.c[r][d0 + c], sm.c[r][d0 + c], ss);
+    ss += __shfl_xor(ss, 1);
+    const float rs = rsqrtf(ss / (float)D + EPS);
+    const uint16_t* nw = tn < HQ ? g.q_norm : g.k_norm;
+    const uint16_t* cr = g.cos_tab + (size_t)pos * D;
+    const uint16_t* sr = g.sin_tab + (size_t)pos * D;
+    const int dp = 64 - d0;  // partner half
+#pragma unroll
+    for (int c = 0; c < 64; c += 8) {
+      float o[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = c + q;
+        const float u = sm.c[r][d0 + i] * rs * bf16_to_f32(nw[d0 + i]);
+        const float up = sm.c[r][dp + i] * rs * bf16_to_f32(nw[dp + i]);
+        const float cs = bf16_to_f32(cr[i]), sn = bf16_to_f32(sr[i]);
+        o[q] = half == 0 ? u * cs - up * sn : u * cs + up * sn;
+      }
+      if (tn < HQ) {
+        uint4 hi, lo;
+        split8(o, hi, lo);
+        const size_t off = (size_t)m * (HQ * D) + tn * D + d0 + c;
+        *reinterpret_cast<uint4*>(g.qh + off) = hi;
+        *reinterpret_cast<uint4*>(g.ql + off) = lo;
+      } else {
+        uint32_t p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(o[2 * q], o[2 * q + 1]);
+        *reinterpret_cast<uint4*>(g.k_cache + (((size_t)g.layer * HKV + (tn - HQ)) * g.max_seq + pos) * D + d0 + c) =
+            make_uint4(p[0], p[1], p[2], p[3]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Causal attention of the prompt rows (/root/reference/megakernel.cu:228-370 for one query; here a
+// block of 64 queries of one head per workgroup, flash-style over blocks of 64 keys). Query row m
+// sits at position `position + m` and attends keys [0, position + m] of the cache, which already
+// holds this layer's new rows (written by the QKV epilogue). Wave w owns queries 16w..16w+15 of
+// the block.
+//   S^T = K . Q^T on the matrix cores (keys as rows): lane l holds the scores of query i = l % 16
+//         against keys 16 mb + 4 g + j -- so each query's row statistics (max, sum) are a
+//         reduction over registers and the 4 lanes i, i+16, i+32, i+48;
+//   O  += P . V: the A operand (8 keys of query i per lane) is exactly what a lane holds of two
+//         consecutive S^T blocks, with key slot 8g + jj meaning key 4g + jj (jj < 4) or
+//         16 + 4g + jj - 4; V is staged transposed in LDS ([dim][key]) so that the B operand
+//         (those 8 keys at one dim) is two 8-byte reads.
+// Output rows (normalised) as the bf16 hi/lo pair the O-projection GEMM takes, [M][16 * 128].
+// ------------------------------------------------------------------------------------------------
+constexpr int QB = 64, KB = 64;
+constexpr int KSP = D + 8;   // padded K row in LDS (272 B)
+constexpr int VSP = KB + 8;  // padded V^T row (144 B)
+
+struct AttnArgs {
+  const uint16_t* qh;
+  const uint16_t* ql;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  uint16_t* oh;
+  uint16_t* ol;
+  int ldo;
+  int M, layer, position, max_seq;
+};
+
+__global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[KB][KSP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[D][VSP];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int h = blockIdx.y, kvh = h >> 1;
+  const int q0 = blockIdx.x * QB;                       // first query row of the block
+  const int qrow = q0 + 16 * w + li;                    // this lane's query (score layout)
+  const int qpos = a.position + qrow;
+  const int last = a.position + min(a.M, q0 + QB) - 1;  // last position any query of the block sees
+  const int nkb = last / KB + 1;
+  const size_t kvbase = ((size_t)a.layer * HKV + kvh) * a.max_seq * D;
+
+  // this lane's query fragments (B operand of S^T = K . Q^T): dims 32 s + 8 g .. +7, hi and lo
+  uint4 fq[2][4];
+  {
+    const int qr = min(qrow, a.M - 1);
+    const size_t o = (size_t)qr * (HQ * D) + h * D + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      fq[0][s] = *reinterpret_cast<const uint4*>(a.qh + o + 32 * s);
+      fq[1][s] = *reinterpret_cast<const uint4*>(a.ql + o + 32 * s);
+    }
+  }
+  f32x4 acc[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lrun = 0.f;  // running max and sum of query qrow (replicated on its 4 lanes)
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int kp0 = kb * KB;
+    __syncthreads();  // the previous block's tiles are consumed
+    // K rows -> ks[key][dim]; V rows -> vt[dim][key]; keys past `last` are zero
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, key = c >> 4, ch = c & 15;
+      const int kp = kp0 + key;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (kp <= last) {
+        kv = *reinterpret_cast<const uint4*>(a.k_cache + kvbase + (size_t)kp * D + 8 * ch);
+        vv = *reinterpret_cast<const uint4*>(a.v_cache + kvbase + (size_t)kp * D + 8 * ch);
+      }
+      *reinterpret_cast<uint4*>(&ks[key][8 * ch]) = kv;
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        vt[8 * ch + 2 * q][key] = (uint16_t)(vw[q] & 0xFFFFu);
+        vt[8 * ch + 2 * q + 1][key] = (uint16_t)(vw[q] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
+    f32x4 st[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 fk = *reinterpret_cast<const uint4*>(&ks[16 * mb + li][32 * s + 8 * lg]);
+        c = mfma(fk, fq[0][s], c);
+        c = mfma(fk, fq[1][s], c);
+      }
+      st[mb] = c;
+    }
+    // causal mask and scale; block maximum of this lane's query
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kp = kp0 + 16 * mb + 4 * lg + j;
+        const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
+        st[mb][j] = sv;
+        bmax = fmaxf(bmax, sv);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
+    const float alpha = __expf(mrun - mnew);
+    float psum = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = __expf(st[mb][j] - mnew);
+        st[mb][j] = p;
+        psum += p;
+      }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    lrun = lrun * alpha + psum;
+    mrun = mnew;
+    // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits in
+    // lane 4g + j (and its copies)
+    float ar[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
+    // O += P . V over two 32-key steps
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { pv[j] = st[2 * t][j]; pv[4 + j] = st[2 * t + 1][j]; }
+      uint4 ph, pl;
+      split8(pv, ph, pl);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const uint16_t* vr = &vt[16 * nb + li][32 * t + 4 * lg];
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
+        const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        acc[nb] = mfma(ph, fv, acc[nb]);
+        acc[nb] = mfma(pl, fv, acc[nb]);
+      }
+    }
+  }
+  // normalise by each row's sum (query 4g + j's, from lane 4g + j) and write hi/lo
+  float linv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) linv[j] = 1.f / __shfl(lrun, 4 * lg + j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = q0 + 16 * w + 4 * lg + j;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const float o = acc[nb][j] * linv[j];
+      const uint16_t hi = f32_to_bf16(o);
+      const uint16_t lo = f32_to_bf16(o - bf16_to_f32(hi));
+      const size_t off = (size_t)m * a.ldo + h * D + 16 * nb + li;
+      a.oh[off] = hi;
+      a.ol[off] = lo;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Final RMSNorm of rows row0 .. row0 + R - 1 of x and the tied LM head with fused greedy argmax
+// (/root/reference/megakernel.cu:876-893 and model.py:97): logits[r][v] = E[v] . norm(x[row0 + r]);
+// keys[r] = max over v
+// of (order-preserving bf16 of the logit) << 32 | ~v, so equal bf16 values prefer the lowest index.
+// Every workgroup normalises the R rows into LDS (bf16 hi/lo), then its 8 waves stream vocabulary
+// rows (row v to wave v % (8 * grid)), 4 rows in flight per wave.
+// ------------------------------------------------------------------------------------------------
+constexpr int LM_MAXR = 8;
+
+__device__ __forceinline__ u64 argmax_key(float logit, int idx) {
+  uint32_t u = (uint32_t)f32_to_bf16(logit) << 16;
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((u64)u << 32) | (0xffffffffu - (uint32_t)idx);
+}
+
+template <int H>
+__global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, int R,
+                                                      const uint16_t* final_norm, const uint16_t* lm_head, int vocab,
+                                                      float* logits, u64* keys, const int32_t* bad) {
+  constexpr int C = H / 512;  // 16-byte chunks per lane of one vocabulary row
+  __shared__ __attribute__((aligned(16))) uint4 xs[2][LM_MAXR][H / 8];
+  __shared__ u64 best[8][LM_MAXR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // normalise: wave w < R handles row w
+  if (w < R) {
+    constexpr int E = H / 64;
+    const float* xr = x + (size_t)(row0 + w) * H + E * lane;
+    float v[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = xr[k];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < E; ++k) ss = fmaf(v[k], v[k], ss);
+    const float rs = rsqrtf(wave_sum(ss) / (float)H + EPS);
+#pragma unroll
+    for (int k = 0; k < E; k += 8) {
+      float wv[8], y[8];
+      unpack8(*reinterpret_cast<const uint4*>(final_norm + E * lane + k), wv);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
+      split8(y, xs[0][w][(E * lane + k) / 8], xs[1][w][(E * lane + k) / 8]);
+    }
+  }
+  __syncthreads();
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  auto dot2 = [](uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  };
+  u64 mine[LM_MAXR];
+#pragma unroll
+  for (int r = 0; r < LM_MAXR; ++r) mine[r] = 0;
+  const int stride = 8 * gridDim.x;
+  const bool failed = *bad != 0;  // an input token was out of range: NaN logits
+  constexpr int LP = 4;
+  for (int v0 = blockIdx.x * 8 + w; v0 < vocab; v0 += LP * stride) {
+    uint4 wr[LP][C];
+#pragma unroll
+    for (int p = 0; p < LP; ++p) {
+      const int v = min(v0 + p * stride, vocab - 1);
+#pragma unroll
+      for (int k = 0; k < C; ++k) wr[p][k] = ld_stream(reinterpret_cast<const uint4*>(lm_head + (size_t)v * H) + 64 * k + lane);
+    }
+#pragma unroll
+    for (int p = 0; p < LP; ++p) {
+      const int v = v0 + p * stride;
+#pragma unroll
+      for (int r = 0; r < LM_MAXR; ++r) {
+        if (r >= R) break;
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          const uint4 h = xs[0][r][64 * k + lane], l = xs[1][r][64 * k + lane];
+          s0 = dot2(wr[p][k].x, h.x, s0); s1 = dot2(wr[p][k].x, l.x, s1);
+          s0 = dot2(wr[p][k].y, h.y, s0); s1 = dot2(wr[p][k].y, l.y, s1);
+          s0 = dot2(wr[p][k].z, h.z, s0); s1 = dot2(wr[p][k].z, l.z, s1);
+          s0 = dot2(wr[p][k].w, h.w, s0); s1 = dot2(wr[p][k].w, l.w, s1);
+        }
+        const float s = wave_sum(s0 + s1);
+        if (v < vocab) {
+          if (lane == 0) logits[(size_t)r * vocab + v] = failed ? __builtin_nanf("") : s;
+          const u64 k = argmax_key(s, v);
+          mine[r] = mine[r] > k ? mine[r] : k;
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < LM_MAXR; ++r) best[w][r] = mine[r];
+  }
+  __syncthreads();
+  if (tid < R) {
+    u64 b = 0;
+    for (int q = 0; q < 8; ++q) b = b > best[q][tid] ? b : best[q][tid];
+    atomicMax(keys + tid, b);
+  }
+}
+
+__global__ void keys_init_kernel(u64* keys, int32_t* bad) {
+  if (threadIdx.x < LM_MAXR) keys[threadIdx.x] = 0;
+  if (threadIdx.x == 0) *bad = 0;
+}
+
+__global__ void keys_to_tokens_kernel(const u64* keys, int R, const int32_t* bad, int32_t* out) {
+  const int r = threadIdx.x;
+  if (r < R) out[r] = (keys[r] && *bad == 0) ? (int32_t)(0xffffffffu - (uint32_t)(keys[r] & 0xffffffffu)) : -1;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------------
+struct Work {
+  float* x;
+  uint16_t *ah, *al, *bh, *bl, *qh, *ql;
+  u64* keys;
+  int32_t* bad;
+};
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16 [M][max(H, 2048)]; b (hi, lo) bf16
+// [M][I]; q (hi, lo) bf16 [M][2048]; the argmax keys. Offsets in bytes, each 256-byte aligned.
+struct Layout {
+  size_t x, ah, al, bh, bl, qh, ql, keys, bad, bytes;
+};
+static Layout layout(int H, int I, int M) {
+  const size_t A = H > HQ * D ? H : HQ * D;
+  Layout L;
+  size_t o = 0;
+  auto take = [&](size_t n) { const size_t r = o; o += align256(n); return r; };
+  L.x = take((size_t)M * H * 4);
+  L.ah = take((size_t)M * A * 2);
+  L.al = take((size_t)M * A * 2);
+  L.bh = take((size_t)M * I * 2);
+  L.bl = take((size_t)M * I * 2);
+  L.qh = take((size_t)M * HQ * D * 2);
+  L.ql = take((size_t)M * HQ * D * 2);
+  L.keys = take(LM_MAXR * 8);
+  L.bad = take(4);
+  L.bytes = o;
+  return L;
+}
+static Work carve(void* base, const Layout& L) {
+  char* p = static_cast<char*>(base);
+  Work w;
+  w.x = reinterpret_cast<float*>(p + L.x);
+  w.ah = reinterpret_cast<uint16_t*>(p + L.ah);
+  w.al = reinterpret_cast<uint16_t*>(p + L.al);
+  w.bh = reinterpret_cast<uint16_t*>(p + L.bh);
+  w.bl = reinterpret_cast<uint16_t*>(p + L.bl);
+  w.qh = reinterpret_cast<uint16_t*>(p + L.qh);
+  w.ql = reinterpret_cast<uint16_t*>(p + L.ql);
+  w.keys = reinterpret_cast<u64*>(p + L.keys);
+  w.bad = reinterpret_cast<int32_t*>(p + L.bad);
+  return w;
+}
+
+template <int H, int I>
+static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, int position, const uint16_t* embed,
+                      const uint16_t* lm_head, const uint16_t* final_norm, const mk_layer_weights* layers,
+                      const uint16_t* cos_tab, const uint16_t* sin_tab, uint16_t* k_cache, uint16_t* v_cache,
+                      int max_seq, float* logits, int32_t* out_token, const Work& wk, hipStream_t st) {
+  const int A = H > HQ * D ? H : HQ * D;
+  const int mtiles = (M + MT - 1) / MT;
+  hipError_t e;
+#define MKP_LAUNCH(...)                                   \
+  do {                                                    \
+    hipLaunchKernelGGL(__VA_ARGS__);                      \
+    if ((e = hipGetLastError()) != hipSuccess) return e;  \
+  } while (0)
+  MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, wk.bad);
+  for (int l = 0; l < dims.num_layers; ++l) {
+    const mk_layer_weights& lw = layers[l];
+    MKP_LAUNCH(norm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed,
+               dims.vocab, wk.bad, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
+    GemmArgs g{};
+    g.ah = wk.ah; g.al = wk.al; g.lda = A; g.M = M; g.K = H;
+    g.w0 = (const uint16_t*)lw.q_weight; g.w1 = (const uint16_t*)lw.k_weight; g.w2 = (const uint16_t*)lw.v_weight;
+    g.N = (HQ + 2 * HKV) * D;
+    g.q_norm = (const uint16_t*)lw.q_norm_weight; g.k_norm = (const uint16_t*)lw.k_norm_weight;
+    g.cos_tab = cos_tab; g.sin_tab = sin_tab; g.qh = wk.qh; g.ql = wk.ql; g.k_cache = k_cache; g.v_cache = v_cache;
+    g.layer = l; g.position = position; g.max_seq = max_seq;
+    MKP_LAUNCH(gemm_kernel<EPI_QKV>, dim3(g.N / NT, mtiles), dim3(256), 0, st, g);
+    AttnArgs at{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, l, position, max_seq};
+    MKP_LAUNCH(attn_kernel, dim3((M + QB - 1) / QB, HQ), dim3(256), 0, st, at);
+    GemmArgs go{};
+    go.ah = wk.ah; go.al = wk.al; go.lda = A; go.M = M; go.N = H; go.K = HQ * D;
+    go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H;
+    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles), dim3(256), 0, st, go);
+    MKP_LAUNCH(norm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad,
+               (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
+    GemmArgs gu{};
+    gu.ah = wk.ah; gu.al = wk.al; gu.lda = A; gu.M = M; gu.N = 2 * I; gu.K = H;
+    gu.w0 = (const uint16_t*)lw.gate_proj_weight; gu.w1 = (const uint16_t*)lw.up_proj_weight;
+    gu.bh = wk.bh; gu.bl = wk.bl; gu.ldb = I;
+    MKP_LAUNCH(gemm_kernel<EPI_SILU>, dim3(I / (NT / 2), mtiles), dim3(256), 0, st, gu);
+    GemmArgs gd{};
+    gd.ah = wk.bh; gd.al = wk.bl; gd.lda = I; gd.M = M; gd.N = H; gd.K = I;
+    gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H;
+    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles), dim3(256), 0, st, gd);
+  }
+  // the last row's logits and greedy token
+  MKP_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, wk.x, M - 1, 1, final_norm, lm_head, dims.vocab, logits,
+             wk.keys, wk.bad);
+  if (out_token) MKP_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad, out_token);
+#undef MKP_LAUNCH
+  return hipSuccess;
+}
+
+}  // namespace mkp
+
+using namespace mkp;
+
+extern "C" size_t mk_prefill_workspace_bytes(const mk_model_dims* dims, int num_tokens) {
+  if (!dims || num_tokens < 1) return 0;
+  return layout(dims->hidden, dims->intermediate, num_tokens).bytes;
+}
+
+extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                                 const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                                 const void* layer_weights, const void* cos_table, const void* sin_table,
+                                 void* k_cache, void* v_cache, int max_seq_len, float* logits, int32_t* out_token,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!dims || !tokens || !embed_weight || !lm_head_weight || !final_norm_weight || !layer_weights ||
+      !cos_table || !sin_table || !k_cache || !v_cache || !logits || !workspace)
+    return hipErrorInvalidValue;
+  const bool s06 = dims->hidden == 1024 && dims->intermediate == 3072;
+  const bool s17 = dims->hidden == 2048 && dims->intermediate == 6144;
+  if (!(s06 || s17) || dims->num_layers < 1 || dims->vocab < 1) return hipErrorInvalidValue;
+  if (num_tokens < 1 || position < 0 || max_seq_len < 1 || (long long)position + num_tokens > max_seq_len)
+    return hipErrorInvalidValue;
+  const Layout L = layout(dims->hidden, dims->intermediate, num_tokens);
+  if (workspace_bytes < L.bytes) return hipErrorInvalidValue;
+  const Work wk = carve(workspace, L);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return hipErrorInvalidValue;
+  const mk_layer_weights* lw = static_cast<const mk_layer_weights*>(layer_weights);  // host array
+  if (s06)
+    return run<1024, 3072>(*dims, tokens, num_tokens, position, (const uint16_t*)embed_weight,
+                           (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
+                           (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
+                           (uint16_t*)v_cache, max_seq_len, logits, out_token, wk, stream);
+  return run<2048, 6144>(*dims, tokens, num_tokens, position, (const uint16_t*)embed_weight,
+                         (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
+                         (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
+                         (uint16_t*)v_cache, max_seq_len, logits, out_token, wk, stream);
+}

@@ -262,6 +262,40 @@ torch::Tensor decode_steps_paged(torch::Tensor tokens, int64_t n, bool generate,
   return logits;
 }
 
+// Batched prefill (mk_prefill): tokens (int32 [n] on the weights' device) at positions position ..
+// position + n - 1, K/V rows written into the [L, 8, max_seq, 128] caches; returns the last token's
+// fp32 logits [V] and its greedy token (int32 [1] on the device). The workspace is a tensor from
+// torch's caching allocator, held until the call's work is queued.
+std::tuple<torch::Tensor, torch::Tensor> prefill(torch::Tensor tokens, torch::Tensor embed, torch::Tensor lm_head,
+                                                 torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                 torch::Tensor cos, torch::Tensor sin, torch::Tensor kc, torch::Tensor vc,
+                                                 int64_t position, int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len);
+  TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
+                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) >= 1,
+              "megakernel: tokens must be a non-empty contiguous int32 [n] tensor on ", c.dev);
+  const int64_t n = tokens.size(0);
+  TORCH_CHECK(position + n <= max_seq_len, "megakernel: position + n (", position + n, ") exceeds max_seq_len (",
+              max_seq_len, ")");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  std::vector<mk_layer_weights> table(c.dims.num_layers);
+  for (int64_t l = 0; l < c.dims.num_layers; ++l) {
+    const torch::Tensor* t = &lw[l * kPerLayer];
+    table[l] = {t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), t[3].data_ptr(), t[4].data_ptr(), t[5].data_ptr(),
+                t[6].data_ptr(), t[7].data_ptr(), t[8].data_ptr(), t[9].data_ptr(), t[10].data_ptr()};
+  }
+  const size_t bytes = mk_prefill_workspace_bytes(&c.dims, (int)n);
+  auto ws = torch::empty({(int64_t)bytes}, embed.options().dtype(torch::kUInt8));
+  auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  auto tok = torch::empty({1}, embed.options().dtype(torch::kInt32));
+  MK_HIP_CHECK(mk_prefill(&c.dims, tokens.data_ptr<int32_t>(), (int)n, (int)position, embed.data_ptr(),
+                          lm_head.data_ptr(), final_norm.data_ptr(), table.data(), cos.data_ptr(), sin.data_ptr(),
+                          kc.data_ptr(), vc.data_ptr(), (int)max_seq_len, logits.data_ptr<float>(),
+                          tok.data_ptr<int32_t>(), ws.data_ptr(), bytes, stream));
+  return {logits, tok};
+}
+
 int64_t status() {
   uint32_t s = 0;
   MK_HIP_CHECK(mk_status(&s));
@@ -301,6 +335,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "int32 greedy token on device)");
   m.def("decode_steps_paged", &decode_steps_paged,
         "decode_steps on a paged K/V cache (tensors as decode_paged); returns the last step's fp32 logits");
+  m.def("prefill", &prefill,
+        "batched prefill of int32 tokens [n] at positions position..position+n-1 into the [L, 8, max_seq, 128] "
+        "caches; returns (fp32 logits of the last token, int32 greedy token on device)");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
   m.def("reset", &reset, "clear the decode workspaces (exchange words, status words) and restart their launch sequences; synchronizes");

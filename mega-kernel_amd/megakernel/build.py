@@ -1,7 +1,7 @@
 """Build the gfx950 decode library and its PyTorch extension in-tree.
 
 Two artefacts, both next to this package (``mega-kernel_amd/``):
-  ``libmegakernel_amd.so``   the HIP kernel and its C ABI (``include/megakernel_amd.h``), no torch
+  ``libmegakernel_amd.so``   the HIP kernels (decode, prefill) and their C ABI (``include/megakernel_amd.h``), no torch
   ``megakernel_extension*.so``  the PyTorch operator ``decode`` (reference name, reference signature)
                                 linked against the library with an $ORIGIN rpath.
 Run ``python -m megakernel.build`` from ``mega-kernel_amd/`` or call ``build()``.
@@ -41,9 +41,9 @@ def _run(cmd, verbose):
 
 
 def build_library(verbose=True):
-    src = os.path.join(CSRC, "decode_kernel.hip")
+    srcs = [os.path.join(CSRC, f) for f in ("decode_kernel.hip", "prefill_kernel.hip")]
     tmp = LIB + ".tmp"
-    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", src, "-o", tmp], verbose)
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

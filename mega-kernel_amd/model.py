@@ -15,8 +15,9 @@ Mirrors ``/root/reference/model.py`` step for step:
     the host reads each token back only to feed the next call, as the reference does.
   * ``--device-loop``: the same greedy generation as one ``decode_steps`` call, which feeds each
     step's argmax to the next launch on the device; the host reads the tokens once at the end.
-  * ``--native-prefill``: the prompt goes through ``decode_steps`` in teacher mode from an empty
-    cache (one launch per prompt token) instead of the Transformers prefill and cache copy.
+  * ``--native-prefill``: the prompt goes through the batched prefill kernel (``prefill``: all
+    prompt tokens at once on the matrix cores, writing the ``[L, 8, max_seq, 128]`` cache
+    directly) instead of the Transformers prefill and cache copy.
 
     python mega-kernel_amd/model.py [--shape qwen3-0.6b] [--prompt 32] [--max-seq 512] [--new 64]
                                     [--device-loop] [--native-prefill]
@@ -72,10 +73,14 @@ def main(argv=None):
 
     k_cache, v_cache = megakernel.empty_cache(len(model.model.layers), a.max_seq, dev)
     if a.native_prefill:
-        prompt = torch.cat([ids[0], torch.zeros(1, dtype=ids.dtype)]).to(device=dev, dtype=torch.int32)
-        kernel.decode_steps(prompt, a.prompt, False, embed, embed, final_norm, layer_weights, cos, sin, k_cache,
-                            v_cache, 0, a.max_seq)
-        position, token = a.prompt, int(prompt[a.prompt].item())
+        prompt = ids[0].to(device=dev, dtype=torch.int32)
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record()
+        _, first = kernel.prefill(prompt, embed, embed, final_norm, layer_weights, cos, sin, k_cache, v_cache, 0,
+                                  a.max_seq)
+        p1.record()
+        position, token = a.prompt, int(first.item())
+        print(f"prefill: {a.prompt} tokens in {p0.elapsed_time(p1):.2f} ms (batched prefill kernel)")
     else:
         with torch.inference_mode():
             out = model(ids, use_cache=True)

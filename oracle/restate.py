@@ -264,3 +264,59 @@ def attention_split(q, k, v, scale, splits):
     lsum = sum(p[1] * torch.exp(p[0] - M) for p in parts)
     acc = sum(p[2] * torch.exp(p[0] - M) for p in parts)
     return acc / lsum
+
+
+def prefill(W, ids, cos, sin, max_seq, position=0, k_cache=None, v_cache=None, causal=True):
+    """Batched form of ``decode_step(..., numerics="fp32")`` run once per token: the tokens ``ids``
+    (list or 1-D tensor) at positions ``position .. position + len(ids) - 1`` go through the model
+    together (fp32 matrix products over all rows, causal fp32 softmax attention), their K/V rows
+    are written to the bf16 caches ``[L, Hkv, max_seq, D]`` (new ones if not given; positions before
+    ``position`` must already hold earlier tokens), and the logits of the last token are returned.
+    This is the arithmetic of a prefill that keeps the reference kernel's fp32 activations
+    (/root/reference/megakernel.cu), the work Transformers' prefill does at /root/reference/model.py:72-73.
+    ``causal=False`` lets every row see every key of the prompt (a planted mistake for tests).
+    Returns (fp32 logits [V], k_cache, v_cache)."""
+    s = W.shape
+    D, eps = s.head_dim, s.eps
+    scale = D ** -0.5
+    ids = torch.as_tensor(ids, dtype=torch.long).reshape(-1)
+    P = ids.numel()
+    if k_cache is None:
+        k_cache = torch.zeros(s.layers, s.kv_heads, max_seq, D, dtype=torch.bfloat16)
+        v_cache = torch.zeros_like(k_cache)
+    pos = torch.arange(position, position + P)
+    half = D // 2
+    c = cos[pos].float()[:, None, :half]
+    sn = sin[pos].float()[:, None, :half]
+    T = position + P
+    causal = torch.arange(T)[None, :] <= (pos[:, None] if causal else T)  # [P, T]: key t visible to row p
+    rep = s.q_heads // s.kv_heads
+    x = W.embed[ids].float().clone()
+
+    def rms(t, w):
+        return t * torch.rsqrt((t * t).mean(-1, keepdim=True) + eps) * w
+
+    def nr(t, w):
+        t = rms(t, w)
+        a, b = t[..., :half], t[..., half:]
+        return torch.cat((a * c - b * sn, b * c + a * sn), -1)
+
+    for li, lw in enumerate(W.layers):
+        h = rms(x, lw["input_layernorm"])
+        q = (h @ lw["q_proj"].T).view(P, s.q_heads, D)
+        k = (h @ lw["k_proj"].T).view(P, s.kv_heads, D)
+        v = (h @ lw["v_proj"].T).view(P, s.kv_heads, D)
+        q, k = nr(q, lw["q_norm"]), nr(k, lw["k_norm"])
+        k_cache[li, :, position:T] = k.transpose(0, 1).to(torch.bfloat16)
+        v_cache[li, :, position:T] = v.transpose(0, 1).to(torch.bfloat16)
+        kk = k_cache[li, :, :T].float().repeat_interleave(rep, 0)  # [Hq, T, D]
+        vv = v_cache[li, :, :T].float().repeat_interleave(rep, 0)
+        sc = (q.transpose(0, 1) @ kk.transpose(1, 2)) * scale      # [Hq, P, T]
+        sc = sc.masked_fill(~causal[None], -math.inf)
+        attn = (torch.softmax(sc, -1) @ vv).transpose(0, 1).reshape(P, -1)
+        x = x + attn @ lw["o_proj"].T
+        h2 = rms(x, lw["post_attention_layernorm"])
+        g, u = h2 @ lw["gate_proj"].T, h2 @ lw["up_proj"].T
+        x = x + (g / (1 + torch.exp(-g)) * u) @ lw["down_proj"].T
+    hfin = rms(x[-1], W.final_norm)
+    return W.embed @ hfin, k_cache, v_cache

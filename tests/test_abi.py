@@ -217,3 +217,38 @@ def test_noalloc_entry_point_rejects_out_of_limit_arguments_before_launch(lib):
     assert call(Dims(1024, 3072, 28, 151936), token=151936) == HIP_ERROR_INVALID_VALUE
     lib.mk_workspace_bytes.restype = ctypes.c_size_t
     assert 1 << 20 <= lib.mk_workspace_bytes() <= 2 << 20
+
+
+def test_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
+    """``mk_prefill`` validates shape, token count, positions and the workspace size and alignment
+    before any HIP call; ``mk_prefill_workspace_bytes`` grows with the token count."""
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                    ("num_layers", ctypes.c_int32), ("vocab", ctypes.c_int32)]
+
+    ws = lib.mk_prefill_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.POINTER(Dims), i32]
+    good = Dims(1024, 3072, 28, 151936)
+    n1, n2 = ws(ctypes.byref(good), 32), ws(ctypes.byref(good), 3584)
+    assert 0 < n1 < n2 and n1 % 256 == 0
+    assert ws(ctypes.byref(good), 0) == 0
+
+    f = lib.mk_prefill
+    f.restype = i32
+    f.argtypes = [ctypes.POINTER(Dims), vp, i32, i32] + [vp] * 8 + [i32, vp, vp, vp, ctypes.c_size_t, vp]
+    d = vp(256)
+
+    def call(dims=good, n=32, position=0, max_seq=512, workspace=d, nbytes=None):
+        nb = ws(ctypes.byref(dims), n) if nbytes is None else nbytes
+        return f(ctypes.byref(dims), d, n, position, *([d] * 8), max_seq, d, None, workspace, nb, None)
+
+    assert call(Dims(1024, 4096, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(n=0) == HIP_ERROR_INVALID_VALUE
+    assert call(position=-1) == HIP_ERROR_INVALID_VALUE
+    assert call(position=500, n=13) == HIP_ERROR_INVALID_VALUE  # past max_seq_len
+    assert call(nbytes=n1 - 1) == HIP_ERROR_INVALID_VALUE
+    assert call(workspace=vp(256 + 16)) == HIP_ERROR_INVALID_VALUE  # not 256-byte aligned
+    assert call(workspace=None) == HIP_ERROR_INVALID_VALUE

@@ -284,3 +284,46 @@ def test_bf16_emulation_is_no_closer_to_transformers_than_fp32():
           f"mean rms logit distance: bf16 emulation {mean_hf:.5f}, fp32 {mean_fp32:.5f}")
     assert agree_hf <= agree_fp32
     assert mean_hf > mean_fp32
+
+
+@pytest.mark.parametrize("name, P, position", [("tiny", 1, 0), ("tiny", 13, 0), ("tiny", 9, 6), ("mini", 20, 0)])
+def test_batched_prefill_equals_decode_steps(name, P, position):
+    """``restate.prefill`` (all tokens in one pass: batched products, causal softmax) is the same
+    arithmetic as ``restate.decode_step(numerics="fp32")`` run once per token. Summation orders
+    differ, so a K/V value whose fp32 sums differ in the last bits may round to the neighbouring
+    bf16, and such a flip moves the later layers slightly: the last logits agree to the tolerance
+    the GPU checks use (5e-3), the rows to one bf16 rounding step of the largest values. With
+    ``position`` > 0 the earlier rows come from the cache (a chunked prefill). The causal mask is
+    pinned by planting its removal: the K/V rows of layer 1 then move by more than 1e-2."""
+    s = SHAPES[name]
+    model = hf.build_model(name, max_positions=64)
+    W = restate.Weights.from_model(model, s)
+    cos, sin = hf.rope_tables(model, 64)
+    ids = hf.prompt_ids(position + P, s.vocab, seed=5)[0].tolist()
+    kd = torch.zeros(s.layers, s.kv_heads, 64, s.head_dim, dtype=torch.bfloat16)
+    vd = torch.zeros_like(kd)
+    for p, t in enumerate(ids):
+        want, _ = restate.decode_step(W, kd, vd, t, p, cos, sin, numerics="fp32")
+    kb = torch.zeros_like(kd)
+    vb = torch.zeros_like(vd)
+    if position:
+        kb[:, :, :position], vb[:, :, :position] = kd[:, :, :position], vd[:, :, :position]
+    got, kb, vb = restate.prefill(W, ids[position:], cos, sin, 64, position, kb.clone(), vb.clone())
+    assert (got - want).abs().max().item() < 5e-3
+    assert torch.nn.functional.cosine_similarity(got.double(), want.double(), dim=0).item() > 0.999999
+    for a, b in ((kb, kd), (vb, vd)):
+        # one bf16 rounding step of the largest values, the bound the GPU cache checks use; beyond
+        # one step of their own magnitude only where an earlier flip propagated (rare)
+        d = (a.float() - b.float()).abs()
+        assert d.max().item() <= 2 ** -6 * max(1.0, b.float().abs().max().item())
+        ulp = 2.0 ** (torch.floor(torch.log2(b.float().abs().clamp_min(2 ** -126))) - 7)
+        assert (d > ulp).float().mean().item() < 0.01
+        assert a[:, :, position + P:].abs().sum() == 0
+    # the causal mask matters: rows that also see later keys give other K/V rows from layer 1 on
+    if P > 2:
+        k0 = torch.zeros_like(kd)
+        v0 = torch.zeros_like(vd)
+        if position:
+            k0[:, :, :position], v0[:, :, :position] = kd[:, :, :position], vd[:, :, :position]
+        _, kw, _ = restate.prefill(W, ids[position:], cos, sin, 64, position, k0, v0, causal=False)
+        assert (kw[1:, :, position:position + P - 1].float() - kd[1:, :, position:position + P - 1].float()).abs().max() > 1e-2
