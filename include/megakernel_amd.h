@@ -148,6 +148,31 @@ hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Batched decode: `batch` (1..8) independent sequences advance by one token each in one call.
+ * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a
+ * device-side loop can advance them): it writes its K/V rows at positions[b] of its own cache and
+ * attends over [0, positions[b]]. k_cache/v_cache are bf16 [batch][num_layers][8][max_seq_len][128]
+ * (sequence b's cache is the decode layout at offset b). Writes fp32 logits [batch][vocab] and,
+ * when out_tokens is not NULL, each sequence's greedy token (argmax of the bf16-rounded logits,
+ * lowest index on ties). Each layer's products run on the matrix cores with the weights read once
+ * for all sequences; numerics are mk_decode's, so each sequence gets what mk_decode gives it up to
+ * fp32 summation order.
+ *   layer_weights     HOST array of mk_layer_weights[num_layers] (device pointers inside)
+ *   workspace         device memory of at least mk_decode_batch_workspace_bytes(dims, batch,
+ *                     max_seq_len) bytes, 256-byte aligned, owned by the caller
+ * A token or position out of range (checked on the device) makes the call report NaN logits and
+ * token -1 for every sequence. Asynchronous on `stream`; argument errors return
+ * hipErrorInvalidValue before any launch. No counterpart in the reference, whose operator decodes
+ * one token of one sequence (/root/reference/pytorch_binding.cu:36-48).
+ */
+size_t mk_decode_batch_workspace_bytes(const mk_model_dims* dims, int batch, int max_seq_len);
+hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens, const int32_t* positions,
+                           const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                           const void* layer_weights, const void* cos_table, const void* sin_table, void* k_cache,
+                           void* v_cache, int max_seq_len, float* logits, int32_t* out_tokens, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Several decode steps in one call, with no host synchronization between them: the device-side
  * multi-token loop. Step i (0 <= i < n) runs at position + i and reads its input token from device
  * memory, tokens[i] (int32, device array of n + 1 entries, tokens[0] set by the caller).

@@ -533,8 +533,8 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
 // ------------------------------------------------------------------------------------------------
 // Final RMSNorm of rows row0 .. row0 + R - 1 of x and the tied LM head with fused greedy argmax
 // (/root/reference/megakernel.cu:876-893 and model.py:97): logits[r][v] = E[v] . norm(x[row0 + r]);
-// keys[r] = max over v
-// of (order-preserving bf16 of the logit) << 32 | ~v, so equal bf16 values prefer the lowest index.
+// keys[r] = max over v of (order-preserving bf16 of the logit) << 32 | ~v, so equal bf16 values
+// prefer the lowest index.
 // Every workgroup normalises the R rows into LDS (bf16 hi/lo), then its 8 waves stream vocabulary
 // rows (row v to wave v % (8 * grid)), 4 rows in flight per wave.
 // ------------------------------------------------------------------------------------------------
@@ -637,6 +637,324 @@ __global__ void keys_init_kernel(u64* keys, int32_t* bad) {
 __global__ void keys_to_tokens_kernel(const u64* keys, int R, const int32_t* bad, int32_t* out) {
   const int r = threadIdx.x;
   if (r < R) out[r] = (keys[r] && *bad == 0) ? (int32_t)(0xffffffffu - (uint32_t)(keys[r] & 0xffffffffu)) : -1;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched decode: BMAX = 8 sequences at most, one token each per step, every sequence with its own
+// cache ([B][L][8][max_seq][128]) and position. The layer structure of the prefill, with the
+// products as skinny GEMMs: the weights are the MFMA's 16-row operand A and the sequences'
+// activations, hi and lo, its 16 columns (B operand column 2b + hl), so one
+// v_mfma_f32_16x16x32_bf16 multiplies 16 weight rows x 32 inputs by all 8 sequences at once and
+// each weight byte is read once per step. Sums split over K are written as partials and added in
+// a fixed order by the next kernel, so results are deterministic.
+// ------------------------------------------------------------------------------------------------
+constexpr int BMAX = 8;
+constexpr int KS = 256;  // keys per attention split
+
+enum SkEpi { SK_RAW = 0, SK_PART = 1, SK_SILU = 2 };
+
+struct SkArgs {
+  const uint16_t* xh;  // activations [B][ldx], bf16 hi/lo
+  const uint16_t* xl;
+  int ldx;
+  int B, N, K;
+  // SK_RAW: rows [0, n1) of w0, [n1, n2) of w1, [n2, N) of w2 (Q, K, V); SK_PART: w0; SK_SILU: w0 gate, w1 up
+  const uint16_t* w0;
+  const uint16_t* w1;
+  const uint16_t* w2;
+  int n1, n2;
+  float* out;    // SK_RAW: [B][N]; SK_PART: [gridDim.y][B][N]
+  uint16_t* mh;  // SK_SILU: silu(gate) * up, bf16 hi/lo [B][ldm]
+  uint16_t* ml;
+  int ldm;
+};
+
+// A workgroup takes 16 weight rows (rows 16 bx ..). SK_RAW / SK_PART: its K range [by K / gy, ...)
+// split over the 4 waves; SK_SILU: 16 intermediates, gate rows on waves 0-1 and up rows on waves
+// 2-3, each pair splitting K in two. Each wave's K range is a multiple of 256 (checked on the host).
+template <int EPI>
+__global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
+  __shared__ float red[4][16][BMAX + 1];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int n0 = 16 * blockIdx.x, n = n0 + li;
+  const uint16_t* wrow;
+  int kb, ke;
+  if constexpr (EPI == SK_SILU) {
+    wrow = (w < 2 ? g.w0 : g.w1) + (size_t)n * g.K;
+    const int kc = g.K / 2;
+    kb = (w & 1) * kc;
+    ke = kb + kc;
+  } else {
+    if constexpr (EPI == SK_RAW)
+      wrow = n < g.n1 ? g.w0 + (size_t)n * g.K
+                      : (n < g.n2 ? g.w1 + (size_t)(n - g.n1) * g.K : g.w2 + (size_t)(n - g.n2) * g.K);
+    else
+      wrow = g.w0 + (size_t)n * g.K;
+    const int kc = g.K / gridDim.y, kw = kc / 4;
+    kb = blockIdx.y * kc + w * kw;
+    ke = kb + kw;
+  }
+  // B operand: column li is sequence li / 2, hi (even) or lo (odd)
+  const int sb = li >> 1;
+  const bool live = sb < g.B;
+  const uint16_t* xs = (li & 1 ? g.xl : g.xh) + (size_t)(live ? sb : 0) * g.ldx;
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = kb; k0 < ke; k0 += 256) {
+    uint4 wa[8], xb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      wa[u] = ld_stream(reinterpret_cast<const uint4*>(wrow + k0 + 32 * u + 8 * lg));
+      xb[u] = live ? *reinterpret_cast<const uint4*>(xs + k0 + 32 * u + 8 * lg) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c = mfma(wa[u], xb[u], c);
+  }
+  // C[row 4 lg + j][column li]: sequence li / 2 is the sum of its hi and lo columns
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float v = c[j] + __shfl_xor(c[j], 1);
+    if (!(li & 1)) red[w][4 * lg + j][sb] = v;
+  }
+  __syncthreads();
+  if constexpr (EPI == SK_SILU) {
+    if (tid < 16 * g.B) {
+      const int r = tid / g.B, b = tid % g.B;
+      const float gt = red[0][r][b] + red[1][r][b], up = red[2][r][b] + red[3][r][b];
+      const float m = gt / (1.f + expf(-gt)) * up;
+      const uint16_t hi = f32_to_bf16(m);
+      g.mh[(size_t)b * g.ldm + n0 + r] = hi;
+      g.ml[(size_t)b * g.ldm + n0 + r] = f32_to_bf16(m - bf16_to_f32(hi));
+    }
+  } else {
+    if (tid < 16 * g.B) {
+      const int r = tid / g.B, b = tid % g.B;
+      const float v = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
+      g.out[((size_t)blockIdx.y * g.B + b) * g.N + n0 + r] = v;
+    }
+  }
+}
+
+// Rows b < B of the residual: with `tokens`, x[b] = embed[tokens[b]] (a token outside [0, vocab)
+// reads row 0 and sets *bad); with `part`, x[b] += sum over s < S of part[s][b] (in order); then,
+// with `w`, RMSNorm into the bf16 hi/lo pair [B][lda]. One wave per row.
+template <int H>
+__global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tokens, const uint16_t* embed, int vocab,
+                                                    int32_t* bad, const float* part, int S, const uint16_t* w,
+                                                    uint16_t* ah, uint16_t* al, int lda, int B) {
+  constexpr int E = H / 64;
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  float v[E];
+  float* xr = x + (size_t)b * H + E * lane;
+  if (tokens) {
+    int tok = tokens[b];
+    if (tok < 0 || tok >= vocab) {
+      if (lane == 0) *bad = 1;
+      tok = 0;
+    }
+    const uint16_t* er = embed + (size_t)tok * H + E * lane;
+#pragma unroll
+    for (int k = 0; k < E; k += 8) {
+      float t[8];
+      unpack8(*reinterpret_cast<const uint4*>(er + k), t);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[k + q] = t[q];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = xr[k];
+    for (int s = 0; s < S; ++s) {
+      const float* pr = part + ((size_t)s * B + b) * H + E * lane;
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[k] += pr[k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < E; k += 4) *reinterpret_cast<float4*>(xr + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+  if (!w) return;
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < E; ++k) ss = fmaf(v[k], v[k], ss);
+  const float rs = rsqrtf(wave_sum(ss) / (float)H + EPS);
+#pragma unroll
+  for (int k = 0; k < E; k += 8) {
+    float wv[8], y[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + E * lane + k), wv);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
+    uint4 hi, lo;
+    split8(y, hi, lo);
+    *reinterpret_cast<uint4*>(ah + (size_t)b * lda + E * lane + k) = hi;
+    *reinterpret_cast<uint4*>(al + (size_t)b * lda + E * lane + k) = lo;
+  }
+}
+
+// Position of sequence b, clamped into the cache (an out-of-range position sets *bad).
+__device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_seq, int32_t* bad) {
+  const int p = positions[b];
+  if (p < 0 || p >= max_seq) {
+    if (bad) *bad = 1;
+    return p < 0 ? 0 : max_seq - 1;
+  }
+  return p;
+}
+
+// The raw Q/K/V sums of each sequence (fp32 [B][4096]): per-head RMSNorm + RoPE on q and k (one
+// wave per sequence and head, lane l holding dims l and l + 64, the RoPE pair), q kept as a bf16
+// hi/lo pair [B][2048], k and v rounded to bf16 into the sequence's cache at its position.
+__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, const int32_t* positions,
+                                                       const uint16_t* q_norm, const uint16_t* k_norm,
+                                                       const uint16_t* cos_tab, const uint16_t* sin_tab, uint16_t* qh,
+                                                       uint16_t* ql, uint16_t* k_cache, uint16_t* v_cache, int L,
+                                                       int layer, int max_seq, int32_t* bad) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= B * (HQ + 2 * HKV)) return;
+  const int b = item / (HQ + 2 * HKV), hd = item % (HQ + 2 * HKV);
+  const int pos = seq_pos(positions, b, max_seq, lane == 0 ? bad : nullptr);
+  const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
+  float u0 = r[lane], u1 = r[lane + 64];
+  auto cache_row = [&](uint16_t* cache, int kvh) {
+    return cache + ((((size_t)b * L + layer) * HKV + kvh) * max_seq + pos) * D;
+  };
+  if (hd >= HQ + HKV) {  // v
+    uint16_t* dst = cache_row(v_cache, hd - HQ - HKV);
+    dst[lane] = f32_to_bf16(u0);
+    dst[lane + 64] = f32_to_bf16(u1);
+    return;
+  }
+  const float rs = rsqrtf(wave_sum(u0 * u0 + u1 * u1) / (float)D + EPS);
+  const uint16_t* nw = hd < HQ ? q_norm : k_norm;
+  u0 *= rs * bf16_to_f32(nw[lane]);
+  u1 *= rs * bf16_to_f32(nw[lane + 64]);
+  const float cs = bf16_to_f32(cos_tab[(size_t)pos * D + lane]), sn = bf16_to_f32(sin_tab[(size_t)pos * D + lane]);
+  const float o0 = u0 * cs - u1 * sn, o1 = u1 * cs + u0 * sn;
+  if (hd < HQ) {
+    uint16_t* h = qh + (size_t)b * HQ * D + hd * D;
+    uint16_t* l = ql + (size_t)b * HQ * D + hd * D;
+    const uint16_t h0 = f32_to_bf16(o0), h1 = f32_to_bf16(o1);
+    h[lane] = h0;
+    h[lane + 64] = h1;
+    l[lane] = f32_to_bf16(o0 - bf16_to_f32(h0));
+    l[lane + 64] = f32_to_bf16(o1 - bf16_to_f32(h1));
+  } else {
+    uint16_t* dst = cache_row(k_cache, hd - HQ);
+    dst[lane] = f32_to_bf16(o0);
+    dst[lane + 64] = f32_to_bf16(o1);
+  }
+}
+
+// Split-K attention of one sequence and K/V head over keys [KS s, KS s + KS) of [0, position]: the
+// head pair's two queries against each key (16 groups of 16 lanes, lane t holding dims 8t..8t+7,
+// keys dealt to the groups in turn, online softmax per group, /root/reference/megakernel.cu:228-370),
+// the 16 group partials merged in LDS into this split's (acc[128], m, l) per query head.
+// part: [B][8][S][2][D + 2].
+constexpr int APW = D + 2;
+
+__global__ void __launch_bounds__(256) battn_partial_kernel(const uint16_t* qh, const uint16_t* ql,
+                                                            const uint16_t* k_cache, const uint16_t* v_cache,
+                                                            const int32_t* positions, int L, int layer, int max_seq,
+                                                            float* part, int S) {
+  __shared__ float gacc[16][2][D];
+  __shared__ float gml[16][2][2];
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int ctx = seq_pos(positions, b, max_seq, nullptr) + 1;
+  const int k0 = s * KS;
+  if (k0 >= ctx) return;  // this split is empty; the merge reads splits below ceil(ctx / KS) only
+  const int k1 = min(k0 + KS, ctx);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int gi = w * 4 + (lane >> 4), t = lane & 15;
+  float qa[8], qb[8];
+  {
+    const size_t o0 = (size_t)b * HQ * D + (2 * kvh) * D + 8 * t, o1 = o0 + D;
+    float h[8], l[8];
+    unpack8(*reinterpret_cast<const uint4*>(qh + o0), h);
+    unpack8(*reinterpret_cast<const uint4*>(ql + o0), l);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qa[i] = h[i] + l[i];
+    unpack8(*reinterpret_cast<const uint4*>(qh + o1), h);
+    unpack8(*reinterpret_cast<const uint4*>(ql + o1), l);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qb[i] = h[i] + l[i];
+  }
+  const size_t base = (((size_t)b * L + layer) * HKV + kvh) * max_seq * D + 8 * t;
+  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f, a0[8], a1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
+  auto step = [&](float sc, const float (&v)[8], float& m, float& l, float (&acc)[8]) {
+    const float nm = fmaxf(m, sc);
+    const float cm = __expf(m - nm), e = __expf(sc - nm);
+    l = l * cm + e;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * cm + e * v[i];
+    m = nm;
+  };
+  constexpr int U = 4;
+  for (int p = k0 + gi; p < k1; p += 16 * U) {
+    uint4 kw[U], vw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int pu = min(p + 16 * u, k1 - 1);
+      kw[u] = *reinterpret_cast<const uint4*>(k_cache + base + (size_t)pu * D);
+      vw[u] = *reinterpret_cast<const uint4*>(v_cache + base + (size_t)pu * D);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[8], vf[8];
+      unpack8(kw[u], kf);
+      unpack8(vw[u], vf);
+      float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
+      d0 = row16_sum(d0) * ATT_SCALE;
+      d1 = row16_sum(d1) * ATT_SCALE;
+      if (p + 16 * u < k1) {
+        step(d0, vf, m0, l0, a0);
+        step(d1, vf, m1, l1, a1);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { gacc[gi][0][8 * t + i] = a0[i]; gacc[gi][1][8 * t + i] = a1[i]; }
+  if (t == 0) { gml[gi][0][0] = m0; gml[gi][0][1] = l0; gml[gi][1][0] = m1; gml[gi][1][1] = l1; }
+  __syncthreads();
+  const int h = tid >> 7, d = tid & 127;
+  float M = -INFINITY;
+  for (int q = 0; q < 16; ++q) M = fmaxf(M, gml[q][h][0]);  // finite: the split has a key
+  float A = 0.f, Ls = 0.f;
+  for (int q = 0; q < 16; ++q) {
+    const float f = __expf(gml[q][h][0] - M);  // 0 for a group without keys
+    A = fmaf(gacc[q][h][d], f, A);
+    Ls = fmaf(gml[q][h][1], f, Ls);
+  }
+  float* o = part + ((((size_t)b * HKV + kvh) * S + s) * 2 + h) * APW;
+  o[d] = A;
+  if (d == 0) { o[D] = M; o[D + 1] = Ls; }
+}
+
+// Merge of the splits of each sequence and query head into the O-projection's input row (bf16 hi/lo
+// [B][2048]); 128 threads, one per dim.
+__global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int S, const int32_t* positions,
+                                                          int max_seq, uint16_t* oh, uint16_t* ol, int ldo) {
+  const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int kvh = h >> 1, hh = h & 1;
+  const int ns = (seq_pos(positions, b, max_seq, nullptr) + KS) / KS;  // ceil((pos + 1) / KS)
+  const float* p = part + (((size_t)b * HKV + kvh) * S * 2 + hh) * APW;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, p[(size_t)s * 2 * APW + D]);
+  float A = 0.f, Ls = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float* q = p + (size_t)s * 2 * APW;
+    const float f = __expf(q[D] - M);
+    A = fmaf(q[d], f, A);
+    Ls = fmaf(q[D + 1], f, Ls);
+  }
+  const float o = A / Ls;
+  const uint16_t hi = f32_to_bf16(o);
+  oh[(size_t)b * ldo + h * D + d] = hi;
+  ol[(size_t)b * ldo + h * D + d] = f32_to_bf16(o - bf16_to_f32(hi));
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -776,4 +1094,149 @@ extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* token
                          (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
                          (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
                          (uint16_t*)v_cache, max_seq_len, logits, out_token, wk, stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched decode, host side
+// ------------------------------------------------------------------------------------------------
+namespace mkp {
+
+// Split-K factors of the O and down products (each wave's K range a multiple of 256)
+template <int H, int I>
+struct BatchPlan {
+  static constexpr int SO = H == 1024 ? 2 : 2;  // O: K = 2048
+  static constexpr int SD = H == 1024 ? 3 : 2;  // down: K = I
+  static constexpr int SP = SO > SD ? SO : SD;
+  static_assert((HQ * D / SO / 4) % 256 == 0 && (I / SD / 4) % 256 == 0 && (H / 4) % 256 == 0 && (H / 2) % 256 == 0,
+                "wave K ranges must be multiples of 256");
+};
+
+struct BLayout {
+  size_t x, ah, al, bh, bl, raw, qh, ql, part, apart, keys, bad, bytes;
+};
+static BLayout blayout(int H, int I, int B, int max_seq) {
+  const size_t A = H > HQ * D ? H : HQ * D;
+  const int S = (max_seq + KS - 1) / KS;
+  BLayout L;
+  size_t o = 0;
+  auto take = [&](size_t n) { const size_t r = o; o += align256(n); return r; };
+  L.x = take((size_t)B * H * 4);
+  L.ah = take((size_t)B * A * 2);
+  L.al = take((size_t)B * A * 2);
+  L.bh = take((size_t)B * I * 2);
+  L.bl = take((size_t)B * I * 2);
+  L.raw = take((size_t)B * (HQ + 2 * HKV) * D * 4);
+  L.qh = take((size_t)B * HQ * D * 2);
+  L.ql = take((size_t)B * HQ * D * 2);
+  L.part = take((size_t)3 * B * H * 4);
+  L.apart = take((size_t)B * HKV * S * 2 * APW * 4);
+  L.keys = take(LM_MAXR * 8);
+  L.bad = take(4);
+  L.bytes = o;
+  return L;
+}
+
+template <int H, int I>
+static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tokens, const int32_t* positions,
+                            const uint16_t* embed, const uint16_t* lm_head, const uint16_t* final_norm,
+                            const mk_layer_weights* layers, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                            uint16_t* k_cache, uint16_t* v_cache, int max_seq, float* logits, int32_t* out_tokens,
+                            char* ws, const BLayout& Lo, hipStream_t st) {
+  typedef BatchPlan<H, I> BP;
+  const int A = H > HQ * D ? H : HQ * D;
+  const int S = (max_seq + KS - 1) / KS;
+  float* x = reinterpret_cast<float*>(ws + Lo.x);
+  uint16_t* ah = reinterpret_cast<uint16_t*>(ws + Lo.ah);
+  uint16_t* al = reinterpret_cast<uint16_t*>(ws + Lo.al);
+  uint16_t* bh = reinterpret_cast<uint16_t*>(ws + Lo.bh);
+  uint16_t* bl = reinterpret_cast<uint16_t*>(ws + Lo.bl);
+  float* raw = reinterpret_cast<float*>(ws + Lo.raw);
+  uint16_t* qh = reinterpret_cast<uint16_t*>(ws + Lo.qh);
+  uint16_t* ql = reinterpret_cast<uint16_t*>(ws + Lo.ql);
+  float* part = reinterpret_cast<float*>(ws + Lo.part);
+  float* apart = reinterpret_cast<float*>(ws + Lo.apart);
+  u64* keys = reinterpret_cast<u64*>(ws + Lo.keys);
+  int32_t* bad = reinterpret_cast<int32_t*>(ws + Lo.bad);
+  const int L = dims.num_layers;
+  hipError_t e;
+#define MKB_LAUNCH(...)                                   \
+  do {                                                    \
+    hipLaunchKernelGGL(__VA_ARGS__);                      \
+    if ((e = hipGetLastError()) != hipSuccess) return e;  \
+  } while (0)
+  MKB_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, keys, bad);
+  const dim3 rows((B + 3) / 4);
+  for (int l = 0; l < L; ++l) {
+    const mk_layer_weights& lw = layers[l];
+    // x (embedding, or + the previous layer's down partials) -> input norm
+    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, l == 0 ? tokens : nullptr, embed, dims.vocab, bad,
+               part, l == 0 ? 0 : BP::SD, (const uint16_t*)lw.norm_weight, ah, al, A, B);
+    SkArgs q{};
+    q.xh = ah; q.xl = al; q.ldx = A; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
+    q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
+    q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
+    MKB_LAUNCH(skinny_kernel<SK_RAW>, dim3(q.N / 16, 1), dim3(256), 0, st, q);
+    MKB_LAUNCH(qkv_post_kernel, dim3((B * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, raw, B, positions,
+               (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, qh, ql, k_cache,
+               v_cache, L, l, max_seq, bad);
+    MKB_LAUNCH(battn_partial_kernel, dim3(S, HKV, B), dim3(256), 0, st, qh, ql, k_cache, v_cache, positions, L, l,
+               max_seq, apart, S);
+    MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
+    SkArgs o{};
+    o.xh = ah; o.xl = al; o.ldx = A; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
+    MKB_LAUNCH(skinny_kernel<SK_PART>, dim3(H / 16, BP::SO), dim3(256), 0, st, o);
+    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SO,
+               (const uint16_t*)lw.post_attn_norm_weight, ah, al, A, B);
+    SkArgs u{};
+    u.xh = ah; u.xl = al; u.ldx = A; u.B = B; u.N = I; u.K = H;
+    u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bh; u.ml = bl; u.ldm = I;
+    MKB_LAUNCH(skinny_kernel<SK_SILU>, dim3(I / 16, 1), dim3(256), 0, st, u);
+    SkArgs dn{};
+    dn.xh = bh; dn.xl = bl; dn.ldx = I; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
+    dn.out = part;
+    MKB_LAUNCH(skinny_kernel<SK_PART>, dim3(H / 16, BP::SD), dim3(256), 0, st, dn);
+  }
+  // the last layer's down partials, then the final norm and LM head over all B rows
+  MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, nullptr,
+             nullptr, nullptr, A, B);
+  MKB_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, x, 0, B, final_norm, lm_head, dims.vocab, logits, keys,
+             bad);
+  if (out_tokens) MKB_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, keys, B, bad, out_tokens);
+#undef MKB_LAUNCH
+  return hipSuccess;
+}
+
+}  // namespace mkp
+
+extern "C" size_t mk_decode_batch_workspace_bytes(const mk_model_dims* dims, int batch, int max_seq_len) {
+  if (!dims || batch < 1 || batch > BMAX || max_seq_len < 1) return 0;
+  return blayout(dims->hidden, dims->intermediate, batch, max_seq_len).bytes;
+}
+
+extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens,
+                                      const int32_t* positions, const void* embed_weight, const void* lm_head_weight,
+                                      const void* final_norm_weight, const void* layer_weights, const void* cos_table,
+                                      const void* sin_table, void* k_cache, void* v_cache, int max_seq_len,
+                                      float* logits, int32_t* out_tokens, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+  if (!dims || !tokens || !positions || !embed_weight || !lm_head_weight || !final_norm_weight || !layer_weights ||
+      !cos_table || !sin_table || !k_cache || !v_cache || !logits || !workspace)
+    return hipErrorInvalidValue;
+  const bool s06 = dims->hidden == 1024 && dims->intermediate == 3072;
+  const bool s17 = dims->hidden == 2048 && dims->intermediate == 6144;
+  if (!(s06 || s17) || dims->num_layers < 1 || dims->vocab < 1) return hipErrorInvalidValue;
+  if (batch < 1 || batch > BMAX || max_seq_len < 1) return hipErrorInvalidValue;
+  const BLayout Lo = blayout(dims->hidden, dims->intermediate, batch, max_seq_len);
+  if (workspace_bytes < Lo.bytes || reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return hipErrorInvalidValue;
+  const mk_layer_weights* lw = static_cast<const mk_layer_weights*>(layer_weights);  // host array
+  char* ws = static_cast<char*>(workspace);
+  if (s06)
+    return run_batch<1024, 3072>(*dims, batch, tokens, positions, (const uint16_t*)embed_weight,
+                                 (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
+                                 (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
+                                 (uint16_t*)v_cache, max_seq_len, logits, out_tokens, ws, Lo, stream);
+  return run_batch<2048, 6144>(*dims, batch, tokens, positions, (const uint16_t*)embed_weight,
+                               (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
+                               (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
+                               (uint16_t*)v_cache, max_seq_len, logits, out_tokens, ws, Lo, stream);
 }

@@ -296,6 +296,42 @@ std::tuple<torch::Tensor, torch::Tensor> prefill(torch::Tensor tokens, torch::Te
   return {logits, tok};
 }
 
+// Batched decode (mk_decode_batch): B sequences, tokens and positions int32 [B] on the weights' device,
+// caches bf16 [B, L, 8, max_seq, 128]; returns (fp32 logits [B, V], int32 greedy tokens [B] on the
+// device).
+std::tuple<torch::Tensor, torch::Tensor> decode_batch(torch::Tensor tokens, torch::Tensor positions, torch::Tensor embed,
+                                                      torch::Tensor lm_head, torch::Tensor final_norm,
+                                                      std::vector<torch::Tensor> lw, torch::Tensor cos, torch::Tensor sin,
+                                                      torch::Tensor kc, torch::Tensor vc, int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, 0, max_seq_len, true, true);
+  TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
+                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) >= 1 && tokens.size(0) <= 8,
+              "megakernel: tokens must be a contiguous int32 [B] tensor (1 <= B <= 8) on ", c.dev);
+  const int64_t B = tokens.size(0);
+  TORCH_CHECK(positions.defined() && positions.device() == c.dev && positions.scalar_type() == torch::kInt32 &&
+                  positions.is_contiguous() && positions.dim() == 1 && positions.size(0) == B,
+              "megakernel: positions must be a contiguous int32 [B] tensor on ", c.dev);
+  check_bf16(kc, "k_cache", {B, c.dims.num_layers, kKVHeads, max_seq_len, kHeadDim}, c.dev);
+  check_bf16(vc, "v_cache", {B, c.dims.num_layers, kKVHeads, max_seq_len, kHeadDim}, c.dev);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.dev);
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(c.dev.index()).stream();
+  std::vector<mk_layer_weights> table(c.dims.num_layers);
+  for (int64_t l = 0; l < c.dims.num_layers; ++l) {
+    const torch::Tensor* t = &lw[l * kPerLayer];
+    table[l] = {t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), t[3].data_ptr(), t[4].data_ptr(), t[5].data_ptr(),
+                t[6].data_ptr(), t[7].data_ptr(), t[8].data_ptr(), t[9].data_ptr(), t[10].data_ptr()};
+  }
+  const size_t bytes = mk_decode_batch_workspace_bytes(&c.dims, (int)B, (int)max_seq_len);
+  auto ws = torch::empty({(int64_t)bytes}, embed.options().dtype(torch::kUInt8));
+  auto logits = torch::empty({B, c.dims.vocab}, embed.options().dtype(torch::kFloat32));
+  auto toks = torch::empty({B}, embed.options().dtype(torch::kInt32));
+  MK_HIP_CHECK(mk_decode_batch(&c.dims, (int)B, tokens.data_ptr<int32_t>(), positions.data_ptr<int32_t>(),
+                               embed.data_ptr(), lm_head.data_ptr(), final_norm.data_ptr(), table.data(), cos.data_ptr(),
+                               sin.data_ptr(), kc.data_ptr(), vc.data_ptr(), (int)max_seq_len, logits.data_ptr<float>(),
+                               toks.data_ptr<int32_t>(), ws.data_ptr(), bytes, stream));
+  return {logits, toks};
+}
+
 int64_t status() {
   uint32_t s = 0;
   MK_HIP_CHECK(mk_status(&s));
@@ -338,6 +374,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("prefill", &prefill,
         "batched prefill of int32 tokens [n] at positions position..position+n-1 into the [L, 8, max_seq, 128] "
         "caches; returns (fp32 logits of the last token, int32 greedy token on device)");
+  m.def("decode_batch", &decode_batch,
+        "batched decode of B <= 8 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
+        "returns (fp32 logits [B, V], int32 greedy tokens [B] on device)");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
   m.def("reset", &reset, "clear the decode workspaces (exchange words, status words) and restart their launch sequences; synchronizes");

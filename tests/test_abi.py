@@ -252,3 +252,37 @@ def test_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
     assert call(nbytes=n1 - 1) == HIP_ERROR_INVALID_VALUE
     assert call(workspace=vp(256 + 16)) == HIP_ERROR_INVALID_VALUE  # not 256-byte aligned
     assert call(workspace=None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
+    """``mk_decode_batch`` checks the batch size (1..8), shape, workspace size and alignment before any
+    HIP call; ``mk_decode_batch_workspace_bytes`` is 0 for an unsupported batch."""
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                    ("num_layers", ctypes.c_int32), ("vocab", ctypes.c_int32)]
+
+    ws = lib.mk_decode_batch_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.POINTER(Dims), i32, i32]
+    good = Dims(1024, 3072, 28, 151936)
+    assert ws(ctypes.byref(good), 0, 512) == 0 and ws(ctypes.byref(good), 9, 512) == 0
+    n8 = ws(ctypes.byref(good), 8, 4096)
+    assert n8 > ws(ctypes.byref(good), 1, 512) > 0 and n8 % 256 == 0
+
+    f = lib.mk_decode_batch
+    f.restype = i32
+    f.argtypes = [ctypes.POINTER(Dims), i32, vp, vp] + [vp] * 8 + [i32, vp, vp, vp, ctypes.c_size_t, vp]
+    d = vp(256)
+
+    def call(dims=good, batch=4, max_seq=512, workspace=d, nbytes=None):
+        nb = ws(ctypes.byref(dims), batch, max_seq) if nbytes is None else nbytes
+        return f(ctypes.byref(dims), batch, d, d, *([d] * 8), max_seq, d, None, workspace, nb, None)
+
+    assert call(batch=0) == HIP_ERROR_INVALID_VALUE
+    assert call(batch=9) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(2048, 3072, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE
+    assert call(workspace=vp(256 + 64)) == HIP_ERROR_INVALID_VALUE
+    assert call(workspace=None) == HIP_ERROR_INVALID_VALUE

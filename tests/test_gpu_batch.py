@@ -1,0 +1,138 @@
+"""GPU parity tests of the batched decode (``decode_batch``, C ABI ``mk_decode_batch``): B sequences of
+different lengths advance one token each per call, each against its own cache.
+
+Per sequence, every step is checked against the fp32 restatement (``restate.decode_step``) run on the
+cache the kernel has written for that sequence -- the same tight check as the single-sequence
+decode (max-abs 5e-3, same greedy token, the new K/V rows within one bf16 rounding step) -- and, at
+the full 0.6B shape, against the single-sequence decode kernel on the same inputs."""
+import pytest
+import torch
+
+from oracle import hf, restate
+from tests.gpu_common import DEV, Session, stats
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mini():
+    return Session("mini", 512)
+
+
+@pytest.fixture(scope="module")
+def mini17():
+    return Session("mini-1.7b", 512)
+
+
+def _batched_cache(sess, prompts):
+    """Oracle prefill of each prompt into its slot of a [B, L, 8, max_seq, 128] cache (CPU), and each
+    prompt's greedy next token."""
+    ks, vs, first = [], [], []
+    for ids in prompts:
+        lg, k, v = restate.prefill(sess.W, ids, sess.cos_cpu, sess.sin_cpu, sess.max_seq)
+        ks.append(k)
+        vs.append(v)
+        first.append(restate.argmax_bf16(lg))
+    return torch.stack(ks), torch.stack(vs), first
+
+
+def _decode_batch(sess, toks, pos, kd, vd):
+    t = torch.tensor(toks, dtype=torch.int32, device=DEV)
+    p = torch.tensor(pos, dtype=torch.int32, device=DEV)
+    return sess.kernel.decode_batch(t, p, sess.embed, sess.lm_head, sess.final_norm, sess.layers, sess.cos, sess.sin,
+                                    kd, vd, sess.max_seq)
+
+
+@pytest.mark.parametrize("shape_fixture, lengths, steps", [
+    ("mini", (5, 40, 100, 300), 6),
+    ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4),
+    ("mini17", (33, 200, 90), 4),
+])
+def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, request):
+    """Sequences of different lengths in one batch (so their attention spans 1 to 2 key splits of
+    256, and a sequence ends a split exactly at 256): every step, each sequence's logits and greedy
+    token against the restatement on the kernel's cache for that sequence, and its new K/V rows."""
+    sess = request.getfixturevalue(shape_fixture)
+    prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
+    kc, vc, toks = _batched_cache(sess, prompts)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    pos = list(lengths)
+    B = len(lengths)
+    worst = 0.0
+    for t in range(steps):
+        before_k, before_v = kd.cpu(), vd.cpu()
+        logits, dev_toks = _decode_batch(sess, toks, pos, kd, vd)
+        logits, dev_toks = logits.cpu(), dev_toks.cpu().tolist()
+        for b in range(B):
+            want = sess.oracle_step(before_k[b], before_v[b], toks[b], pos[b])
+            maxabs, cos = stats(logits[b], want)
+            worst = max(worst, maxabs)
+            assert maxabs < 5e-3 and cos > 0.999999, (t, b, maxabs, cos)
+            assert dev_toks[b] == restate.argmax_bf16(logits[b]) == restate.argmax_bf16(want), (t, b)
+            for got_c, ref_c in ((kd, before_k), (vd, before_v)):
+                row = got_c[b, :, :, pos[b]].float().cpu()
+                d = (row - ref_c[b, :, :, pos[b]].float()).abs().max().item()
+                assert d <= 2 ** -6 * max(1.0, ref_c[b, :, :, pos[b]].float().abs().max().item()), (t, b, d)
+        # nothing but the new rows changed
+        changed = ((kd.cpu() != before_k).any(-1)).nonzero().tolist()
+        assert sorted({(c[0], c[3]) for c in changed}) <= sorted({(b, pos[b]) for b in range(B)})
+        toks = dev_toks
+        pos = [p + 1 for p in pos]
+    print(f"[batch {shape_fixture} B={B}] {steps} steps, every sequence matches the restatement, "
+          f"max|d| {worst:.3e}", flush=True)
+
+
+def test_batch_agrees_with_single_sequence_decode_at_0_6b():
+    """The full Qwen3-0.6B shape, 8 sequences of lengths 32..480: each sequence's batched logits and
+    token against the single-sequence decode kernel on an identical cache, for 6 steps (both are
+    fp32-accurate, so they agree to the restatement tolerance), and against the restatement on the
+    first step. Prints the batched step time."""
+    sess = Session("qwen3-0.6b", 512)
+    lengths = (32, 64, 100, 150, 200, 256, 300, 480)
+    B = len(lengths)
+    prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=20 + i)[0].tolist() for i, n in enumerate(lengths)]
+    kc, vc, toks = _batched_cache(sess, prompts)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    singles = [(kc[b].to(DEV), vc[b].to(DEV)) for b in range(B)]
+    pos = list(lengths)
+    for t in range(6):
+        if t == 0:
+            want0 = [sess.oracle_step(kc[b].clone(), vc[b].clone(), toks[b], pos[b]) for b in range(B)]
+        logits, dev_toks = _decode_batch(sess, toks, pos, kd, vd)
+        logits, dev_toks = logits.cpu(), dev_toks.cpu().tolist()
+        for b in range(B):
+            ls, ts = sess.decode(toks[b], singles[b][0], singles[b][1], pos[b], greedy=True)
+            maxabs, _ = stats(logits[b], ls.cpu())
+            assert maxabs < 5e-3, (t, b, maxabs)
+            assert dev_toks[b] == int(ts.item()), (t, b)
+            if t == 0:
+                assert stats(logits[b], want0[b])[0] < 5e-3
+        toks = dev_toks
+        pos = [p + 1 for p in pos]
+    # timing: 20 batched steps (tokens and positions held, so the same work each step)
+    tt = torch.tensor(toks, dtype=torch.int32, device=DEV)
+    pp = torch.tensor(pos, dtype=torch.int32, device=DEV)
+    args = (tt, pp, sess.embed, sess.lm_head, sess.final_norm, sess.layers, sess.cos, sess.sin, kd, vd, sess.max_seq)
+    for _ in range(3):
+        sess.kernel.decode_batch(*args)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(20):
+        sess.kernel.decode_batch(*args)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / 20
+    print(f"[batch qwen3-0.6b B={B}] {ms * 1e3:.0f} us per batched step, {B / ms * 1e3:.0f} tokens/s", flush=True)
+    assert sess.kernel.status() == 0
+
+
+def test_batch_bad_position_is_reported_in_band(mini):
+    """A position outside [0, max_seq) cannot be checked on the host without a copy: the call reports
+    NaN logits and token -1 for every sequence, and accesses stay inside the cache."""
+    kd = torch.zeros(2, mini.shape.layers, 8, mini.max_seq, 128, dtype=torch.bfloat16, device=DEV)
+    vd = torch.zeros_like(kd)
+    logits, toks = _decode_batch(mini, [3, 4], [10, mini.max_seq + 7], kd, vd)
+    assert torch.isnan(logits).all() and toks.tolist() == [-1, -1]
+    logits, toks = _decode_batch(mini, [3, 4], [10, 11], kd, vd)
+    assert torch.isfinite(logits).all() and min(toks.tolist()) >= 0
