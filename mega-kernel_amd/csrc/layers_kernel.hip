@@ -360,23 +360,31 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Causal attention of the prompt rows (/root/reference/megakernel.cu:228-370 for one query; here a
-// block of 64 queries of one head per workgroup, flash-style over blocks of 64 keys). Query row m
-// sits at position `position + m` and attends keys [0, position + m] of the cache, which already
-// holds this layer's new rows (written by the QKV epilogue). Wave w owns queries 16w..16w+15 of
-// the block.
+// Causal attention of the prompt rows (/root/reference/megakernel.cu:228-370 for one query; here
+// flash-style over blocks of 64 keys). Query row m sits at position `position + m` and attends keys
+// [0, position + m] of the cache, which already holds this layer's new rows (written by the QKV
+// epilogue).
+//   Work split: a workgroup (8 waves) takes one K/V head and a pair of 64-query blocks, i and
+//   nqb - 1 - i, one after the other, so that every workgroup does the same causal work. Waves 0-3
+//   take query head 2 kvh, waves 4-7 head 2 kvh + 1, 16 queries each: the two heads of a GQA pair
+//   share each K/V block staged in LDS.
+//   Pipeline: the next K/V block is loaded into registers while the current one is multiplied,
+//   then written into the other half of a double-buffered LDS tile; one barrier per block.
 //   S^T = K . Q^T on the matrix cores (keys as rows): lane l holds the scores of query i = l % 16
 //         against keys 16 mb + 4 g + j -- so each query's row statistics (max, sum) are a
 //         reduction over registers and the 4 lanes i, i+16, i+32, i+48;
 //   O  += P . V: the A operand (8 keys of query i per lane) is exactly what a lane holds of two
 //         consecutive S^T blocks, with key slot 8g + jj meaning key 4g + jj (jj < 4) or
 //         16 + 4g + jj - 4; V is staged transposed in LDS ([dim][key]) so that the B operand
-//         (those 8 keys at one dim) is two 8-byte reads.
-// Output rows (normalised) as the bf16 hi/lo pair the O-projection GEMM takes, [M][16 * 128].
+//         (those 8 keys at one dim) is two 8-byte reads. The transpose is written as 32-bit words
+//         (two consecutive keys of one dim), bank-conflict free.
+// Output rows (normalised) as the bf16 hi/lo pair the O-projection GEMM takes, [M][16 * 128],
+// staged through LDS so that every global store is 16 bytes.
 // ------------------------------------------------------------------------------------------------
 constexpr int QB = 64, KB = 64;
 constexpr int KSP = D + 8;   // padded K row in LDS (272 B)
-constexpr int VSP = KB + 8;  // padded V^T row (144 B)
+constexpr int VSP = KB + 8;  // padded V^T row (144 B = 36 banks: rows 8 apart sit 32 banks apart)
+constexpr int OSP = D + 8;   // padded output staging row
 
 struct AttnArgs {
   const uint16_t* qh;
@@ -389,143 +397,186 @@ struct AttnArgs {
   int M, layer, position, max_seq;
 };
 
-__global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[KB][KSP];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[D][VSP];
+struct AttnSmem {
+  union {
+    struct {
+      uint16_t ks[2][KB][KSP];
+      uint16_t vt[2][D][VSP];
+    } kv;
+    uint16_t o[8][2][16][OSP];  // per wave: hi, lo of its 16 output rows
+  };
+};
+
+__global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) AttnSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y, kvh = h >> 1;
-  const int q0 = blockIdx.x * QB;                       // first query row of the block
-  const int qrow = q0 + 16 * w + li;                    // this lane's query (score layout)
-  const int qpos = a.position + qrow;
-  const int last = a.position + min(a.M, q0 + QB) - 1;  // last position any query of the block sees
-  const int nkb = last / KB + 1;
+  const int kvh = blockIdx.y, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
+  const int nqb = (a.M + QB - 1) / QB;
   const size_t kvbase = ((size_t)a.layer * HKV + kvh) * a.max_seq * D;
+  // staging roles: K chunk c = tid + 512 r (key c / 16, dims 8 (c % 16)); V: keys 2 vp, 2 vp + 1 at
+  // dims 8 vc .. +7 (lanes of a wave span 32 key pairs and two chunks: conflict-free 32-bit writes)
+  const int vp = lane & 31, vc = 2 * w + (lane >> 5);
 
-  // this lane's query fragments (B operand of S^T = K . Q^T): dims 32 s + 8 g .. +7, hi and lo
-  uint4 fq[2][4];
-  {
-    const int qr = min(qrow, a.M - 1);
-    const size_t o = (size_t)qr * (HQ * D) + h * D + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      fq[0][s] = *reinterpret_cast<const uint4*>(a.qh + o + 32 * s);
-      fq[1][s] = *reinterpret_cast<const uint4*>(a.ql + o + 32 * s);
-    }
-  }
-  f32x4 acc[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mrun = -INFINITY, lrun = 0.f;  // running max and sum of query qrow (replicated on its 4 lanes)
+  for (int pass = 0; pass < 2; ++pass) {
+    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
+    if (pass == 1 && qb <= (int)blockIdx.x) break;  // odd nqb: the middle block runs once
+    const int q0 = qb * QB;
+    const int qrow = q0 + wq + li;                       // this lane's query (score layout)
+    const int qpos = a.position + qrow;
+    const int wlast = a.position + q0 + wq + 15;         // last position any query of this wave has
+    const int last = a.position + min(a.M, q0 + QB) - 1;  // last key any query of the block sees
+    const int nkb = last / KB + 1;
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int kp0 = kb * KB;
-    __syncthreads();  // the previous block's tiles are consumed
-    // K rows -> ks[key][dim]; V rows -> vt[dim][key]; keys past `last` are zero
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, key = c >> 4, ch = c & 15;
-      const int kp = kp0 + key;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (kp <= last) {
-        kv = *reinterpret_cast<const uint4*>(a.k_cache + kvbase + (size_t)kp * D + 8 * ch);
-        vv = *reinterpret_cast<const uint4*>(a.v_cache + kvbase + (size_t)kp * D + 8 * ch);
-      }
-      *reinterpret_cast<uint4*>(&ks[key][8 * ch]) = kv;
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        vt[8 * ch + 2 * q][key] = (uint16_t)(vw[q] & 0xFFFFu);
-        vt[8 * ch + 2 * q + 1][key] = (uint16_t)(vw[q] >> 16);
-      }
-    }
-    __syncthreads();
-
-    // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
-    f32x4 st[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    // this lane's query fragments (B operand of S^T = K . Q^T): dims 32 s + 8 g .. +7, hi and lo
+    uint4 fq[2][4];
+    {
+      const int qr = min(qrow, a.M - 1);
+      const size_t o = (size_t)qr * (HQ * D) + h * D + 8 * lg;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint4 fk = *reinterpret_cast<const uint4*>(&ks[16 * mb + li][32 * s + 8 * lg]);
-        c = mfma(fk, fq[0][s], c);
-        c = mfma(fk, fq[1][s], c);
+        fq[0][s] = *reinterpret_cast<const uint4*>(a.qh + o + 32 * s);
+        fq[1][s] = *reinterpret_cast<const uint4*>(a.ql + o + 32 * s);
       }
-      st[mb] = c;
     }
-    // causal mask and scale; block maximum of this lane's query
-    float bmax = -INFINITY;
+    f32x4 acc[8];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrun = -INFINITY, lrun = 0.f;  // running max and sum of query qrow (replicated on its 4 lanes)
+
+    uint4 pk[2], pv[2];  // the next block's K chunks and V rows, in flight during the current block
+    auto load_block = [&](int kb) {
+      const int kp0 = kb * KB;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kp = kp0 + 16 * mb + 4 * lg + j;
-        const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
-        st[mb][j] = sv;
-        bmax = fmaxf(bmax, sv);
+      for (int r = 0; r < 2; ++r) {
+        const int c = tid + 512 * r, kp = kp0 + (c >> 4);
+        pk[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.k_cache + kvbase + (size_t)kp * D + 8 * (c & 15))
+                           : make_uint4(0, 0, 0, 0);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
-    const float alpha = __expf(mrun - mnew);
-    float psum = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = __expf(st[mb][j] - mnew);
-        st[mb][j] = p;
-        psum += p;
+      for (int r = 0; r < 2; ++r) {
+        const int kp = kp0 + 2 * vp + r;
+        pv[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.v_cache + kvbase + (size_t)kp * D + 8 * vc)
+                           : make_uint4(0, 0, 0, 0);
       }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
-    lrun = lrun * alpha + psum;
-    mrun = mnew;
-    // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits in
-    // lane 4g + j (and its copies)
-    float ar[4];
+    };
+    auto store_block = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+      for (int r = 0; r < 2; ++r) {
+        const int c = tid + 512 * r;
+        *reinterpret_cast<uint4*>(&sm.kv.ks[buf][c >> 4][8 * (c & 15)]) = pk[r];
+      }
+      const uint32_t x0[4] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w};
+      const uint32_t x1[4] = {pv[1].x, pv[1].y, pv[1].z, pv[1].w};
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
+      for (int q = 0; q < 4; ++q) {
+        uint32_t* lo = reinterpret_cast<uint32_t*>(&sm.kv.vt[buf][8 * vc + 2 * q][2 * vp]);
+        uint32_t* hi = reinterpret_cast<uint32_t*>(&sm.kv.vt[buf][8 * vc + 2 * q + 1][2 * vp]);
+        *lo = (x0[q] & 0xFFFFu) | (x1[q] << 16);
+        *hi = (x0[q] >> 16) | (x1[q] & 0xFFFF0000u);
+      }
+    };
+
+    if (pass == 1) __syncthreads();  // the first pass's output staging (which aliases the tiles) is read
+    load_block(0);
+    store_block(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int kp0 = kb * KB, buf = kb & 1;
+      if (kb + 1 < nkb) load_block(kb + 1);
+      if (kp0 <= wlast) {  // a block entirely after this wave's queries adds nothing
+        // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
+        f32x4 st[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
-    // O += P . V over two 32-key steps
+        for (int mb = 0; mb < 4; ++mb) {
+          f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float pv[8];
+          for (int s = 0; s < 4; ++s) {
+            const uint4 fk = *reinterpret_cast<const uint4*>(&sm.kv.ks[buf][16 * mb + li][32 * s + 8 * lg]);
+            c = mfma(fk, fq[0][s], c);
+            c = mfma(fk, fq[1][s], c);
+          }
+          st[mb] = c;
+        }
+        // causal mask and scale; block maximum of this lane's query
+        float bmax = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { pv[j] = st[2 * t][j]; pv[4 + j] = st[2 * t + 1][j]; }
-      uint4 ph, pl;
-      split8(pv, ph, pl);
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int kp = kp0 + 16 * mb + 4 * lg + j;
+            const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
+            st[mb][j] = sv;
+            bmax = fmaxf(bmax, sv);
+          }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
+        const float alpha = __expf(mrun - mnew);
+        float psum = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p = __expf(st[mb][j] - mnew);
+            st[mb][j] = p;
+            psum += p;
+          }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        lrun = lrun * alpha + psum;
+        mrun = mnew;
+        // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits
+        // in lane 4g + j (and its copies)
+        float ar[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
+        // O += P . V over two 32-key steps
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          float pw[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) { pw[j] = st[2 * t][j]; pw[4 + j] = st[2 * t + 1][j]; }
+          uint4 ph, pl;
+          split8(pw, ph, pl);
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb) {
+            const uint16_t* vr = &sm.kv.vt[buf][16 * nb + li][32 * t + 4 * lg];
+            const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
+            const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
+            const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+            acc[nb] = mfma(ph, fv, acc[nb]);
+            acc[nb] = mfma(pl, fv, acc[nb]);
+          }
+        }
+      }
+      if (kb + 1 < nkb) store_block(buf ^ 1);
+      __syncthreads();  // block kb consumed by every wave; block kb + 1 staged
+    }
+    // normalise by each row's sum (query 4g + j's, from lane 4g + j), stage this wave's 16 rows as
+    // hi/lo in LDS (the tiles are free after the loop's last barrier), then store 16-byte chunks
+    float linv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) linv[j] = 1.f / __shfl(lrun, 4 * lg + j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) {
-        const uint16_t* vr = &vt[16 * nb + li][32 * t + 4 * lg];
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
-        const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
-        acc[nb] = mfma(ph, fv, acc[nb]);
-        acc[nb] = mfma(pl, fv, acc[nb]);
+        const float o = acc[nb][j] * linv[j];
+        const uint16_t hi = f32_to_bf16(o);
+        sm.o[w][0][4 * lg + j][16 * nb + li] = hi;
+        sm.o[w][1][4 * lg + j][16 * nb + li] = f32_to_bf16(o - bf16_to_f32(hi));
       }
-    }
-  }
-  // normalise by each row's sum (query 4g + j's, from lane 4g + j) and write hi/lo
-  float linv[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) linv[j] = 1.f / __shfl(lrun, 4 * lg + j);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = q0 + 16 * w + 4 * lg + j;
-    if (m >= a.M) continue;
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const float o = acc[nb][j] * linv[j];
-      const uint16_t hi = f32_to_bf16(o);
-      const uint16_t lo = f32_to_bf16(o - bf16_to_f32(hi));
-      const size_t off = (size_t)m * a.ldo + h * D + 16 * nb + li;
-      a.oh[off] = hi;
-      a.ol[off] = lo;
+    for (int r = 0; r < 8; ++r) {  // 2 x 16 rows x 16 chunks = 512 chunks, 8 per lane
+      const int c = lane + 64 * r, part = c >> 8, row = (c >> 4) & 15, ch = c & 15;
+      const int m = q0 + wq + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(&sm.o[w][part][row][8 * ch]);
+      if (m < a.M) *reinterpret_cast<uint4*>((part ? a.ol : a.oh) + (size_t)m * a.ldo + h * D + 8 * ch) = v;
     }
   }
 }
@@ -1033,7 +1084,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     g.layer = l; g.position = position; g.max_seq = max_seq;
     MKP_LAUNCH(gemm_kernel<EPI_QKV>, dim3(g.N / NT, mtiles), dim3(256), 0, st, g);
     AttnArgs at{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, l, position, max_seq};
-    MKP_LAUNCH(attn_kernel, dim3((M + QB - 1) / QB, HQ), dim3(256), 0, st, at);
+    MKP_LAUNCH(attn_kernel, dim3(((M + QB - 1) / QB + 1) / 2, HKV), dim3(512), 0, st, at);
     GemmArgs go{};
     go.ah = wk.ah; go.al = wk.al; go.lda = A; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H;
