@@ -723,9 +723,14 @@ struct SkArgs {
 // A workgroup takes 16 weight rows (rows 16 bx ..). SK_RAW / SK_PART: its K range [by K / gy, ...)
 // split over the 4 waves; SK_SILU: 16 intermediates, gate rows on waves 0-1 and up rows on waves
 // 2-3, each pair splitting K in two. Each wave's K range is a multiple of 256 (checked on the host).
-template <int EPI>
+// The B operand holds CB column blocks of 8 rows of activations (a decode batch, or up to 64 prompt
+// tokens): column li of block cb is row 8 cb + li / 2, hi (even li) or lo (odd li). The weight
+// fragments of a K chunk stay in registers across the column blocks; the next block's activation
+// fragments are loaded while the current block is multiplied.
+template <int EPI, int CB>
 __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
-  __shared__ float red[4][16][BMAX + 1];
+  constexpr int NC = 8 * CB;
+  __shared__ float red[4][16][NC + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int n0 = 16 * blockIdx.x, n = n0 + li;
@@ -746,40 +751,59 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
     kb = blockIdx.y * kc + w * kw;
     ke = kb + kw;
   }
-  // B operand: column li is sequence li / 2, hi (even) or lo (odd)
   const int sb = li >> 1;
-  const bool live = sb < g.B;
-  const uint16_t* xs = (li & 1 ? g.xl : g.xh) + (size_t)(live ? sb : 0) * g.ldx;
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xs[CB];
+  bool live[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const int b = 8 * cb + sb;
+    live[cb] = b < g.B;
+    xs[cb] = (li & 1 ? g.xl : g.xh) + (size_t)(live[cb] ? b : 0) * g.ldx + 8 * lg;
+  }
+  f32x4 c[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) c[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int k0 = kb; k0 < ke; k0 += 256) {
     uint4 wa[8], xb[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       wa[u] = ld_stream(reinterpret_cast<const uint4*>(wrow + k0 + 32 * u + 8 * lg));
-      xb[u] = live ? *reinterpret_cast<const uint4*>(xs + k0 + 32 * u + 8 * lg) : make_uint4(0, 0, 0, 0);
+      xb[u] = live[0] ? *reinterpret_cast<const uint4*>(xs[0] + k0 + 32 * u) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) c = mfma(wa[u], xb[u], c);
-  }
-  // C[row 4 lg + j][column li]: sequence li / 2 is the sum of its hi and lo columns
+    for (int cb = 0; cb < CB; ++cb) {
+      uint4 xn[8];
+      if (cb + 1 < CB) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float v = c[j] + __shfl_xor(c[j], 1);
-    if (!(li & 1)) red[w][4 * lg + j][sb] = v;
+        for (int u = 0; u < 8; ++u)
+          xn[u] = live[cb + 1] ? *reinterpret_cast<const uint4*>(xs[cb + 1] + k0 + 32 * u) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[cb] = mfma(wa[u], xb[u], c[cb]);
+      if (cb + 1 < CB) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) xb[u] = xn[u];
+      }
+    }
   }
+  // C[row 4 lg + j][column li]: activation row 8 cb + li / 2 is the sum of its hi and lo columns
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = c[cb][j] + __shfl_xor(c[cb][j], 1);
+      if (!(li & 1)) red[w][4 * lg + j][8 * cb + sb] = v;
+    }
   __syncthreads();
-  if constexpr (EPI == SK_SILU) {
-    if (tid < 16 * g.B) {
-      const int r = tid / g.B, b = tid % g.B;
+  for (int idx = tid; idx < 16 * g.B; idx += 256) {
+    const int r = idx / g.B, b = idx % g.B;
+    if constexpr (EPI == SK_SILU) {
       const float gt = red[0][r][b] + red[1][r][b], up = red[2][r][b] + red[3][r][b];
       const float m = gt / (1.f + expf(-gt)) * up;
       const uint16_t hi = f32_to_bf16(m);
       g.mh[(size_t)b * g.ldm + n0 + r] = hi;
       g.ml[(size_t)b * g.ldm + n0 + r] = f32_to_bf16(m - bf16_to_f32(hi));
-    }
-  } else {
-    if (tid < 16 * g.B) {
-      const int r = tid / g.B, b = tid % g.B;
+    } else {
       const float v = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
       g.out[((size_t)blockIdx.y * g.B + b) * g.N + n0 + r] = v;
     }
@@ -852,10 +876,12 @@ __device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_
   return p;
 }
 
-// The raw Q/K/V sums of each sequence (fp32 [B][4096]): per-head RMSNorm + RoPE on q and k (one
-// wave per sequence and head, lane l holding dims l and l + 64, the RoPE pair), q kept as a bf16
-// hi/lo pair [B][2048], k and v rounded to bf16 into the sequence's cache at its position.
-__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, const int32_t* positions,
+// The raw Q/K/V sums of each row (fp32 [B][4096]): per-head RMSNorm + RoPE on q and k (one wave per
+// row and head, lane l holding dims l and l + 64, the RoPE pair), q kept as a bf16 hi/lo pair
+// [B][2048], k and v rounded to bf16 into the cache. With `positions`, row b is sequence b at
+// positions[b] of its own cache ([B][L][8][max_seq][128]); without, the rows are consecutive
+// prompt tokens of one sequence, row b at position pos0 + b of the cache [L][8][max_seq][128].
+__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, const int32_t* positions, int pos0,
                                                        const uint16_t* q_norm, const uint16_t* k_norm,
                                                        const uint16_t* cos_tab, const uint16_t* sin_tab, uint16_t* qh,
                                                        uint16_t* ql, uint16_t* k_cache, uint16_t* v_cache, int L,
@@ -864,11 +890,12 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, 
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= B * (HQ + 2 * HKV)) return;
   const int b = item / (HQ + 2 * HKV), hd = item % (HQ + 2 * HKV);
-  const int pos = seq_pos(positions, b, max_seq, lane == 0 ? bad : nullptr);
+  const int pos = positions ? seq_pos(positions, b, max_seq, lane == 0 ? bad : nullptr) : pos0 + b;
+  const size_t seq = positions ? (size_t)b : 0;
   const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
   float u0 = r[lane], u1 = r[lane + 64];
   auto cache_row = [&](uint16_t* cache, int kvh) {
-    return cache + ((((size_t)b * L + layer) * HKV + kvh) * max_seq + pos) * D;
+    return cache + (((seq * L + layer) * HKV + kvh) * max_seq + pos) * D;
   };
   if (hd >= HQ + HKV) {  // v
     uint16_t* dst = cache_row(v_cache, hd - HQ - HKV);
@@ -1011,19 +1038,35 @@ __global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int
 // ------------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------------
+template <int H, int I>
+struct BatchPlan {  // K splits of the skinny O and down products
+  static constexpr int SO = H == 1024 ? 2 : 2;  // O: K = 2048
+  static constexpr int SD = H == 1024 ? 3 : 2;  // down: K = I
+  static constexpr int SP = SO > SD ? SO : SD;
+  static_assert((HQ * D / SO / 4) % 256 == 0 && (I / SD / 4) % 256 == 0 && (H / 4) % 256 == 0 && (H / 2) % 256 == 0,
+                "wave K ranges must be multiples of 256");
+};
+
 struct Work {
   float* x;
   uint16_t *ah, *al, *bh, *bl, *qh, *ql;
+  float* raw;   // short prompts: Q/K/V row sums [M][4096]
+  float* part;  // short prompts: split-K partials of the O and down products [3][M][H]
   u64* keys;
   int32_t* bad;
 };
 
+// Prompts of at most SMALL_M tokens run their products on the skinny kernels (weights as the MFMA A
+// operand, the tokens as up to 8 column blocks); longer ones on 128 x 128 tiles.
+constexpr int SMALL_M = 64;
+
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16 [M][max(H, 2048)]; b (hi, lo) bf16
-// [M][I]; q (hi, lo) bf16 [M][2048]; the argmax keys. Offsets in bytes, each 256-byte aligned.
+// [M][I]; q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums and the split-K partials;
+// the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
-  size_t x, ah, al, bh, bl, qh, ql, keys, bad, bytes;
+  size_t x, ah, al, bh, bl, qh, ql, raw, part, keys, bad, bytes;
 };
 static Layout layout(int H, int I, int M) {
   const size_t A = H > HQ * D ? H : HQ * D;
@@ -1037,6 +1080,8 @@ static Layout layout(int H, int I, int M) {
   L.bl = take((size_t)M * I * 2);
   L.qh = take((size_t)M * HQ * D * 2);
   L.ql = take((size_t)M * HQ * D * 2);
+  L.raw = take(M <= SMALL_M ? (size_t)M * (HQ + 2 * HKV) * D * 4 : 0);
+  L.part = take(M <= SMALL_M ? (size_t)3 * M * H * 4 : 0);
   L.keys = take(LM_MAXR * 8);
   L.bad = take(4);
   L.bytes = o;
@@ -1052,6 +1097,8 @@ static Work carve(void* base, const Layout& L) {
   w.bl = reinterpret_cast<uint16_t*>(p + L.bl);
   w.qh = reinterpret_cast<uint16_t*>(p + L.qh);
   w.ql = reinterpret_cast<uint16_t*>(p + L.ql);
+  w.raw = reinterpret_cast<float*>(p + L.raw);
+  w.part = reinterpret_cast<float*>(p + L.part);
   w.keys = reinterpret_cast<u64*>(p + L.keys);
   w.bad = reinterpret_cast<int32_t*>(p + L.bad);
   return w;
@@ -1071,7 +1118,60 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, wk.bad);
-  for (int l = 0; l < dims.num_layers; ++l) {
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, 0, position, max_seq};
+  const dim3 attn_grid(((M + QB - 1) / QB + 1) / 2, HKV);
+  if (M <= SMALL_M) {
+    // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
+    // weight rows per workgroup, 256 to 384 workgroups), the O and down products split over K into
+    // partials that the next norm adds to the residual in a fixed order.
+    typedef BatchPlan<H, I> BP;
+    const int cb = M <= 8 ? 1 : M <= 16 ? 2 : M <= 32 ? 4 : 8;
+    auto skinny = [&](int epi, dim3 grid, const SkArgs& a) -> hipError_t {
+#define MKP_SK(E, C) hipLaunchKernelGGL((skinny_kernel<E, C>), grid, dim3(256), 0, st, a)
+#define MKP_SK_CB(E) \
+  if (cb == 1) MKP_SK(E, 1); else if (cb == 2) MKP_SK(E, 2); else if (cb == 4) MKP_SK(E, 4); else MKP_SK(E, 8)
+      if (epi == SK_RAW) { MKP_SK_CB(SK_RAW); } else if (epi == SK_PART) { MKP_SK_CB(SK_PART); } else { MKP_SK_CB(SK_SILU); }
+#undef MKP_SK_CB
+#undef MKP_SK
+      return hipGetLastError();
+    };
+    const dim3 rows((M + 3) / 4);
+    for (int l = 0; l < dims.num_layers; ++l) {
+      const mk_layer_weights& lw = layers[l];
+      MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab, wk.bad,
+                 wk.part, l == 0 ? 0 : BP::SD, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
+      SkArgs q{};
+      q.xh = wk.ah; q.xl = wk.al; q.ldx = A; q.B = M; q.N = (HQ + 2 * HKV) * D; q.K = H;
+      q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
+      q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = wk.raw;
+      if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, M, nullptr, position,
+                 (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
+                 k_cache, v_cache, dims.num_layers, l, max_seq, wk.bad);
+      AttnArgs at = at0;
+      at.layer = l;
+      MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
+      SkArgs o{};
+      o.xh = wk.ah; o.xl = wk.al; o.ldx = A; o.B = M; o.N = H; o.K = HQ * D;
+      o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = wk.part;
+      if ((e = skinny(SK_PART, dim3(H / 16, BP::SO), o)) != hipSuccess) return e;
+      MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SO,
+                 (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
+      SkArgs u{};
+      u.xh = wk.ah; u.xl = wk.al; u.ldx = A; u.B = M; u.N = I; u.K = H;
+      u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight;
+      u.mh = wk.bh; u.ml = wk.bl; u.ldm = I;
+      if ((e = skinny(SK_SILU, dim3(I / 16, 1), u)) != hipSuccess) return e;
+      SkArgs dn{};
+      dn.xh = wk.bh; dn.xl = wk.bl; dn.ldx = I; dn.B = M; dn.N = H; dn.K = I;
+      dn.w0 = (const uint16_t*)lw.down_proj_weight; dn.out = wk.part;
+      if ((e = skinny(SK_PART, dim3(H / 16, BP::SD), dn)) != hipSuccess) return e;
+    }
+    // the last layer's down partials into the residual (no norm: the LM head normalises its row)
+    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SD,
+               nullptr, nullptr, nullptr, A, M);
+  }
+  for (int l = 0; M > SMALL_M && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
     MKP_LAUNCH(norm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed,
                dims.vocab, wk.bad, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
@@ -1083,8 +1183,9 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     g.cos_tab = cos_tab; g.sin_tab = sin_tab; g.qh = wk.qh; g.ql = wk.ql; g.k_cache = k_cache; g.v_cache = v_cache;
     g.layer = l; g.position = position; g.max_seq = max_seq;
     MKP_LAUNCH(gemm_kernel<EPI_QKV>, dim3(g.N / NT, mtiles), dim3(256), 0, st, g);
-    AttnArgs at{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, l, position, max_seq};
-    MKP_LAUNCH(attn_kernel, dim3(((M + QB - 1) / QB + 1) / 2, HKV), dim3(512), 0, st, at);
+    AttnArgs at = at0;
+    at.layer = l;
+    MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
     GemmArgs go{};
     go.ah = wk.ah; go.al = wk.al; go.lda = A; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H;
@@ -1153,14 +1254,6 @@ extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* token
 namespace mkp {
 
 // Split-K factors of the O and down products (each wave's K range a multiple of 256)
-template <int H, int I>
-struct BatchPlan {
-  static constexpr int SO = H == 1024 ? 2 : 2;  // O: K = 2048
-  static constexpr int SD = H == 1024 ? 3 : 2;  // down: K = I
-  static constexpr int SP = SO > SD ? SO : SD;
-  static_assert((HQ * D / SO / 4) % 256 == 0 && (I / SD / 4) % 256 == 0 && (H / 4) % 256 == 0 && (H / 2) % 256 == 0,
-                "wave K ranges must be multiples of 256");
-};
 
 struct BLayout {
   size_t x, ah, al, bh, bl, raw, qh, ql, part, apart, keys, bad, bytes;
@@ -1226,8 +1319,8 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.xh = ah; q.xl = al; q.ldx = A; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
-    MKB_LAUNCH(skinny_kernel<SK_RAW>, dim3(q.N / 16, 1), dim3(256), 0, st, q);
-    MKB_LAUNCH(qkv_post_kernel, dim3((B * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, raw, B, positions,
+    MKB_LAUNCH((skinny_kernel<SK_RAW, 1>), dim3(q.N / 16, 1), dim3(256), 0, st, q);
+    MKB_LAUNCH(qkv_post_kernel, dim3((B * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, raw, B, positions, 0,
                (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, qh, ql, k_cache,
                v_cache, L, l, max_seq, bad);
     MKB_LAUNCH(battn_partial_kernel, dim3(S, HKV, B), dim3(256), 0, st, qh, ql, k_cache, v_cache, positions, L, l,
@@ -1235,17 +1328,17 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
     SkArgs o{};
     o.xh = ah; o.xl = al; o.ldx = A; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
-    MKB_LAUNCH(skinny_kernel<SK_PART>, dim3(H / 16, BP::SO), dim3(256), 0, st, o);
+    MKB_LAUNCH((skinny_kernel<SK_PART, 1>), dim3(H / 16, BP::SO), dim3(256), 0, st, o);
     MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SO,
                (const uint16_t*)lw.post_attn_norm_weight, ah, al, A, B);
     SkArgs u{};
     u.xh = ah; u.xl = al; u.ldx = A; u.B = B; u.N = I; u.K = H;
     u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bh; u.ml = bl; u.ldm = I;
-    MKB_LAUNCH(skinny_kernel<SK_SILU>, dim3(I / 16, 1), dim3(256), 0, st, u);
+    MKB_LAUNCH((skinny_kernel<SK_SILU, 1>), dim3(I / 16, 1), dim3(256), 0, st, u);
     SkArgs dn{};
     dn.xh = bh; dn.xl = bl; dn.ldx = I; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
     dn.out = part;
-    MKB_LAUNCH(skinny_kernel<SK_PART>, dim3(H / 16, BP::SD), dim3(256), 0, st, dn);
+    MKB_LAUNCH((skinny_kernel<SK_PART, 1>), dim3(H / 16, BP::SD), dim3(256), 0, st, dn);
   }
   // the last layer's down partials, then the final norm and LM head over all B rows
   MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, nullptr,
