@@ -161,8 +161,9 @@ hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_
  *   workspace         device memory of at least mk_decode_batch_workspace_bytes(dims, batch,
  *                     max_seq_len) bytes, 256-byte aligned, owned by the caller
  * A token or position out of range (checked on the device) makes the call report NaN logits and
- * token -1 for every sequence. Asynchronous on `stream`; argument errors return
- * hipErrorInvalidValue before any launch. No counterpart in the reference, whose operator decodes
+ * token -1 for every sequence. The vocabulary size must be a multiple of 16 (Qwen3's 151936 is).
+ * Asynchronous on `stream`; argument errors return hipErrorInvalidValue before any launch. No
+ * counterpart in the reference, whose operator decodes
  * one token of one sequence (/root/reference/pytorch_binding.cu:36-48).
  */
 size_t mk_decode_batch_workspace_bytes(const mk_model_dims* dims, int batch, int max_seq_len);

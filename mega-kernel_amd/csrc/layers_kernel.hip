@@ -680,6 +680,37 @@ __global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, 
   }
 }
 
+// Greedy keys of B rows of logits [B][vocab] (the batched LM head's MFMA output): keys[b] = max over
+// v of argmax_key(logits[b][v], v); with *bad set the rows are overwritten with NaN instead (a
+// failed call is visible in its output). Grid (ceil(vocab / 4096), B), 16 logits per thread.
+__global__ void __launch_bounds__(256) logits_argmax_kernel(float* logits, int vocab, u64* keys, const int32_t* bad) {
+  __shared__ u64 best[4];
+  const int b = blockIdx.y, tid = threadIdx.x;
+  float* row = logits + (size_t)b * vocab;
+  const bool failed = *bad != 0;
+  u64 k = 0;
+  for (int i = 0; i < 16; ++i) {
+    const int v = blockIdx.x * 4096 + i * 256 + tid;
+    if (v < vocab) {
+      const u64 kv = argmax_key(row[v], v);
+      k = k > kv ? k : kv;
+      if (failed) row[v] = __builtin_nanf("");
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const u64 other = __shfl_xor(k, o);
+    k = k > other ? k : other;
+  }
+  if ((tid & 63) == 0) best[tid >> 6] = k;
+  __syncthreads();
+  if (tid == 0) {
+    u64 m = best[0];
+    for (int q = 1; q < 4; ++q) m = m > best[q] ? m : best[q];
+    atomicMax(keys + b, m);
+  }
+}
+
 __global__ void keys_init_kernel(u64* keys, int32_t* bad) {
   if (threadIdx.x < LM_MAXR) keys[threadIdx.x] = 0;
   if (threadIdx.x == 0) *bad = 0;
@@ -700,7 +731,7 @@ __global__ void keys_to_tokens_kernel(const u64* keys, int R, const int32_t* bad
 // a fixed order by the next kernel, so results are deterministic.
 // ------------------------------------------------------------------------------------------------
 constexpr int BMAX = 8;
-constexpr int KS = 256;  // keys per attention split
+constexpr int KS = 64;  // keys per attention split (one round of 4 keys per 16-lane group)
 
 enum SkEpi { SK_RAW = 0, SK_PART = 1, SK_SILU = 2 };
 
@@ -1340,11 +1371,16 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     dn.out = part;
     MKB_LAUNCH((skinny_kernel<SK_PART, 1>), dim3(H / 16, BP::SD), dim3(256), 0, st, dn);
   }
-  // the last layer's down partials, then the final norm and LM head over all B rows
-  MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, nullptr,
-             nullptr, nullptr, A, B);
-  MKB_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, x, 0, B, final_norm, lm_head, dims.vocab, logits, keys,
-             bad);
+  // the last layer's down partials and the final norm, then the tied LM head as one more skinny
+  // product (vocabulary rows x the B normalised rows: each table byte read once, on the matrix
+  // cores) and the greedy keys
+  MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, final_norm,
+             ah, al, A, B);
+  SkArgs lmh{};
+  lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
+  lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
+  MKB_LAUNCH((skinny_kernel<SK_RAW, 1>), dim3(dims.vocab / 16, 1), dim3(256), 0, st, lmh);
+  MKB_LAUNCH(logits_argmax_kernel, dim3((dims.vocab + 4095) / 4096, B), dim3(256), 0, st, logits, dims.vocab, keys, bad);
   if (out_tokens) MKB_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, keys, B, bad, out_tokens);
 #undef MKB_LAUNCH
   return hipSuccess;
@@ -1370,6 +1406,7 @@ extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, cons
   const bool s17 = dims->hidden == 2048 && dims->intermediate == 6144;
   if (!(s06 || s17) || dims->num_layers < 1 || dims->vocab < 1) return hipErrorInvalidValue;
   if (batch < 1 || batch > BMAX || max_seq_len < 1) return hipErrorInvalidValue;
+  if (dims->vocab % 16 != 0) return hipErrorInvalidValue;  // the LM head's skinny product takes 16 rows per workgroup
   const BLayout Lo = blayout(dims->hidden, dims->intermediate, batch, max_seq_len);
   if (workspace_bytes < Lo.bytes || reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return hipErrorInvalidValue;
   const mk_layer_weights* lw = static_cast<const mk_layer_weights*>(layer_weights);  // host array
