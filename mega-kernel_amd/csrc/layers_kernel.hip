@@ -7,7 +7,7 @@
 // GEMMs on the matrix cores (v_mfma_f32_16x16x32_bf16), with the elementwise work fused into the
 // GEMM epilogues:
 //   x = embed[tokens]                                  (fp32 residual rows, workspace)
-//   per layer:  a = RMSNorm(x)                         (norm_kernel, as bf16 hi/lo pair)
+//   per layer:  a = RMSNorm(x)                         (bnorm_kernel, as bf16 hi/lo pair)
 //               q, k, v = a . [Wq; Wk; Wv]^T           (gemm, EPI_QKV: per-head RMSNorm + RoPE on q and k,
 //                                                       k and v rounded to bf16 into the cache, q kept)
 //               o = causal attention(q, cache)         (attn_kernel: flash-style, online softmax)
@@ -16,6 +16,9 @@
 //               m = silu(a . Wg^T) * (a . Wu^T)        (gemm, EPI_SILU: gate and up rows in one tile)
 //               x += m . Wd^T                          (gemm, EPI_RESID)
 //   logits of the last row = RMSNorm(x) . E^T, greedy token (lm_head_kernel, fused argmax)
+// When the residual products' tile grid is small (prompts up to ~1000 tokens) they are split over K
+// into partials that the next norm adds in a fixed order. Prompts of at most SMALL_M tokens run the
+// products on the skinny kernels of the batched decode instead (weights as the MFMA A operand).
 //
 // Numerics are the decode kernel's (the reference kernel's fp32 design, /root/reference/
 // megakernel.cu): fp32 residual and accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to
@@ -65,62 +68,6 @@ __device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
   v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
 }
 
-// ------------------------------------------------------------------------------------------------
-// RMSNorm of rows of x (fp32 [M][H]) into a bf16 hi/lo pair [M][lda]: y = x * w * rsqrt(mean(x^2) +
-// eps) (/root/reference/megakernel.cu:704-739). With `tokens`, x is first filled with the
-// embedding rows (fp32 copies of bf16 embed[tokens[m]]); a token outside [0, vocab) reads row 0
-// instead and sets *bad, which makes the call's logits NaN and its token -1. One wave per row.
-// ------------------------------------------------------------------------------------------------
-template <int H>
-__global__ void __launch_bounds__(256) norm_kernel(float* x, const int32_t* tokens, const uint16_t* embed, int vocab,
-                                                   int32_t* bad, const uint16_t* w, uint16_t* ah, uint16_t* al, int lda,
-                                                   int M) {
-  constexpr int E = H / 64;  // contiguous elements per lane
-  const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;
-  float v[E];
-  float* xr = x + (size_t)m * H + E * lane;
-  if (tokens) {
-    int tok = tokens[m];
-    if (tok < 0 || tok >= vocab) {
-      if (lane == 0) *bad = 1;
-      tok = 0;
-    }
-    const uint16_t* er = embed + (size_t)tok * H + E * lane;
-#pragma unroll
-    for (int k = 0; k < E; k += 8) {
-      float t[8];
-      unpack8(*reinterpret_cast<const uint4*>(er + k), t);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[k + q] = t[q];
-    }
-#pragma unroll
-    for (int k = 0; k < E; k += 4) *reinterpret_cast<float4*>(xr + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
-  } else {
-#pragma unroll
-    for (int k = 0; k < E; k += 4) {
-      const float4 t = *reinterpret_cast<const float4*>(xr + k);
-      v[k] = t.x; v[k + 1] = t.y; v[k + 2] = t.z; v[k + 3] = t.w;
-    }
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < E; ++k) ss = fmaf(v[k], v[k], ss);
-  const float rs = rsqrtf(wave_sum(ss) / (float)H + EPS);
-  const uint16_t* wr = w + E * lane;
-#pragma unroll
-  for (int k = 0; k < E; k += 8) {
-    float wv[8], y[8];
-    unpack8(*reinterpret_cast<const uint4*>(wr + k), wv);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
-    uint4 hi, lo;
-    split8(y, hi, lo);
-    *reinterpret_cast<uint4*>(ah + (size_t)m * lda + E * lane + k) = hi;
-    *reinterpret_cast<uint4*>(al + (size_t)m * lda + E * lane + k) = lo;
-  }
-}
 
 // ------------------------------------------------------------------------------------------------
 // GEMM C[M][N] = A[M][K] . W[N][K]^T on the matrix cores, A given as a bf16 hi/lo pair, W bf16
@@ -142,9 +89,11 @@ struct GemmArgs {
   const uint16_t* w0;
   const uint16_t* w1;
   const uint16_t* w2;
-  // EPI_RESID: x[M][ldx] += C
+  // EPI_RESID: x[M][ldx] += C; or, with `part`, the K range of blockIdx.z (K / gridDim.z wide) into
+  // part[blockIdx.z][M][N], summed into x by the next norm
   float* x;
   int ldx;
+  float* part;
   // EPI_SILU: m = silu(gate) * up into bh/bl [M][ldb]
   uint16_t* bh;
   uint16_t* bl;
@@ -226,12 +175,13 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int bn = 0; bn < 4; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  load(0);
-  for (int k0 = 0; k0 < g.K; k0 += KT) {
+  const int kspan = g.K / gridDim.z, kb = blockIdx.z * kspan, ke = kb + kspan;  // a multiple of KT
+  load(kb);
+  for (int k0 = kb; k0 < ke; k0 += KT) {
     __syncthreads();  // every wave is done with the previous step's tile
     store();
     __syncthreads();
-    if (k0 + KT < g.K) load(k0 + KT);
+    if (k0 + KT < ke) load(k0 + KT);
 #pragma unroll
     for (int s = 0; s < KT / 32; ++s) {
       uint4 fa[2][4], fw[4];
@@ -255,20 +205,25 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   }
 
   if constexpr (EPI == EPI_RESID) {
-    // x += C, each element owned by one lane
+    // x += C (or C into this K range's partial), each element owned by one lane
+    auto each = [&](auto&& f) {
 #pragma unroll
-    for (int bm = 0; bm < 4; ++bm)
+      for (int bm = 0; bm < 4; ++bm)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 64 + bm * 16 + 4 * lg + j;
-        if (m < g.M) {
+        for (int j = 0; j < 4; ++j) {
+          const int m = m0 + wm * 64 + bm * 16 + 4 * lg + j;
+          if (m < g.M) {
 #pragma unroll
-          for (int bn = 0; bn < 4; ++bn) {
-            float* p = g.x + (size_t)m * g.ldx + tn * NT + wn * 64 + bn * 16 + li;
-            *p += acc[bm][bn][j];
+            for (int bn = 0; bn < 4; ++bn) f(m, tn * NT + wn * 64 + bn * 16 + li, acc[bm][bn][j]);
           }
         }
-      }
+    };
+    if (g.part) {
+      float* pz = g.part + (size_t)blockIdx.z * g.M * g.N;
+      each([&](int m, int n, float v) { pz[(size_t)m * g.N + n] = v; });
+    } else {
+      each([&](int m, int n, float v) { g.x[(size_t)m * g.ldx + n] += v; });
+    }
     return;
   }
 
@@ -870,15 +825,23 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < E; ++k) v[k] = xr[k];
+    for (int k = 0; k < E; k += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(xr + k);
+      v[k] = t.x; v[k + 1] = t.y; v[k + 2] = t.z; v[k + 3] = t.w;
+    }
     for (int s = 0; s < S; ++s) {
       const float* pr = part + ((size_t)s * B + b) * H + E * lane;
 #pragma unroll
-      for (int k = 0; k < E; ++k) v[k] += pr[k];
+      for (int k = 0; k < E; k += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(pr + k);
+        v[k] += t.x; v[k + 1] += t.y; v[k + 2] += t.z; v[k + 3] += t.w;
+      }
     }
   }
+  if (tokens || S > 0) {  // x changed
 #pragma unroll
-  for (int k = 0; k < E; k += 4) *reinterpret_cast<float4*>(xr + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+    for (int k = 0; k < E; k += 4) *reinterpret_cast<float4*>(xr + k) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+  }
   if (!w) return;
   float ss = 0.f;
 #pragma unroll
@@ -962,16 +925,11 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, 
 // part: [B][8][S][2][D + 2].
 constexpr int APW = D + 2;
 
-__global__ void __launch_bounds__(256) battn_partial_kernel(const uint16_t* qh, const uint16_t* ql,
-                                                            const uint16_t* k_cache, const uint16_t* v_cache,
-                                                            const int32_t* positions, int L, int layer, int max_seq,
-                                                            float* part, int S) {
-  __shared__ float gacc[16][2][D];
-  __shared__ float gml[16][2][2];
-  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int ctx = seq_pos(positions, b, max_seq, nullptr) + 1;
+__device__ __forceinline__ void battn_split(const uint16_t* qh, const uint16_t* ql, const uint16_t* k_cache,
+                                            const uint16_t* v_cache, int b, int kvh, int s, int ctx, int L, int layer,
+                                            int max_seq, float* part, int S, float (&gacc)[16][2][D],
+                                            float (&gml)[16][2][2]) {
   const int k0 = s * KS;
-  if (k0 >= ctx) return;  // this split is empty; the merge reads splits below ceil(ctx / KS) only
   const int k1 = min(k0 + KS, ctx);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int gi = w * 4 + (lane >> 4), t = lane & 15;
@@ -1043,6 +1001,22 @@ __global__ void __launch_bounds__(256) battn_partial_kernel(const uint16_t* qh, 
   if (d == 0) { o[D] = M; o[D + 1] = Ls; }
 }
 
+__global__ void __launch_bounds__(256) battn_partial_kernel(const uint16_t* qh, const uint16_t* ql,
+                                                            const uint16_t* k_cache, const uint16_t* v_cache,
+                                                            const int32_t* positions, int L, int layer, int max_seq,
+                                                            float* part, int S) {
+  __shared__ float gacc[16][2][D];
+  __shared__ float gml[16][2][2];
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int ctx = seq_pos(positions, b, max_seq, nullptr) + 1;
+  // workgroup x takes splits x, x + gridDim.x, ... of [0, ctx) (the grid does not depend on the
+  // device-side positions); the merge reads splits below ceil(ctx / KS) only
+  for (int s = blockIdx.x; s * KS < ctx; s += gridDim.x) {
+    battn_split(qh, ql, k_cache, v_cache, b, kvh, s, ctx, L, layer, max_seq, part, S, gacc, gml);
+    __syncthreads();  // gacc / gml are reused by the next split
+  }
+}
+
 // Merge of the splits of each sequence and query head into the O-projection's input row (bf16 hi/lo
 // [B][2048]); 128 threads, one per dim.
 __global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int S, const int32_t* positions,
@@ -1082,7 +1056,7 @@ struct Work {
   float* x;
   uint16_t *ah, *al, *bh, *bl, *qh, *ql;
   float* raw;   // short prompts: Q/K/V row sums [M][4096]
-  float* part;  // short prompts: split-K partials of the O and down products [3][M][H]
+  float* part;  // split-K partials of the O and down products [splits][M][H]
   u64* keys;
   int32_t* bad;
 };
@@ -1093,9 +1067,22 @@ constexpr int SMALL_M = 64;
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// K splits of a residual product (O or down, N = H columns) on 128 x 128 tiles for M > SMALL_M:
+// enough workgroups for two per CU when the tile grid alone is small (8 x ceil(M / 128) tiles at
+// the 0.6B width), at most 8, each K range a whole number of 64-wide steps. The partials are added
+// to the residual by the next norm, in split order.
+static int resid_splits(int H, int M, int K) {
+  const int tiles = (H / NT) * ((M + MT - 1) / MT);
+  if (M <= SMALL_M || tiles >= 192) return 1;
+  int sp = (512 + tiles - 1) / tiles;
+  sp = sp < 8 ? sp : 8;
+  while ((K / KT) % sp != 0) --sp;
+  return sp;
+}
+
 // Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16 [M][max(H, 2048)]; b (hi, lo) bf16
-// [M][I]; q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums and the split-K partials;
-// the argmax keys. Offsets in bytes, each 256-byte aligned.
+// [M][I]; q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums; the split-K partials of
+// the residual products; the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
   size_t x, ah, al, bh, bl, qh, ql, raw, part, keys, bad, bytes;
 };
@@ -1112,7 +1099,9 @@ static Layout layout(int H, int I, int M) {
   L.qh = take((size_t)M * HQ * D * 2);
   L.ql = take((size_t)M * HQ * D * 2);
   L.raw = take(M <= SMALL_M ? (size_t)M * (HQ + 2 * HKV) * D * 4 : 0);
-  L.part = take(M <= SMALL_M ? (size_t)3 * M * H * 4 : 0);
+  const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
+  const int sp = M <= SMALL_M ? 3 : (so > sd ? so : sd);
+  L.part = take(sp > 1 ? (size_t)sp * M * H * 4 : 0);
   L.keys = take(LM_MAXR * 8);
   L.bad = take(4);
   L.bytes = o;
@@ -1202,10 +1191,14 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SD,
                nullptr, nullptr, nullptr, A, M);
   }
+  // Longer prompts: 128 x 128 tiles with the epilogues fused; the residual products split over K
+  // into partials when their tile grid is small (the norm after them adds the partials).
+  const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
   for (int l = 0; M > SMALL_M && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
-    MKP_LAUNCH(norm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed,
-               dims.vocab, wk.bad, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
+    const dim3 rows((M + 3) / 4);
+    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab, wk.bad,
+               wk.part, l > 0 && sd > 1 ? sd : 0, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
     GemmArgs g{};
     g.ah = wk.ah; g.al = wk.al; g.lda = A; g.M = M; g.K = H;
     g.w0 = (const uint16_t*)lw.q_weight; g.w1 = (const uint16_t*)lw.k_weight; g.w2 = (const uint16_t*)lw.v_weight;
@@ -1219,10 +1212,10 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
     GemmArgs go{};
     go.ah = wk.ah; go.al = wk.al; go.lda = A; go.M = M; go.N = H; go.K = HQ * D;
-    go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H;
-    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles), dim3(256), 0, st, go);
-    MKP_LAUNCH(norm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad,
-               (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
+    go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H; go.part = so > 1 ? wk.part : nullptr;
+    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, so), dim3(256), 0, st, go);
+    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
+               so > 1 ? so : 0, (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
     GemmArgs gu{};
     gu.ah = wk.ah; gu.al = wk.al; gu.lda = A; gu.M = M; gu.N = 2 * I; gu.K = H;
     gu.w0 = (const uint16_t*)lw.gate_proj_weight; gu.w1 = (const uint16_t*)lw.up_proj_weight;
@@ -1230,9 +1223,12 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     MKP_LAUNCH(gemm_kernel<EPI_SILU>, dim3(I / (NT / 2), mtiles), dim3(256), 0, st, gu);
     GemmArgs gd{};
     gd.ah = wk.bh; gd.al = wk.bl; gd.lda = I; gd.M = M; gd.N = H; gd.K = I;
-    gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H;
-    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles), dim3(256), 0, st, gd);
+    gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H; gd.part = sd > 1 ? wk.part : nullptr;
+    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, sd), dim3(256), 0, st, gd);
   }
+  if (M > SMALL_M && sd > 1)  // the last layer's down partials into the residual
+    MKP_LAUNCH(bnorm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
+               sd, nullptr, nullptr, nullptr, A, M);
   // the last row's logits and greedy token
   MKP_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, wk.x, M - 1, 1, final_norm, lm_head, dims.vocab, logits,
              wk.keys, wk.bad);
@@ -1354,7 +1350,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     MKB_LAUNCH(qkv_post_kernel, dim3((B * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, raw, B, positions, 0,
                (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, qh, ql, k_cache,
                v_cache, L, l, max_seq, bad);
-    MKB_LAUNCH(battn_partial_kernel, dim3(S, HKV, B), dim3(256), 0, st, qh, ql, k_cache, v_cache, positions, L, l,
+    MKB_LAUNCH(battn_partial_kernel, dim3(S < 16 ? S : 16, HKV, B), dim3(256), 0, st, qh, ql, k_cache, v_cache, positions, L, l,
                max_seq, apart, S);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
     SkArgs o{};
