@@ -8,6 +8,10 @@ with HIP events around each call on the current stream.
 Prints one line per prompt length / batch size: the median over ``--runs`` calls after ``--warmup``
 calls, and tokens per second (prompt tokens, or sequences x 1 token for a decode step). Under
 ``rocprofv3 --kernel-trace --stats`` the same command gives the per-kernel split.
+
+``--transformers`` also times the path ``prefill`` replaces, on the same GPU and prompts: the
+reference's Transformers prefill ``model(input_ids, use_cache=True)`` and the copy of its cache into
+the decode layout (/root/reference/model.py:72-87; ``megakernel.copy_prefill_cache``).
 """
 import argparse
 import statistics
@@ -38,6 +42,8 @@ def main(argv=None):
     ap.add_argument("--max-seq", type=int, default=4096)
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--transformers", action="store_true",
+                    help="also time the reference path: Transformers' GPU prefill plus the cache copy")
     a = ap.parse_args(argv)
     import torch
     import megakernel
@@ -62,6 +68,18 @@ def main(argv=None):
                           a.warmup, a.runs)
         print(f"[prefill {a.shape} P={P}] {med:.3f} ms median of {len(runs)} ({P / med * 1e3:,.0f} tokens/s); "
               f"runs {[round(t, 3) for t in runs]}", flush=True)
+        if a.transformers:
+            gpu_model = model.to(dev)
+            ids2 = ids.long().unsqueeze(0)
+
+            def reference_path():
+                with torch.inference_mode():
+                    out = gpu_model(ids2, use_cache=True)
+                megakernel.copy_prefill_cache(out.past_key_values, kc, vc)
+
+            med_r, runs_r = _time(reference_path, a.warmup, a.runs)
+            print(f"[transformers prefill + cache copy {a.shape} P={P}] {med_r:.3f} ms median of {len(runs_r)} "
+                  f"({P / med_r * 1e3:,.0f} tokens/s); native prefill {med_r / med:.2f}x faster", flush=True)
         del kc, vc
     for B in [int(x) for x in a.batch.split(",") if x]:
         if a.context >= a.max_seq:
