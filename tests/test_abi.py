@@ -255,8 +255,9 @@ def test_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
 
 
 def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
-    """``mk_decode_batch`` checks the batch size (1..8), shape, workspace size and alignment before any
-    HIP call; ``mk_decode_batch_workspace_bytes`` is 0 for an unsupported batch."""
+    """``mk_decode_batch`` checks the batch size (1..8), shape, vocabulary (a multiple of 16: the LM
+    head's skinny product takes 16 rows per workgroup), workspace size and alignment before any HIP
+    call; ``mk_decode_batch_workspace_bytes`` is 0 for an unsupported batch."""
     vp, i32 = ctypes.c_void_p, ctypes.c_int
 
     class Dims(ctypes.Structure):
@@ -283,6 +284,7 @@ def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
     assert call(batch=0) == HIP_ERROR_INVALID_VALUE
     assert call(batch=9) == HIP_ERROR_INVALID_VALUE
     assert call(Dims(2048, 3072, 28, 151936)) == HIP_ERROR_INVALID_VALUE
+    assert call(Dims(1024, 3072, 28, 151930)) == HIP_ERROR_INVALID_VALUE  # vocabulary not a multiple of 16
     assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE
     assert call(workspace=vp(256 + 64)) == HIP_ERROR_INVALID_VALUE
     assert call(workspace=None) == HIP_ERROR_INVALID_VALUE

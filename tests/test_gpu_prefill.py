@@ -53,12 +53,14 @@ def _check_cache(got, want, upto, tag):
     assert rel.max().item() <= 2 ** -8
 
 
-@pytest.mark.parametrize("shape_fixture, P", [("mini", 1), ("mini", 24), ("mini", 100), ("mini", 300),
-                                              ("mini17", 64), ("mini17", 200)])
+@pytest.mark.parametrize("shape_fixture, P", [("mini", 1), ("mini", 24), ("mini", 64), ("mini", 65), ("mini", 100),
+                                              ("mini", 300), ("mini17", 64), ("mini17", 200)])
 def test_prefill_matches_oracle(shape_fixture, P, request):
     """Prefill from an empty cache against ``restate.prefill`` on the same prompt: the last token's
     logits and greedy token, every K/V row written, and nothing written past the prompt. P = 1 has
-    one key; P = 300 spans 5 query blocks of the attention and 3 row tiles of the products."""
+    one key; P <= 64 runs the skinny products (64: all 8 column blocks), P = 65 the 128-row tiles
+    (65 rows live, the residual products split over K) and two attention query blocks, the second
+    with one row; P = 300 spans 5 query blocks of the attention and 3 row tiles of the products."""
     sess = request.getfixturevalue(shape_fixture)
     ids = hf.prompt_ids(P, sess.shape.vocab, seed=3)[0].tolist()
     s = sess.shape
