@@ -453,19 +453,29 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
           }
           st[mb] = c;
         }
-        // causal mask and scale; block maximum of this lane's query
+        // causal mask (only on blocks that reach past the wave's first query) and scale; block
+        // maximum of this lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip)
         float bmax = -INFINITY;
+        if (kp0 + KB - 1 <= a.position + q0 + wq) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+          for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int kp = kp0 + 16 * mb + 4 * lg + j;
-            const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
-            st[mb][j] = sv;
-            bmax = fmaxf(bmax, sv);
-          }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            for (int j = 0; j < 4; ++j) {
+              st[mb][j] *= ATT_SCALE;
+              bmax = fmaxf(bmax, st[mb][j]);
+            }
+        } else {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int kp = kp0 + 16 * mb + 4 * lg + j;
+              const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
+              st[mb][j] = sv;
+              bmax = fmaxf(bmax, sv);
+            }
+        }
+        bmax = xmax32(xmax16(bmax));
         const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
         const float alpha = __expf(mrun - mnew);
         float psum = 0.f;
@@ -477,8 +487,7 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
             st[mb][j] = p;
             psum += p;
           }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
+        psum = xsum32(xsum16(psum));
         lrun = lrun * alpha + psum;
         mrun = mnew;
         // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits
