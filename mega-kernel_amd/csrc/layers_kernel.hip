@@ -934,28 +934,51 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, 
 // part: [B][8][S][2][D + 2].
 constexpr int APW = D + 2;
 
-__device__ __forceinline__ void battn_split(const uint16_t* qh, const uint16_t* ql, const uint16_t* k_cache,
-                                            const uint16_t* v_cache, int b, int kvh, int s, int ctx, int L, int layer,
-                                            int max_seq, float* part, int S, float (&gacc)[16][2][D],
+// Per-head RMSNorm + rotate-half RoPE of 8 dims of one head row held by a 16-lane row (lane t: dims
+// 8t..8t+7; the RoPE partner of dim d is d +- 64, in lane t ^ 8), as the decode kernel applies them
+// (/root/reference/megakernel.cu:490-630, 548-555).
+__device__ __forceinline__ void head_norm_rope(float (&v)[8], const float (&wn)[8], const float (&cs)[8],
+                                               const float (&sn)[8], int t) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  const float rs = rsqrtf(row16_sum(ss) / (float)D + EPS);
+  float u[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) u[i] = v[i] * rs * wn[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float pr = dpp<0x128>(u[i]);  // row_ror:8 inside the 16-lane row: lane t ^ 8
+    v[i] = t < 8 ? u[i] * cs[i] - pr * sn[i] : u[i] * cs[i] + pr * sn[i];
+  }
+}
+
+constexpr int BU = 4;  // keys per 16-lane group and split: one round of loads
+static_assert(KS == 16 * BU, "a split is one round of loads");
+
+// Group gi's keys of split s (positions k0 + gi + 16 u; past the split they re-read its last key).
+__device__ __forceinline__ void battn_load(const uint16_t* k_cache, const uint16_t* v_cache, int b, int kvh, int s,
+                                           int ctx, int L, int layer, int max_seq, uint4 (&kw)[BU],
+                                           uint4 (&vw)[BU]) {
+  const int lane = threadIdx.x & 63, gi = (threadIdx.x >> 6) * 4 + (lane >> 4), t = lane & 15;
+  const int k0 = s * KS, k1 = min(k0 + KS, ctx);
+  const size_t base = (((size_t)b * L + layer) * HKV + kvh) * max_seq * D + 8 * t;
+#pragma unroll
+  for (int u = 0; u < BU; ++u) {
+    const int pu = min(k0 + gi + 16 * u, k1 - 1);
+    kw[u] = *reinterpret_cast<const uint4*>(k_cache + base + (size_t)pu * D);
+    vw[u] = *reinterpret_cast<const uint4*>(v_cache + base + (size_t)pu * D);
+  }
+}
+
+__device__ __forceinline__ void battn_split(const float (&qa)[8], const float (&qb)[8], uint4 knew, uint4 vnew,
+                                            int pos, const uint4 (&kw)[BU], const uint4 (&vw)[BU], int b,
+                                            int kvh, int s, int ctx, float* part, int S, float (&gacc)[16][2][D],
                                             float (&gml)[16][2][2]) {
   const int k0 = s * KS;
   const int k1 = min(k0 + KS, ctx);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int gi = w * 4 + (lane >> 4), t = lane & 15;
-  float qa[8], qb[8];
-  {
-    const size_t o0 = (size_t)b * HQ * D + (2 * kvh) * D + 8 * t, o1 = o0 + D;
-    float h[8], l[8];
-    unpack8(*reinterpret_cast<const uint4*>(qh + o0), h);
-    unpack8(*reinterpret_cast<const uint4*>(ql + o0), l);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qa[i] = h[i] + l[i];
-    unpack8(*reinterpret_cast<const uint4*>(qh + o1), h);
-    unpack8(*reinterpret_cast<const uint4*>(ql + o1), l);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qb[i] = h[i] + l[i];
-  }
-  const size_t base = (((size_t)b * L + layer) * HKV + kvh) * max_seq * D + 8 * t;
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f, a0[8], a1[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
@@ -967,29 +990,21 @@ __device__ __forceinline__ void battn_split(const uint16_t* qh, const uint16_t* 
     for (int i = 0; i < 8; ++i) acc[i] = acc[i] * cm + e * v[i];
     m = nm;
   };
-  constexpr int U = 4;
-  for (int p = k0 + gi; p < k1; p += 16 * U) {
-    uint4 kw[U], vw[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int pu = min(p + 16 * u, k1 - 1);
-      kw[u] = *reinterpret_cast<const uint4*>(k_cache + base + (size_t)pu * D);
-      vw[u] = *reinterpret_cast<const uint4*>(v_cache + base + (size_t)pu * D);
-    }
+  for (int u = 0; u < BU; ++u) {
+    const int p = k0 + gi + 16 * u;
+    const bool own = p == pos;  // the new row, from registers
+    float kf[8], vf[8];
+    unpack8(own ? knew : kw[u], kf);
+    unpack8(own ? vnew : vw[u], vf);
+    float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[8], vf[8];
-      unpack8(kw[u], kf);
-      unpack8(vw[u], vf);
-      float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
-      d0 = row16_sum(d0) * ATT_SCALE;
-      d1 = row16_sum(d1) * ATT_SCALE;
-      if (p + 16 * u < k1) {
-        step(d0, vf, m0, l0, a0);
-        step(d1, vf, m1, l1, a1);
-      }
+    for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
+    d0 = row16_sum(d0) * ATT_SCALE;
+    d1 = row16_sum(d1) * ATT_SCALE;
+    if (p < k1) {
+      step(d0, vf, m0, l0, a0);
+      step(d1, vf, m1, l1, a1);
     }
   }
 #pragma unroll
@@ -1010,18 +1025,56 @@ __device__ __forceinline__ void battn_split(const uint16_t* qh, const uint16_t* 
   if (d == 0) { o[D] = M; o[D + 1] = Ls; }
 }
 
-__global__ void __launch_bounds__(256) battn_partial_kernel(const uint16_t* qh, const uint16_t* ql,
-                                                            const uint16_t* k_cache, const uint16_t* v_cache,
-                                                            const int32_t* positions, int L, int layer, int max_seq,
-                                                            float* part, int S) {
+// The attention of one sequence and K/V head, with the new row's projections finished here (from the
+// raw Q/K/V sums, fp32 [B][4096]): every 16-lane group normalises and rotates the pair's two query
+// heads itself, and the new K row (normalised, rotated) and V row are rounded to bf16; the workgroup
+// whose splits include the sequence's position writes them into the cache and attends to that
+// position from registers. Workgroup x takes splits x, x + gridDim.x, ... of [0, position] (the grid
+// does not depend on the device-side positions); the merge reads splits below ceil(ctx / KS) only.
+__global__ void __launch_bounds__(256) battn_partial_kernel(const float* raw, const int32_t* positions,
+                                                            const uint16_t* q_norm, const uint16_t* k_norm,
+                                                            const uint16_t* cos_tab, const uint16_t* sin_tab,
+                                                            uint16_t* k_cache, uint16_t* v_cache, int L, int layer,
+                                                            int max_seq, float* part, int S, int32_t* bad) {
   __shared__ float gacc[16][2][D];
   __shared__ float gml[16][2][2];
   const int kvh = blockIdx.y, b = blockIdx.z;
-  const int ctx = seq_pos(positions, b, max_seq, nullptr) + 1;
-  // workgroup x takes splits x, x + gridDim.x, ... of [0, ctx) (the grid does not depend on the
-  // device-side positions); the merge reads splits below ceil(ctx / KS) only
+  const int lane = threadIdx.x & 63, t = lane & 15;
+  const int pos = seq_pos(positions, b, max_seq, threadIdx.x == 0 && blockIdx.x == 0 && kvh == 0 ? bad : nullptr);
+  const int ctx = pos + 1;
+  if ((int)blockIdx.x * KS >= ctx) return;  // no split for this workgroup (the grid fits the longest cache)
+  // the first split's K/V rows are in flight while the new row's projections are finished
+  uint4 kw[BU], vw[BU];
+  battn_load(k_cache, v_cache, b, kvh, blockIdx.x, ctx, L, layer, max_seq, kw, vw);
+  const float* rr = raw + (size_t)b * (HQ + 2 * HKV) * D + 8 * t;
+  float qa[8], qb[8], kn[8], vv[8], qw[8], kwn[8], cs[8], sn[8];
+  auto ld8 = [](const float* p, float (&v)[8]) {
+    const float4 x = *reinterpret_cast<const float4*>(p), y = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+  };
+  ld8(rr + (2 * kvh) * D, qa);
+  ld8(rr + (2 * kvh + 1) * D, qb);
+  ld8(rr + (HQ + kvh) * D, kn);
+  ld8(rr + (HQ + HKV + kvh) * D, vv);
+  unpack8(*reinterpret_cast<const uint4*>(q_norm + 8 * t), qw);
+  unpack8(*reinterpret_cast<const uint4*>(k_norm + 8 * t), kwn);
+  unpack8(*reinterpret_cast<const uint4*>(cos_tab + (size_t)pos * D + 8 * (t & 7)), cs);  // dims mod 64
+  unpack8(*reinterpret_cast<const uint4*>(sin_tab + (size_t)pos * D + 8 * (t & 7)), sn);
+  head_norm_rope(qa, qw, cs, sn, t);
+  head_norm_rope(qb, qw, cs, sn, t);
+  head_norm_rope(kn, kwn, cs, sn, t);
+  const uint4 knew = make_uint4(pack_bf16x2(kn[0], kn[1]), pack_bf16x2(kn[2], kn[3]), pack_bf16x2(kn[4], kn[5]),
+                                pack_bf16x2(kn[6], kn[7]));
+  const uint4 vnew = make_uint4(pack_bf16x2(vv[0], vv[1]), pack_bf16x2(vv[2], vv[3]), pack_bf16x2(vv[4], vv[5]),
+                                pack_bf16x2(vv[6], vv[7]));
+  if (threadIdx.x < 16 && (pos / KS) % gridDim.x == blockIdx.x) {
+    const size_t row = ((((size_t)b * L + layer) * HKV + kvh) * max_seq + pos) * D + 8 * t;
+    *reinterpret_cast<uint4*>(k_cache + row) = knew;
+    *reinterpret_cast<uint4*>(v_cache + row) = vnew;
+  }
   for (int s = blockIdx.x; s * KS < ctx; s += gridDim.x) {
-    battn_split(qh, ql, k_cache, v_cache, b, kvh, s, ctx, L, layer, max_seq, part, S, gacc, gml);
+    if (s != (int)blockIdx.x) battn_load(k_cache, v_cache, b, kvh, s, ctx, L, layer, max_seq, kw, vw);
+    battn_split(qa, qb, knew, vnew, pos, kw, vw, b, kvh, s, ctx, part, S, gacc, gml);
     __syncthreads();  // gacc / gml are reused by the next split
   }
 }
@@ -1292,7 +1345,7 @@ namespace mkp {
 // Split-K factors of the O and down products (each wave's K range a multiple of 256)
 
 struct BLayout {
-  size_t x, ah, al, bh, bl, raw, qh, ql, part, apart, keys, bad, bytes;
+  size_t x, ah, al, bh, bl, raw, part, apart, keys, bad, bytes;
 };
 static BLayout blayout(int H, int I, int B, int max_seq) {
   const size_t A = H > HQ * D ? H : HQ * D;
@@ -1306,8 +1359,6 @@ static BLayout blayout(int H, int I, int B, int max_seq) {
   L.bh = take((size_t)B * I * 2);
   L.bl = take((size_t)B * I * 2);
   L.raw = take((size_t)B * (HQ + 2 * HKV) * D * 4);
-  L.qh = take((size_t)B * HQ * D * 2);
-  L.ql = take((size_t)B * HQ * D * 2);
   L.part = take((size_t)3 * B * H * 4);
   L.apart = take((size_t)B * HKV * S * 2 * APW * 4);
   L.keys = take(LM_MAXR * 8);
@@ -1331,8 +1382,6 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   uint16_t* bh = reinterpret_cast<uint16_t*>(ws + Lo.bh);
   uint16_t* bl = reinterpret_cast<uint16_t*>(ws + Lo.bl);
   float* raw = reinterpret_cast<float*>(ws + Lo.raw);
-  uint16_t* qh = reinterpret_cast<uint16_t*>(ws + Lo.qh);
-  uint16_t* ql = reinterpret_cast<uint16_t*>(ws + Lo.ql);
   float* part = reinterpret_cast<float*>(ws + Lo.part);
   float* apart = reinterpret_cast<float*>(ws + Lo.apart);
   u64* keys = reinterpret_cast<u64*>(ws + Lo.keys);
@@ -1356,11 +1405,9 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
     MKB_LAUNCH((skinny_kernel<SK_RAW, 1>), dim3(q.N / 16, 1), dim3(256), 0, st, q);
-    MKB_LAUNCH(qkv_post_kernel, dim3((B * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, raw, B, positions, 0,
-               (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, qh, ql, k_cache,
-               v_cache, L, l, max_seq, bad);
-    MKB_LAUNCH(battn_partial_kernel, dim3(S < 16 ? S : 16, HKV, B), dim3(256), 0, st, qh, ql, k_cache, v_cache, positions, L, l,
-               max_seq, apart, S);
+    MKB_LAUNCH(battn_partial_kernel, dim3(S < 16 ? S : 16, HKV, B), dim3(256), 0, st, raw, positions,
+               (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
+               v_cache, L, l, max_seq, apart, S, bad);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
     SkArgs o{};
     o.xh = ah; o.xl = al; o.ldx = A; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
