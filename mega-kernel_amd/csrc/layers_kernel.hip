@@ -879,26 +879,23 @@ __device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_
   return p;
 }
 
-// The raw Q/K/V sums of each row (fp32 [B][4096]): per-head RMSNorm + RoPE on q and k (one wave per
-// row and head, lane l holding dims l and l + 64, the RoPE pair), q kept as a bf16 hi/lo pair
-// [B][2048], k and v rounded to bf16 into the cache. With `positions`, row b is sequence b at
-// positions[b] of its own cache ([B][L][8][max_seq][128]); without, the rows are consecutive
-// prompt tokens of one sequence, row b at position pos0 + b of the cache [L][8][max_seq][128].
-__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int B, const int32_t* positions, int pos0,
-                                                       const uint16_t* q_norm, const uint16_t* k_norm,
-                                                       const uint16_t* cos_tab, const uint16_t* sin_tab, uint16_t* qh,
-                                                       uint16_t* ql, uint16_t* k_cache, uint16_t* v_cache, int L,
-                                                       int layer, int max_seq, int32_t* bad) {
+// The raw Q/K/V sums of M consecutive prompt tokens of one sequence (fp32 [M][4096]; row m at
+// position pos0 + m): per-head RMSNorm + RoPE on q and k (one wave per row and head, lane l holding
+// dims l and l + 64, the RoPE pair), q kept as a bf16 hi/lo pair [M][2048], k and v rounded to bf16
+// into the cache [L][8][max_seq][128].
+__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, int pos0, const uint16_t* q_norm,
+                                                       const uint16_t* k_norm, const uint16_t* cos_tab,
+                                                       const uint16_t* sin_tab, uint16_t* qh, uint16_t* ql,
+                                                       uint16_t* k_cache, uint16_t* v_cache, int layer, int max_seq) {
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= B * (HQ + 2 * HKV)) return;
+  if (item >= M * (HQ + 2 * HKV)) return;
   const int b = item / (HQ + 2 * HKV), hd = item % (HQ + 2 * HKV);
-  const int pos = positions ? seq_pos(positions, b, max_seq, lane == 0 ? bad : nullptr) : pos0 + b;
-  const size_t seq = positions ? (size_t)b : 0;
+  const int pos = pos0 + b;
   const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
   float u0 = r[lane], u1 = r[lane + 64];
   auto cache_row = [&](uint16_t* cache, int kvh) {
-    return cache + (((seq * L + layer) * HKV + kvh) * max_seq + pos) * D;
+    return cache + (((size_t)layer * HKV + kvh) * max_seq + pos) * D;
   };
   if (hd >= HQ + HKV) {  // v
     uint16_t* dst = cache_row(v_cache, hd - HQ - HKV);
@@ -1227,9 +1224,9 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
       q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = wk.raw;
       if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
-      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, M, nullptr, position,
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, M, position,
                  (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
-                 k_cache, v_cache, dims.num_layers, l, max_seq, wk.bad);
+                 k_cache, v_cache, l, max_seq);
       AttnArgs at = at0;
       at.layer = l;
       MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
