@@ -148,6 +148,24 @@ hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * mk_prefill into a paged K/V cache: k_pages / v_pages, block_table, num_pages and page_size as
+ * mk_decode_paged (bf16 [num_layers][num_pages][8][page_size][128]; position p of every layer and K/V
+ * head in page block_table[p / page_size]; page_size a power of two up to 4096, ceil(max_seq_len /
+ * page_size) at most 2048). The K/V rows of positions [position, position + num_tokens) are written
+ * through the table and the attention reads earlier positions through it, so a prompt can be fed in
+ * chunks and the cache handed to mk_decode_paged. A table entry outside [0, num_pages) that the call
+ * touches is reported in-band (NaN logits, token -1); its rows are neither read (page 0 is) nor
+ * written. Workspace as mk_prefill (mk_prefill_workspace_bytes). No reference counterpart: the
+ * reference's cache is contiguous (/root/reference/model.py:79-87).
+ */
+hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                            const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                            const void* layer_weights, const void* cos_table, const void* sin_table, void* k_pages,
+                            void* v_pages, const int32_t* block_table, int num_pages, int page_size, int max_seq_len,
+                            float* logits, int32_t* out_token, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+/*
  * Batched decode: `batch` (1..8) independent sequences advance by one token each in one call.
  * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a
  * device-side loop can advance them): it writes its K/V rows at positions[b] of its own cache and

@@ -68,6 +68,28 @@ __device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
   v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
 }
 
+// Where the prefill's K/V rows live: the decode layout [L][8][max_seq][128], or (with a block table)
+// the paged layout [L][num_pages][8][page_size][128] of mk_decode_paged, position p in page
+// bt[p >> shift]. An entry outside [0, num_pages) sets *bad (the call then reports NaN logits and
+// token -1), reads page 0 and is never written.
+struct KvMap {
+  const int32_t* bt;
+  int num_pages, shift, max_seq;
+};
+__device__ __forceinline__ int kv_page(const KvMap& m, int p, int32_t* bad) {
+  const int e = m.bt[p >> m.shift];
+  if (e < 0 || e >= m.num_pages) {
+    if (bad) *bad = 1;
+    return -1;
+  }
+  return e;
+}
+// element offset of row p of (layer, head) given its page (ignored without a table)
+__device__ __forceinline__ size_t kv_row(const KvMap& m, int layer, int head, int p, int page) {
+  if (!m.bt) return (((size_t)layer * HKV + head) * m.max_seq + p) * D;
+  return (((((size_t)layer * m.num_pages + page) * HKV + head) << m.shift) + (p & ((1 << m.shift) - 1))) * D;
+}
+
 
 // ------------------------------------------------------------------------------------------------
 // GEMM C[M][N] = A[M][K] . W[N][K]^T on the matrix cores, A given as a bf16 hi/lo pair, W bf16
@@ -107,7 +129,9 @@ struct GemmArgs {
   uint16_t* ql;
   uint16_t* k_cache;
   uint16_t* v_cache;
-  int layer, position, max_seq;
+  KvMap kv;
+  int32_t* bad;
+  int layer, position;
 };
 
 // first element of weight row r (0..127) of N-tile t
@@ -264,8 +288,10 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
     // tile tn is one head: q head tn (< 16), k head tn - 16 (< 24) or v head tn - 24
     const int pos = g.position + m;
     const int d0 = 64 * half;  // this thread's dims [d0, d0 + 64); the RoPE partner of d is d ^ 64
+    const int page = tn >= HQ && g.kv.bt ? kv_page(g.kv, pos, g.bad) : 0;
     if (tn >= HQ + HKV) {      // v: rounded to bf16 into the cache as is
-      uint16_t* dst = g.v_cache + (((size_t)g.layer * HKV + (tn - HQ - HKV)) * g.max_seq + pos) * D + d0;
+      if (page < 0) return;
+      uint16_t* dst = g.v_cache + kv_row(g.kv, g.layer, tn - HQ - HKV, pos, page) + d0;
 #pragma unroll
       for (int c = 0; c < 64; c += 8) {
         uint32_t p[4];
@@ -303,11 +329,11 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
         const size_t off = (size_t)m * (HQ * D) + tn * D + d0 + c;
         *reinterpret_cast<uint4*>(g.qh + off) = hi;
         *reinterpret_cast<uint4*>(g.ql + off) = lo;
-      } else {
+      } else if (page >= 0) {
         uint32_t p[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(o[2 * q], o[2 * q + 1]);
-        *reinterpret_cast<uint4*>(g.k_cache + (((size_t)g.layer * HKV + (tn - HQ)) * g.max_seq + pos) * D + d0 + c) =
+        *reinterpret_cast<uint4*>(g.k_cache + kv_row(g.kv, g.layer, tn - HQ, pos, page) + d0 + c) =
             make_uint4(p[0], p[1], p[2], p[3]);
       }
     }
@@ -349,8 +375,11 @@ struct AttnArgs {
   uint16_t* oh;
   uint16_t* ol;
   int ldo;
-  int M, layer, position, max_seq;
+  int M, layer, position;
+  KvMap kv;
+  int32_t* bad;
 };
+constexpr int ATT_MAX_PAGES = 2048;  // block-table entries staged in LDS (as mk_decode_paged)
 
 struct AttnSmem {
   union {
@@ -364,11 +393,24 @@ struct AttnSmem {
 
 __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) AttnSmem sm;
+  __shared__ int32_t pages[ATT_MAX_PAGES];  // a paged cache's table entries (-1: out of range)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int kvh = blockIdx.y, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
   const int nqb = (a.M + QB - 1) / QB;
-  const size_t kvbase = ((size_t)a.layer * HKV + kvh) * a.max_seq * D;
+  if (a.kv.bt) {
+    const int n = ((a.position + a.M - 1) >> a.kv.shift) + 1;  // entries of keys [0, position + M)
+    for (int i = tid; i < n; i += 512) {
+      const int e = a.kv.bt[i];
+      pages[i] = (e < 0 || e >= a.kv.num_pages) ? -1 : e;
+      if (pages[i] < 0) *a.bad = 1;
+    }
+    __syncthreads();
+  }
+  // element offset of key kp's row of this K/V head (page 0 for an out-of-range entry)
+  auto key_row = [&](int kp) {
+    return kv_row(a.kv, a.layer, kvh, kp, a.kv.bt ? max(pages[kp >> a.kv.shift], 0) : 0);
+  };
   // staging roles: K chunk c = tid + 512 r (key c / 16, dims 8 (c % 16)); V: keys 2 vp, 2 vp + 1 at
   // dims 8 vc .. +7 (lanes of a wave span 32 key pairs and two chunks: conflict-free 32-bit writes)
   const int vp = lane & 31, vc = 2 * w + (lane >> 5);
@@ -405,13 +447,13 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int c = tid + 512 * r, kp = kp0 + (c >> 4);
-        pk[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.k_cache + kvbase + (size_t)kp * D + 8 * (c & 15))
+        pk[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.k_cache + key_row(kp) + 8 * (c & 15))
                            : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int kp = kp0 + 2 * vp + r;
-        pv[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.v_cache + kvbase + (size_t)kp * D + 8 * vc)
+        pv[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.v_cache + key_row(kp) + 8 * vc)
                            : make_uint4(0, 0, 0, 0);
       }
     };
@@ -886,7 +928,8 @@ __device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_
 __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, int pos0, const uint16_t* q_norm,
                                                        const uint16_t* k_norm, const uint16_t* cos_tab,
                                                        const uint16_t* sin_tab, uint16_t* qh, uint16_t* ql,
-                                                       uint16_t* k_cache, uint16_t* v_cache, int layer, int max_seq) {
+                                                       uint16_t* k_cache, uint16_t* v_cache, int layer, KvMap kv,
+                                                       int32_t* bad) {
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= M * (HQ + 2 * HKV)) return;
@@ -894,10 +937,10 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, 
   const int pos = pos0 + b;
   const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
   float u0 = r[lane], u1 = r[lane + 64];
-  auto cache_row = [&](uint16_t* cache, int kvh) {
-    return cache + (((size_t)layer * HKV + kvh) * max_seq + pos) * D;
-  };
+  const int page = hd >= HQ && kv.bt ? kv_page(kv, pos, lane == 0 ? bad : nullptr) : 0;
+  auto cache_row = [&](uint16_t* cache, int kvh) { return cache + kv_row(kv, layer, kvh, pos, page); };
   if (hd >= HQ + HKV) {  // v
+    if (page < 0) return;
     uint16_t* dst = cache_row(v_cache, hd - HQ - HKV);
     dst[lane] = f32_to_bf16(u0);
     dst[lane + 64] = f32_to_bf16(u1);
@@ -917,7 +960,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, 
     h[lane + 64] = h1;
     l[lane] = f32_to_bf16(o0 - bf16_to_f32(h0));
     l[lane + 64] = f32_to_bf16(o1 - bf16_to_f32(h1));
-  } else {
+  } else if (page >= 0) {
     uint16_t* dst = cache_row(k_cache, hd - HQ);
     dst[lane] = f32_to_bf16(o0);
     dst[lane + 64] = f32_to_bf16(o1);
@@ -1187,7 +1230,7 @@ template <int H, int I>
 static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, int position, const uint16_t* embed,
                       const uint16_t* lm_head, const uint16_t* final_norm, const mk_layer_weights* layers,
                       const uint16_t* cos_tab, const uint16_t* sin_tab, uint16_t* k_cache, uint16_t* v_cache,
-                      int max_seq, float* logits, int32_t* out_token, const Work& wk, hipStream_t st) {
+                      const KvMap& kv, float* logits, int32_t* out_token, const Work& wk, hipStream_t st) {
   const int A = H > HQ * D ? H : HQ * D;
   const int mtiles = (M + MT - 1) / MT;
   hipError_t e;
@@ -1197,7 +1240,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, wk.bad);
-  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, 0, position, max_seq};
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, 0, position, kv, wk.bad};
   const dim3 attn_grid(((M + QB - 1) / QB + 1) / 2, HKV);
   if (M <= SMALL_M) {
     // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
@@ -1226,7 +1269,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
       MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, M, position,
                  (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
-                 k_cache, v_cache, l, max_seq);
+                 k_cache, v_cache, l, kv, wk.bad);
       AttnArgs at = at0;
       at.layer = l;
       MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
@@ -1264,7 +1307,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     g.N = (HQ + 2 * HKV) * D;
     g.q_norm = (const uint16_t*)lw.q_norm_weight; g.k_norm = (const uint16_t*)lw.k_norm_weight;
     g.cos_tab = cos_tab; g.sin_tab = sin_tab; g.qh = wk.qh; g.ql = wk.ql; g.k_cache = k_cache; g.v_cache = v_cache;
-    g.layer = l; g.position = position; g.max_seq = max_seq;
+    g.layer = l; g.position = position; g.kv = kv; g.bad = wk.bad;
     MKP_LAUNCH(gemm_kernel<EPI_QKV>, dim3(g.N / NT, mtiles), dim3(256), 0, st, g);
     AttnArgs at = at0;
     at.layer = l;
@@ -1305,11 +1348,11 @@ extern "C" size_t mk_prefill_workspace_bytes(const mk_model_dims* dims, int num_
   return layout(dims->hidden, dims->intermediate, num_tokens).bytes;
 }
 
-extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
-                                 const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
-                                 const void* layer_weights, const void* cos_table, const void* sin_table,
-                                 void* k_cache, void* v_cache, int max_seq_len, float* logits, int32_t* out_token,
-                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+static hipError_t prefill_impl(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                               const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                               const void* layer_weights, const void* cos_table, const void* sin_table,
+                               void* k_cache, void* v_cache, const KvMap& kv, int max_seq_len, float* logits,
+                               int32_t* out_token, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!dims || !tokens || !embed_weight || !lm_head_weight || !final_norm_weight || !layer_weights ||
       !cos_table || !sin_table || !k_cache || !v_cache || !logits || !workspace)
     return hipErrorInvalidValue;
@@ -1327,11 +1370,40 @@ extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* token
     return run<1024, 3072>(*dims, tokens, num_tokens, position, (const uint16_t*)embed_weight,
                            (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
                            (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
-                           (uint16_t*)v_cache, max_seq_len, logits, out_token, wk, stream);
+                           (uint16_t*)v_cache, kv, logits, out_token, wk, stream);
   return run<2048, 6144>(*dims, tokens, num_tokens, position, (const uint16_t*)embed_weight,
                          (const uint16_t*)lm_head_weight, (const uint16_t*)final_norm_weight, lw,
                          (const uint16_t*)cos_table, (const uint16_t*)sin_table, (uint16_t*)k_cache,
-                         (uint16_t*)v_cache, max_seq_len, logits, out_token, wk, stream);
+                         (uint16_t*)v_cache, kv, logits, out_token, wk, stream);
+}
+
+extern "C" hipError_t mk_prefill(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                                 const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                                 const void* layer_weights, const void* cos_table, const void* sin_table,
+                                 void* k_cache, void* v_cache, int max_seq_len, float* logits, int32_t* out_token,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const KvMap kv{nullptr, 0, 0, max_seq_len};
+  return prefill_impl(dims, tokens, num_tokens, position, embed_weight, lm_head_weight, final_norm_weight,
+                      layer_weights, cos_table, sin_table, k_cache, v_cache, kv, max_seq_len, logits, out_token,
+                      workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, int num_tokens, int position,
+                                       const void* embed_weight, const void* lm_head_weight,
+                                       const void* final_norm_weight, const void* layer_weights,
+                                       const void* cos_table, const void* sin_table, void* k_pages, void* v_pages,
+                                       const int32_t* block_table, int num_pages, int page_size, int max_seq_len,
+                                       float* logits, int32_t* out_token, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+  if (!block_table || num_pages < 1 || page_size < 1 || page_size > 4096 || (page_size & (page_size - 1)) != 0 ||
+      max_seq_len < 1 || (max_seq_len + page_size - 1) / page_size > ATT_MAX_PAGES)
+    return hipErrorInvalidValue;
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  const KvMap kv{block_table, num_pages, shift, max_seq_len};
+  return prefill_impl(dims, tokens, num_tokens, position, embed_weight, lm_head_weight, final_norm_weight,
+                      layer_weights, cos_table, sin_table, k_pages, v_pages, kv, max_seq_len, logits, out_token,
+                      workspace, workspace_bytes, stream);
 }
 
 // ------------------------------------------------------------------------------------------------

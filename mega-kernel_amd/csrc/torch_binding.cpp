@@ -262,15 +262,18 @@ torch::Tensor decode_steps_paged(torch::Tensor tokens, int64_t n, bool generate,
   return logits;
 }
 
-// Batched prefill (mk_prefill): tokens (int32 [n] on the weights' device) at positions position ..
-// position + n - 1, K/V rows written into the [L, 8, max_seq, 128] caches; returns the last token's
+// Batched prefill (mk_prefill / mk_prefill_paged): tokens (int32 [n] on the weights' device) at
+// positions position .. position + n - 1, K/V rows written into the caches; returns the last token's
 // fp32 logits [V] and its greedy token (int32 [1] on the device). The workspace is a tensor from
 // torch's caching allocator, held until the call's work is queued.
-std::tuple<torch::Tensor, torch::Tensor> prefill(torch::Tensor tokens, torch::Tensor embed, torch::Tensor lm_head,
-                                                 torch::Tensor final_norm, std::vector<torch::Tensor> lw,
-                                                 torch::Tensor cos, torch::Tensor sin, torch::Tensor kc, torch::Tensor vc,
-                                                 int64_t position, int64_t max_seq_len) {
-  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len);
+static std::tuple<torch::Tensor, torch::Tensor> prefill_common(const torch::Tensor& tokens, const Checked& c,
+                                                               const torch::Tensor& embed, const torch::Tensor& lm_head,
+                                                               const torch::Tensor& final_norm,
+                                                               const std::vector<torch::Tensor>& lw,
+                                                               const torch::Tensor& cos, const torch::Tensor& sin,
+                                                               const torch::Tensor& kc, const torch::Tensor& vc,
+                                                               const torch::Tensor* block_table, const Paged* pg,
+                                                               int64_t position, int64_t max_seq_len) {
   TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
                   tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) >= 1,
               "megakernel: tokens must be a non-empty contiguous int32 [n] tensor on ", c.dev);
@@ -289,11 +292,40 @@ std::tuple<torch::Tensor, torch::Tensor> prefill(torch::Tensor tokens, torch::Te
   auto ws = torch::empty({(int64_t)bytes}, embed.options().dtype(torch::kUInt8));
   auto logits = torch::empty({c.dims.vocab}, embed.options().dtype(torch::kFloat32));
   auto tok = torch::empty({1}, embed.options().dtype(torch::kInt32));
-  MK_HIP_CHECK(mk_prefill(&c.dims, tokens.data_ptr<int32_t>(), (int)n, (int)position, embed.data_ptr(),
-                          lm_head.data_ptr(), final_norm.data_ptr(), table.data(), cos.data_ptr(), sin.data_ptr(),
-                          kc.data_ptr(), vc.data_ptr(), (int)max_seq_len, logits.data_ptr<float>(),
-                          tok.data_ptr<int32_t>(), ws.data_ptr(), bytes, stream));
+  if (pg)
+    MK_HIP_CHECK(mk_prefill_paged(&c.dims, tokens.data_ptr<int32_t>(), (int)n, (int)position, embed.data_ptr(),
+                                  lm_head.data_ptr(), final_norm.data_ptr(), table.data(), cos.data_ptr(),
+                                  sin.data_ptr(), kc.data_ptr(), vc.data_ptr(), block_table->data_ptr<int32_t>(),
+                                  pg->num_pages, pg->page_size, (int)max_seq_len, logits.data_ptr<float>(),
+                                  tok.data_ptr<int32_t>(), ws.data_ptr(), bytes, stream));
+  else
+    MK_HIP_CHECK(mk_prefill(&c.dims, tokens.data_ptr<int32_t>(), (int)n, (int)position, embed.data_ptr(),
+                            lm_head.data_ptr(), final_norm.data_ptr(), table.data(), cos.data_ptr(), sin.data_ptr(),
+                            kc.data_ptr(), vc.data_ptr(), (int)max_seq_len, logits.data_ptr<float>(),
+                            tok.data_ptr<int32_t>(), ws.data_ptr(), bytes, stream));
   return {logits, tok};
+}
+
+// Into the [L, 8, max_seq, 128] caches.
+std::tuple<torch::Tensor, torch::Tensor> prefill(torch::Tensor tokens, torch::Tensor embed, torch::Tensor lm_head,
+                                                 torch::Tensor final_norm, std::vector<torch::Tensor> lw,
+                                                 torch::Tensor cos, torch::Tensor sin, torch::Tensor kc, torch::Tensor vc,
+                                                 int64_t position, int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, position, max_seq_len);
+  return prefill_common(tokens, c, embed, lm_head, final_norm, lw, cos, sin, kc, vc, nullptr, nullptr, position,
+                        max_seq_len);
+}
+
+// Into a paged cache (k_pages / v_pages and block_table as decode_paged).
+std::tuple<torch::Tensor, torch::Tensor> prefill_paged(torch::Tensor tokens, torch::Tensor embed,
+                                                       torch::Tensor lm_head, torch::Tensor final_norm,
+                                                       std::vector<torch::Tensor> lw, torch::Tensor cos,
+                                                       torch::Tensor sin, torch::Tensor kp, torch::Tensor vp,
+                                                       torch::Tensor block_table, int64_t position, int64_t max_seq_len) {
+  Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kp, vp, position, max_seq_len, true, true);
+  const Paged pg = check_paged(c, kp, vp, block_table, max_seq_len);
+  return prefill_common(tokens, c, embed, lm_head, final_norm, lw, cos, sin, kp, vp, &block_table, &pg, position,
+                        max_seq_len);
 }
 
 // Batched decode (mk_decode_batch): B sequences, tokens and positions int32 [B] on the weights' device,
@@ -368,6 +400,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "step without host synchronization; returns the last step's fp32 logits");
   m.def("decode_paged", &decode_paged,
         "decode on a paged K/V cache ([L, pages, 8, page_size, 128] + int32 block table); returns (fp32 logits, "
+        "int32 greedy token on device)");
+  m.def("prefill_paged", &prefill_paged,
+        "batched prefill into a paged K/V cache (tensors as decode_paged); returns (fp32 logits of the last token, "
         "int32 greedy token on device)");
   m.def("decode_steps_paged", &decode_steps_paged,
         "decode_steps on a paged K/V cache (tensors as decode_paged); returns the last step's fp32 logits");

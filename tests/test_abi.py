@@ -254,6 +254,39 @@ def test_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
     assert call(workspace=None) == HIP_ERROR_INVALID_VALUE
 
 
+
+def test_paged_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
+    """``mk_prefill_paged`` checks the block table, page count and page size (a power of two up to
+    4096, at most 2048 table entries for max_seq_len) before any HIP call, then everything
+    ``mk_prefill`` checks."""
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+
+    class Dims(ctypes.Structure):
+        _fields_ = [("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                    ("num_layers", ctypes.c_int32), ("vocab", ctypes.c_int32)]
+
+    ws = lib.mk_prefill_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.POINTER(Dims), i32]
+    good = Dims(1024, 3072, 28, 151936)
+    f = lib.mk_prefill_paged
+    f.restype = i32
+    f.argtypes = [ctypes.POINTER(Dims), vp, i32, i32] + [vp] * 8 + [vp, i32, i32, i32, vp, vp, vp, ctypes.c_size_t, vp]
+    d = vp(256)
+
+    def call(table=d, num_pages=64, page_size=16, n=32, position=0, max_seq=512, nbytes=None):
+        nb = ws(ctypes.byref(good), n) if nbytes is None else nbytes
+        return f(ctypes.byref(good), d, n, position, *([d] * 8), table, num_pages, page_size, max_seq, d, None, d,
+                 nb, None)
+
+    assert call(table=None) == HIP_ERROR_INVALID_VALUE
+    assert call(num_pages=0) == HIP_ERROR_INVALID_VALUE
+    assert call(page_size=24) == HIP_ERROR_INVALID_VALUE   # not a power of two
+    assert call(page_size=8192) == HIP_ERROR_INVALID_VALUE
+    assert call(page_size=1, max_seq=4096) == HIP_ERROR_INVALID_VALUE  # 4096 table entries
+    assert call(position=500, n=13) == HIP_ERROR_INVALID_VALUE  # past max_seq_len
+    assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE
+
 def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
     """``mk_decode_batch`` checks the batch size (1..8), shape, vocabulary (a multiple of 16: the LM
     head's skinny product takes 16 rows per workgroup), workspace size and alignment before any HIP
