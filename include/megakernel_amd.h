@@ -166,7 +166,7 @@ hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, in
                             hipStream_t stream);
 
 /*
- * Batched decode: `batch` (1..8) independent sequences advance by one token each in one call.
+ * Batched decode: `batch` (1..64) independent sequences advance by one token each in one call.
  * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a
  * device-side loop can advance them): it writes its K/V rows at positions[b] of its own cache and
  * attends over [0, positions[b]]. k_cache/v_cache are bf16 [batch][num_layers][8][max_seq_len][128]

@@ -717,8 +717,8 @@ __global__ void __launch_bounds__(256) logits_argmax_kernel(float* logits, int v
   }
 }
 
-__global__ void keys_init_kernel(u64* keys, int32_t* bad) {
-  if (threadIdx.x < LM_MAXR) keys[threadIdx.x] = 0;
+__global__ void keys_init_kernel(u64* keys, int n, int32_t* bad) {  // n <= 64 keys
+  if ((int)threadIdx.x < n) keys[threadIdx.x] = 0;
   if (threadIdx.x == 0) *bad = 0;
 }
 
@@ -728,15 +728,16 @@ __global__ void keys_to_tokens_kernel(const u64* keys, int R, const int32_t* bad
 }
 
 // ------------------------------------------------------------------------------------------------
-// Batched decode: BMAX = 8 sequences at most, one token each per step, every sequence with its own
+// Batched decode: BMAX = 64 sequences at most, one token each per step, every sequence with its own
 // cache ([B][L][8][max_seq][128]) and position. The layer structure of the prefill, with the
-// products as skinny GEMMs: the weights are the MFMA's 16-row operand A and the sequences'
+// products as skinny GEMMs: the weights are the MFMA's 16-row operand A and 8 sequences'
 // activations, hi and lo, its 16 columns (B operand column 2b + hl), so one
-// v_mfma_f32_16x16x32_bf16 multiplies 16 weight rows x 32 inputs by all 8 sequences at once and
-// each weight byte is read once per step. Sums split over K are written as partials and added in
-// a fixed order by the next kernel, so results are deterministic.
+// v_mfma_f32_16x16x32_bf16 multiplies 16 weight rows x 32 inputs by 8 sequences at once, up to 8
+// such column blocks per weight fragment, and each weight byte is read once per step. Sums split
+// over K are written as partials and added in a fixed order by the next kernel, so results are
+// deterministic.
 // ------------------------------------------------------------------------------------------------
-constexpr int BMAX = 8;
+constexpr int BMAX = 64;
 constexpr int KS = 64;  // keys per attention split (one round of 4 keys per 16-lane group)
 
 enum SkEpi { SK_RAW = 0, SK_PART = 1, SK_SILU = 2 };
@@ -846,6 +847,18 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
     }
   }
 }
+
+// The skinny product for up to 8 * cb activation rows (cb: 1, 2, 4 or 8 column blocks).
+static hipError_t launch_skinny(int epi, int cb, dim3 grid, const SkArgs& a, hipStream_t st) {
+#define MK_SK(E, C) hipLaunchKernelGGL((skinny_kernel<E, C>), grid, dim3(256), 0, st, a)
+#define MK_SK_CB(E) \
+  if (cb == 1) MK_SK(E, 1); else if (cb == 2) MK_SK(E, 2); else if (cb == 4) MK_SK(E, 4); else MK_SK(E, 8)
+  if (epi == SK_RAW) { MK_SK_CB(SK_RAW); } else if (epi == SK_PART) { MK_SK_CB(SK_PART); } else { MK_SK_CB(SK_SILU); }
+#undef MK_SK_CB
+#undef MK_SK
+  return hipGetLastError();
+}
+static int column_blocks(int rows) { return rows <= 8 ? 1 : rows <= 16 ? 2 : rows <= 32 ? 4 : 8; }
 
 // Rows b < B of the residual: with `tokens`, x[b] = embed[tokens[b]] (a token outside [0, vocab)
 // reads row 0 and sets *bad); with `part`, x[b] += sum over s < S of part[s][b] (in order); then,
@@ -1239,7 +1252,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     hipLaunchKernelGGL(__VA_ARGS__);                      \
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
-  MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, wk.bad);
+  MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad);
   const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, 0, position, kv, wk.bad};
   const dim3 attn_grid(((M + QB - 1) / QB + 1) / 2, HKV);
   if (M <= SMALL_M) {
@@ -1247,16 +1260,8 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     // weight rows per workgroup, 256 to 384 workgroups), the O and down products split over K into
     // partials that the next norm adds to the residual in a fixed order.
     typedef BatchPlan<H, I> BP;
-    const int cb = M <= 8 ? 1 : M <= 16 ? 2 : M <= 32 ? 4 : 8;
-    auto skinny = [&](int epi, dim3 grid, const SkArgs& a) -> hipError_t {
-#define MKP_SK(E, C) hipLaunchKernelGGL((skinny_kernel<E, C>), grid, dim3(256), 0, st, a)
-#define MKP_SK_CB(E) \
-  if (cb == 1) MKP_SK(E, 1); else if (cb == 2) MKP_SK(E, 2); else if (cb == 4) MKP_SK(E, 4); else MKP_SK(E, 8)
-      if (epi == SK_RAW) { MKP_SK_CB(SK_RAW); } else if (epi == SK_PART) { MKP_SK_CB(SK_PART); } else { MKP_SK_CB(SK_SILU); }
-#undef MKP_SK_CB
-#undef MKP_SK
-      return hipGetLastError();
-    };
+    const int cb = column_blocks(M);
+    auto skinny = [&](int epi, dim3 grid, const SkArgs& a) { return launch_skinny(epi, cb, grid, a, st); };
     const dim3 rows((M + 3) / 4);
     for (int l = 0; l < dims.num_layers; ++l) {
       const mk_layer_weights& lw = layers[l];
@@ -1430,7 +1435,7 @@ static BLayout blayout(int H, int I, int B, int max_seq) {
   L.raw = take((size_t)B * (HQ + 2 * HKV) * D * 4);
   L.part = take((size_t)3 * B * H * 4);
   L.apart = take((size_t)B * HKV * S * 2 * APW * 4);
-  L.keys = take(LM_MAXR * 8);
+  L.keys = take((size_t)B * 8);
   L.bad = take(4);
   L.bytes = o;
   return L;
@@ -1462,7 +1467,8 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     hipLaunchKernelGGL(__VA_ARGS__);                      \
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
-  MKB_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, keys, bad);
+  MKB_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, keys, B, bad);
+  const int cb = column_blocks(B);
   const dim3 rows((B + 3) / 4);
   for (int l = 0; l < L; ++l) {
     const mk_layer_weights& lw = layers[l];
@@ -1473,24 +1479,24 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.xh = ah; q.xl = al; q.ldx = A; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
-    MKB_LAUNCH((skinny_kernel<SK_RAW, 1>), dim3(q.N / 16, 1), dim3(256), 0, st, q);
+    if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st)) != hipSuccess) return e;
     MKB_LAUNCH(battn_partial_kernel, dim3(S < 16 ? S : 16, HKV, B), dim3(256), 0, st, raw, positions,
                (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
                v_cache, L, l, max_seq, apart, S, bad);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
     SkArgs o{};
     o.xh = ah; o.xl = al; o.ldx = A; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
-    MKB_LAUNCH((skinny_kernel<SK_PART, 1>), dim3(H / 16, BP::SO), dim3(256), 0, st, o);
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, BP::SO), o, st)) != hipSuccess) return e;
     MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SO,
                (const uint16_t*)lw.post_attn_norm_weight, ah, al, A, B);
     SkArgs u{};
     u.xh = ah; u.xl = al; u.ldx = A; u.B = B; u.N = I; u.K = H;
     u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bh; u.ml = bl; u.ldm = I;
-    MKB_LAUNCH((skinny_kernel<SK_SILU, 1>), dim3(I / 16, 1), dim3(256), 0, st, u);
+    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 16, 1), u, st)) != hipSuccess) return e;
     SkArgs dn{};
     dn.xh = bh; dn.xl = bl; dn.ldx = I; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
     dn.out = part;
-    MKB_LAUNCH((skinny_kernel<SK_PART, 1>), dim3(H / 16, BP::SD), dim3(256), 0, st, dn);
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, BP::SD), dn, st)) != hipSuccess) return e;
   }
   // the last layer's down partials and the final norm, then the tied LM head as one more skinny
   // product (vocabulary rows x the B normalised rows: each table byte read once, on the matrix
@@ -1500,7 +1506,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   SkArgs lmh{};
   lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
   lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
-  MKB_LAUNCH((skinny_kernel<SK_RAW, 1>), dim3(dims.vocab / 16, 1), dim3(256), 0, st, lmh);
+  if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st)) != hipSuccess) return e;
   MKB_LAUNCH(logits_argmax_kernel, dim3((dims.vocab + 4095) / 4096, B), dim3(256), 0, st, logits, dims.vocab, keys, bad);
   if (out_tokens) MKB_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, keys, B, bad, out_tokens);
 #undef MKB_LAUNCH

@@ -337,8 +337,8 @@ std::tuple<torch::Tensor, torch::Tensor> decode_batch(torch::Tensor tokens, torc
                                                       torch::Tensor kc, torch::Tensor vc, int64_t max_seq_len) {
   Checked c = validate(0, embed, lm_head, final_norm, lw, cos, sin, kc, vc, 0, max_seq_len, true, true);
   TORCH_CHECK(tokens.defined() && tokens.device() == c.dev && tokens.scalar_type() == torch::kInt32 &&
-                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) >= 1 && tokens.size(0) <= 8,
-              "megakernel: tokens must be a contiguous int32 [B] tensor (1 <= B <= 8) on ", c.dev);
+                  tokens.is_contiguous() && tokens.dim() == 1 && tokens.size(0) >= 1 && tokens.size(0) <= 64,
+              "megakernel: tokens must be a contiguous int32 [B] tensor (1 <= B <= 64) on ", c.dev);
   const int64_t B = tokens.size(0);
   TORCH_CHECK(positions.defined() && positions.device() == c.dev && positions.scalar_type() == torch::kInt32 &&
                   positions.is_contiguous() && positions.dim() == 1 && positions.size(0) == B,
@@ -410,7 +410,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "batched prefill of int32 tokens [n] at positions position..position+n-1 into the [L, 8, max_seq, 128] "
         "caches; returns (fp32 logits of the last token, int32 greedy token on device)");
   m.def("decode_batch", &decode_batch,
-        "batched decode of B <= 8 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
+        "batched decode of B <= 64 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
         "returns (fp32 logits [B, V], int32 greedy tokens [B] on device)");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");

@@ -288,7 +288,7 @@ def test_paged_prefill_entry_point_rejects_bad_arguments_before_launch(lib):
     assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE
 
 def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
-    """``mk_decode_batch`` checks the batch size (1..8), shape, vocabulary (a multiple of 16: the LM
+    """``mk_decode_batch`` checks the batch size (1..64), shape, vocabulary (a multiple of 16: the LM
     head's skinny product takes 16 rows per workgroup), workspace size and alignment before any HIP
     call; ``mk_decode_batch_workspace_bytes`` is 0 for an unsupported batch."""
     vp, i32 = ctypes.c_void_p, ctypes.c_int
@@ -301,9 +301,10 @@ def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
     ws.restype = ctypes.c_size_t
     ws.argtypes = [ctypes.POINTER(Dims), i32, i32]
     good = Dims(1024, 3072, 28, 151936)
-    assert ws(ctypes.byref(good), 0, 512) == 0 and ws(ctypes.byref(good), 9, 512) == 0
+    assert ws(ctypes.byref(good), 0, 512) == 0 and ws(ctypes.byref(good), 65, 512) == 0
     n8 = ws(ctypes.byref(good), 8, 4096)
     assert n8 > ws(ctypes.byref(good), 1, 512) > 0 and n8 % 256 == 0
+    assert ws(ctypes.byref(good), 64, 4096) > n8
 
     f = lib.mk_decode_batch
     f.restype = i32
@@ -315,7 +316,7 @@ def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
         return f(ctypes.byref(dims), batch, d, d, *([d] * 8), max_seq, d, None, workspace, nb, None)
 
     assert call(batch=0) == HIP_ERROR_INVALID_VALUE
-    assert call(batch=9) == HIP_ERROR_INVALID_VALUE
+    assert call(batch=65) == HIP_ERROR_INVALID_VALUE
     assert call(Dims(2048, 3072, 28, 151936)) == HIP_ERROR_INVALID_VALUE
     assert call(Dims(1024, 3072, 28, 151930)) == HIP_ERROR_INVALID_VALUE  # vocabulary not a multiple of 16
     assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE

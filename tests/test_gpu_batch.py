@@ -47,11 +47,14 @@ def _decode_batch(sess, toks, pos, kd, vd):
     ("mini", (5, 40, 100, 300), 6),
     ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4),
     ("mini17", (33, 200, 90), 4),
+    ("mini", tuple(3 + 11 * i for i in range(20)), 2),  # 20 sequences: 3 column blocks of 8 (of 4)
+    ("mini", tuple(1 + 5 * i for i in range(64)), 1),   # the largest batch: 8 column blocks
 ])
 def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, request):
-    """Sequences of different lengths in one batch (so their attention spans 1 to 2 key splits of
-    256, and a sequence ends a split exactly at 256): every step, each sequence's logits and greedy
-    token against the restatement on the kernel's cache for that sequence, and its new K/V rows."""
+    """Sequences of different lengths in one batch (so their attention spans 1 to 8 key splits of
+    64, and sequences end a split exactly at 64 and 256): every step, each sequence's logits and
+    greedy token against the restatement on the kernel's cache for that sequence, and its new K/V
+    rows. Up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3 and 8."""
     sess = request.getfixturevalue(shape_fixture)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
