@@ -1469,6 +1469,9 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   } while (0)
   MKB_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, keys, B, bad);
   const int cb = column_blocks(B);
+  // attention workgroups per sequence and K/V head (each loops over its splits): about 1024 in all,
+  // 16 at most (the grid cannot follow the device-side positions, so it must not be mostly idle)
+  const int gx = B <= 8 ? 16 : B <= 16 ? 8 : B <= 32 ? 4 : 2;
   const dim3 rows((B + 3) / 4);
   for (int l = 0; l < L; ++l) {
     const mk_layer_weights& lw = layers[l];
@@ -1480,7 +1483,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
     if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st)) != hipSuccess) return e;
-    MKB_LAUNCH(battn_partial_kernel, dim3(S < 16 ? S : 16, HKV, B), dim3(256), 0, st, raw, positions,
+    MKB_LAUNCH(battn_partial_kernel, dim3(S < gx ? S : gx, HKV, B), dim3(256), 0, st, raw, positions,
                (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
                v_cache, L, l, max_seq, apart, S, bad);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
