@@ -1506,10 +1506,19 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   // cores) and the greedy keys
   MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, final_norm,
              ah, al, A, B);
-  SkArgs lmh{};
-  lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
-  lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
-  if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st)) != hipSuccess) return e;
+  if (B <= 8 || dims.vocab % NT != 0) {
+    SkArgs lmh{};
+    lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
+    lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
+    if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st)) != hipSuccess) return e;
+  } else {
+    // beyond one column block the skinny product re-reads every row's activations per 16 table
+    // rows; a 128-row tile of the table reads them once per 128 (the B rows are one row tile)
+    GemmArgs gl{};
+    gl.ah = ah; gl.al = al; gl.lda = A; gl.M = B; gl.N = dims.vocab; gl.K = H;
+    gl.w0 = lm_head; gl.part = logits;  // logits[b][v], no residual
+    MKB_LAUNCH(gemm_kernel<EPI_RESID>, dim3(dims.vocab / NT, 1, 1), dim3(256), 0, st, gl);
+  }
   MKB_LAUNCH(logits_argmax_kernel, dim3((dims.vocab + 4095) / 4096, B), dim3(256), 0, st, logits, dims.vocab, keys, bad);
   if (out_tokens) MKB_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, keys, B, bad, out_tokens);
 #undef MKB_LAUNCH
