@@ -1,5 +1,7 @@
-// Batched prefill of a Qwen3-shaped model on MI355X (gfx950): all prompt tokens at once, layer by
-// layer, writing the decode kernel's K/V cache layout [L][8][max_seq][128] directly.
+// The layer-by-layer engine of the library on MI355X (gfx950): the batched prefill of a Qwen3-shaped
+// model (all prompt tokens at once, layer by layer, writing the decode kernel's K/V cache layout
+// [L][8][max_seq][128] -- or its paged layout -- directly) and the batched decode of up to 64
+// sequences (second half of this file).
 //
 // The reference prefills with Transformers on the GPU and copies its cache into the kernel's
 // layout (/root/reference/model.py:72-87); the decode kernel of this library could also prefill by
@@ -588,15 +590,12 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Final RMSNorm of rows row0 .. row0 + R - 1 of x and the tied LM head with fused greedy argmax
-// (/root/reference/megakernel.cu:876-893 and model.py:97): logits[r][v] = E[v] . norm(x[row0 + r]);
-// keys[r] = max over v of (order-preserving bf16 of the logit) << 32 | ~v, so equal bf16 values
-// prefer the lowest index.
-// Every workgroup normalises the R rows into LDS (bf16 hi/lo), then its 8 waves stream vocabulary
-// rows (row v to wave v % (8 * grid)), 4 rows in flight per wave.
+// Final RMSNorm of row `row` of x (the prompt's last token) and the tied LM head with fused greedy
+// argmax (/root/reference/megakernel.cu:876-893 and model.py:97): logits[v] = E[v] . norm(x[row]);
+// *key = max over v of (order-preserving bf16 of the logit) << 32 | ~v, so equal bf16 values prefer
+// the lowest index. Every workgroup normalises the row into LDS (bf16 hi/lo), then its 8 waves
+// stream vocabulary rows (row v to wave v % (8 * grid)), 4 rows in flight per wave.
 // ------------------------------------------------------------------------------------------------
-constexpr int LM_MAXR = 8;
-
 __device__ __forceinline__ u64 argmax_key(float logit, int idx) {
   uint32_t u = (uint32_t)f32_to_bf16(logit) << 16;
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -604,17 +603,16 @@ __device__ __forceinline__ u64 argmax_key(float logit, int idx) {
 }
 
 template <int H>
-__global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, int R,
-                                                      const uint16_t* final_norm, const uint16_t* lm_head, int vocab,
-                                                      float* logits, u64* keys, const int32_t* bad) {
+__global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row, const uint16_t* final_norm,
+                                                      const uint16_t* lm_head, int vocab, float* logits, u64* key,
+                                                      const int32_t* bad) {
   constexpr int C = H / 512;  // 16-byte chunks per lane of one vocabulary row
-  __shared__ __attribute__((aligned(16))) uint4 xs[2][LM_MAXR][H / 8];
-  __shared__ u64 best[8][LM_MAXR];
+  __shared__ __attribute__((aligned(16))) uint4 xs[2][H / 8];
+  __shared__ u64 best[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // normalise: wave w < R handles row w
-  if (w < R) {
+  if (w == 0) {  // normalise
     constexpr int E = H / 64;
-    const float* xr = x + (size_t)(row0 + w) * H + E * lane;
+    const float* xr = x + (size_t)row * H + E * lane;
     float v[E];
 #pragma unroll
     for (int k = 0; k < E; ++k) v[k] = xr[k];
@@ -628,7 +626,7 @@ __global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, 
       unpack8(*reinterpret_cast<const uint4*>(final_norm + E * lane + k), wv);
 #pragma unroll
       for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
-      split8(y, xs[0][w][(E * lane + k) / 8], xs[1][w][(E * lane + k) / 8]);
+      split8(y, xs[0][(E * lane + k) / 8], xs[1][(E * lane + k) / 8]);
     }
   }
   __syncthreads();
@@ -636,9 +634,7 @@ __global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, 
   auto dot2 = [](uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
   };
-  u64 mine[LM_MAXR];
-#pragma unroll
-  for (int r = 0; r < LM_MAXR; ++r) mine[r] = 0;
+  u64 mine = 0;
   const int stride = 8 * gridDim.x;
   const bool failed = *bad != 0;  // an input token was out of range: NaN logits
   constexpr int LP = 4;
@@ -653,36 +649,29 @@ __global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row0, 
 #pragma unroll
     for (int p = 0; p < LP; ++p) {
       const int v = v0 + p * stride;
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int r = 0; r < LM_MAXR; ++r) {
-        if (r >= R) break;
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int k = 0; k < C; ++k) {
-          const uint4 h = xs[0][r][64 * k + lane], l = xs[1][r][64 * k + lane];
-          s0 = dot2(wr[p][k].x, h.x, s0); s1 = dot2(wr[p][k].x, l.x, s1);
-          s0 = dot2(wr[p][k].y, h.y, s0); s1 = dot2(wr[p][k].y, l.y, s1);
-          s0 = dot2(wr[p][k].z, h.z, s0); s1 = dot2(wr[p][k].z, l.z, s1);
-          s0 = dot2(wr[p][k].w, h.w, s0); s1 = dot2(wr[p][k].w, l.w, s1);
-        }
-        const float s = wave_sum(s0 + s1);
-        if (v < vocab) {
-          if (lane == 0) logits[(size_t)r * vocab + v] = failed ? __builtin_nanf("") : s;
-          const u64 k = argmax_key(s, v);
-          mine[r] = mine[r] > k ? mine[r] : k;
-        }
+      for (int k = 0; k < C; ++k) {
+        const uint4 h = xs[0][64 * k + lane], l = xs[1][64 * k + lane];
+        s0 = dot2(wr[p][k].x, h.x, s0); s1 = dot2(wr[p][k].x, l.x, s1);
+        s0 = dot2(wr[p][k].y, h.y, s0); s1 = dot2(wr[p][k].y, l.y, s1);
+        s0 = dot2(wr[p][k].z, h.z, s0); s1 = dot2(wr[p][k].z, l.z, s1);
+        s0 = dot2(wr[p][k].w, h.w, s0); s1 = dot2(wr[p][k].w, l.w, s1);
+      }
+      const float s = wave_sum(s0 + s1);
+      if (v < vocab) {
+        if (lane == 0) logits[v] = failed ? __builtin_nanf("") : s;
+        const u64 kv = argmax_key(s, v);
+        mine = mine > kv ? mine : kv;
       }
     }
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < LM_MAXR; ++r) best[w][r] = mine[r];
-  }
+  if (lane == 0) best[w] = mine;
   __syncthreads();
-  if (tid < R) {
-    u64 b = 0;
-    for (int q = 0; q < 8; ++q) b = b > best[q][tid] ? b : best[q][tid];
-    atomicMax(keys + tid, b);
+  if (tid == 0) {
+    u64 m = 0;
+    for (int q = 0; q < 8; ++q) m = m > best[q] ? m : best[q];
+    atomicMax(key, m);
   }
 }
 
@@ -1217,7 +1206,7 @@ static Layout layout(int H, int I, int M) {
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
   const int sp = M <= SMALL_M ? 3 : (so > sd ? so : sd);
   L.part = take(sp > 1 ? (size_t)sp * M * H * 4 : 0);
-  L.keys = take(LM_MAXR * 8);
+  L.keys = take(8);
   L.bad = take(4);
   L.bytes = o;
   return L;
@@ -1337,7 +1326,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     MKP_LAUNCH(bnorm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
                sd, nullptr, nullptr, nullptr, A, M);
   // the last row's logits and greedy token
-  MKP_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, wk.x, M - 1, 1, final_norm, lm_head, dims.vocab, logits,
+  MKP_LAUNCH(lm_head_kernel<H>, dim3(256), dim3(512), 0, st, wk.x, M - 1, final_norm, lm_head, dims.vocab, logits,
              wk.keys, wk.bad);
   if (out_token) MKP_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad, out_token);
 #undef MKP_LAUNCH
