@@ -167,6 +167,9 @@ hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, in
 
 /*
  * Batched decode: `batch` (1..64) independent sequences advance by one token each in one call.
+ * Two engines: up to 8 sequences of the Qwen3-0.6B shape run as one persistent kernel (256
+ * workgroups exchanging data through epoch-tagged words, the batch as the columns of the matrix-core
+ * tiles); other batches run layer by layer (a few kernels per layer). mk_set_batch_engine chooses.
  * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a
  * device-side loop can advance them): it writes its K/V rows at positions[b] of its own cache and
  * attends over [0, positions[b]]. k_cache/v_cache are bf16 [batch][num_layers][8][max_seq_len][128]
@@ -253,6 +256,20 @@ hipError_t mk_decode_steps_paged(const mk_model_dims* dims, int32_t* tokens, int
  * No reference counterpart: the reference surfaces errors only through the launch status. */
 hipError_t mk_status(uint32_t* status);
 
+/* Engine of mk_decode_batch for the calling process: 0 automatic (the persistent kernel where it
+ * applies: the Qwen3-0.6B shape, 1..8 sequences, at most 32 layers, a device with 256 CUs), 1 always
+ * the layer-by-layer engine, 2 the persistent kernel where it applies. Both give each sequence
+ * mk_decode's numerics. hipErrorInvalidValue for another value. No reference counterpart. */
+hipError_t mk_set_batch_engine(int engine);
+
+/* Phase trace of the persistent batched kernel: with a device buffer of at least
+ * mk_batch_trace_bytes() bytes, later launches store s_memrealtime stamps (100 MHz) per workgroup
+ * (index j * 8 + xcd), layer (33 rows of 16 stamps; row 32: kernel start, LM head start and end) at
+ * fixed points of each layer; NULL turns it off. For profiling (megakernel.batch_trace). No
+ * reference counterpart. */
+hipError_t mk_set_batch_trace(uint64_t* device_buffer, size_t bytes);
+size_t mk_batch_trace_bytes(void);
+
 /* Clears the status words and the exchange words of every workspace of the current device and
  * restarts their launch sequences. Synchronizes with the device. No reference counterpart. */
 hipError_t mk_reset(void);
@@ -260,7 +277,8 @@ hipError_t mk_reset(void);
 /* Sets status bit 4 on every workspace of the current device, so that every later launch drains at
  * once (all its waits give up, NaN logits, token -1) until mk_reset: lets a caller abandon work it
  * has queued (a long mk_decode_steps), and lets tests exercise the failure path with every kernel
- * still exiting normally. Synchronizes with the device. No reference counterpart. */
+ * still exiting normally. The persistent batched kernel of mk_decode_batch drains too (NaN logits,
+ * token -1 for every sequence). Synchronizes with the device. No reference counterpart. */
 hipError_t mk_request_drain(void);
 
 /* Bytes of one exchange workspace set (the static array of mk_decode_noalloc has this size; each

@@ -1,0 +1,1008 @@
+// Persistent batched decode on MI355X (gfx950): up to 8 sequences of the Qwen3-0.6B shape advance
+// one token each in one launch of 256 workgroups, one per CU, with no grid barrier and no kernel
+// boundary between layers.
+//
+// The reference decodes one sequence per launch (/root/reference/megakernel.cu:744-994, a cooperative
+// grid with grid.sync() between phases). The layer-by-layer engine of this library runs a batch as
+// ~220 short kernels per step, and on MI355X every kernel boundary costs a few microseconds (launch,
+// cache write-back and invalidation across the 8 XCDs) on top of each kernel's own ramp. Here the
+// batch is the 16 columns of the matrix-core tile instead (sequence b's activations as bf16 hi in
+// column 2b and lo in column 2b + 1), and workgroups hand data to each other through 32-bit
+// "LL" words (value and epoch in one word) as the single-sequence decode kernel does:
+//
+//   XCD x owns K/V head x: its 512 q/k/v rows (16 per workgroup), its attention, its 256 input
+//   columns of o_proj (32 output rows per workgroup), 1/8 of the MLP (12 intermediates per
+//   workgroup) and those intermediates' columns of down_proj (32 rows per workgroup). Per layer:
+//     A  input RMSNorm -> QKV rows (MFMA)                       -> publish (local)
+//     B  split-K attention of one (sequence, key range) per workgroup, q/k norm + RoPE, cache write
+//                                                               -> publish partial (local)
+//     C  merge of every sequence's splits -> o_proj partial      -> publish (cross-XCD)
+//     D  workgroup j sums row block j over the 8 XCDs            -> republish (local)
+//     E  residual, post-attention RMSNorm -> gate/up + SiLU      -> publish (local)
+//     F  down_proj partial                                       -> publish (cross-XCD)
+//     G  workgroup j sums row block j over the 8 XCDs            -> republish (local)
+//   then the final norm and the tied LM head with the greedy keys (finish kernel: tokens).
+//
+// Every workgroup keeps the whole residual [B][1024] in LDS, bitwise identical across workgroups
+// (same data, same order). Waves 0-3 (comm) poll, publish and do the vector work; waves 4-11
+// (math) hold weights in registers, issued phases ahead, and run the MFMA tiles and the attention.
+// Workgroups learn their XCD from the hardware register and their index in it from a ticket counter,
+// so the exchange layout never depends on how the dispatcher placed the grid. Every wait is
+// bounded; a timeout (or a host drain request) aborts the launch, which then reports NaN logits
+// and token -1 for every sequence.
+//
+// Numerics are the single-sequence kernel's: fp32 residual, fp32 RMSNorm (scale applied to the
+// product outputs, a linear map), fp32 softmax, exchanged values rounded to 24 bits, bf16 new K/V.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <mutex>
+
+#include "mk_device.h"
+#include "mk_batch.h"
+#include "mk_layers.h"
+
+namespace mkb {
+using namespace mk;
+using namespace mkp;
+
+constexpr int NXCD = 8, WPX = 32, NWG = NXCD * WPX;
+constexpr int NCW = 4, NMW = 8, NWAVE = NCW + NMW, NT = 64 * NWAVE;  // 768 threads
+constexpr int CL = 64 * NCW;            // comm lanes
+constexpr int BM = 8;                   // sequences per launch (hi and lo of 8 fill the 16 columns)
+constexpr int H = 1024, I = 3072, IX = I / NXCD;
+constexpr int QX = 4 * D;               // q (2 heads), k, v rows of one K/V head: 512
+constexpr int QR = QX / WPX;            // 16 rows per workgroup
+constexpr int OR = H / WPX;             // 32 o_proj rows (and down_proj rows) per workgroup
+constexpr int GI = IX / WPX;            // 12 intermediates per workgroup
+constexpr int APW = 2 * D + 4;          // attention partial: acc[2][128], m0, l0, m1, l1
+constexpr int KST = H + 8;              // LDS row stride of the MFMA B operand (bf16): conflict-free reads
+constexpr int RST = 20;                 // LDS row stride of the reduction tiles (floats): conflict-free writes
+constexpr int MAXL = 32;
+constexpr int NG = 4 * NMW;             // 16-lane attention groups per workgroup
+constexpr int RB = 4;                   // keys per group and round of K/V loads
+constexpr uint32_t SPIN_LIMIT = 1u << 22;
+static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
+
+// Where the math waves issue each group of weight (and K/V) loads, as points of their layer loop:
+//   0 after A1 (before the QKV tile)      1 after A2        2 after B1 (before the attention)
+//   3 after the split partial's publish   4 after C1        5 after C2 (before the o_proj tile)
+//   6 after C3    7 after E1 (before the gate/up tile)     8 after E2    9 after F1    10 after F2
+// (points 2 and 3 are point 1 on a workgroup without a key range). gate/up and down rows are issued
+// in the layer that uses them (at most 6 and 8), QKV, o_proj and the first K/V round for the next
+// layer (at least 1, 6 and 3). A burst of loads delays any poll of the same CU issued after it, so
+// each goes where the comm waves' next poll is furthest away. Measured at 8 sequences of 257 keys
+// (0.6B): gate/up+down after the attention publish 797 us per step, gate/up after C1 729, and the
+// defaults below 708.
+// Polls of up to MKB_TWO_MAX chunks per lane keep two rounds of loads in flight.
+#ifndef MKB_TWO_MAX
+#define MKB_TWO_MAX 4
+#endif
+#ifndef MKB_GU_AT
+#define MKB_GU_AT 4
+#endif
+#ifndef MKB_DN_AT
+#define MKB_DN_AT 8
+#endif
+#ifndef MKB_QKV_AT
+#define MKB_QKV_AT 6
+#endif
+#ifndef MKB_O_AT
+#define MKB_O_AT 10
+#endif
+#ifndef MKB_KV_AT
+#define MKB_KV_AT 8
+#endif
+static_assert(MKB_GU_AT <= 6 && MKB_DN_AT <= 8 && MKB_QKV_AT >= 1 && MKB_O_AT >= 6 && MKB_KV_AT >= 3,
+              "load schedule");
+
+// Exchange area (32-bit words), zeroed before every launch: epoch 0 never matches.
+constexpr size_t W_QX = 0;                                   // [8][BM][512]    q/k/v sums (local)
+constexpr size_t W_AX = W_QX + (size_t)NXCD * BM * QX;       // [8][32][260]    split partials (local)
+constexpr size_t W_OX = W_AX + (size_t)NXCD * WPX * APW;     // [32][8][BM][32] o_proj partials (cross)
+constexpr size_t W_OL = W_OX + (size_t)WPX * NXCD * BM * OR; // [8][BM][H]      o_proj sums (local)
+constexpr size_t W_MX = W_OL + (size_t)NXCD * BM * H;        // [8][BM][IX]     silu(gate) * up (local)
+constexpr size_t W_DX = W_MX + (size_t)NXCD * BM * IX;       // [32][8][BM][32] down partials (cross)
+constexpr size_t W_DL = W_DX + (size_t)WPX * NXCD * BM * OR; // [8][BM][H]      down sums (local)
+constexpr size_t W_TICK = W_DL + (size_t)NXCD * BM * H;      // [8] ticket counters, 64 words apart
+constexpr size_t W_ABORT = W_TICK + NXCD * 64;               // nonzero: the launch gave up
+constexpr size_t W_BAD = W_ABORT + 64;                       // nonzero: a token or position was out of range
+constexpr size_t W_ZERO = W_BAD + 64;                        // words zeroed per launch
+constexpr size_t W_KEYS = W_ZERO;                            // u64 [NWG][BM] greedy keys per workgroup
+constexpr size_t W_END = W_KEYS + 2 * (size_t)NWG * BM;
+constexpr size_t WS_BYTES = W_END * 4;
+static_assert(W_AX % 4 == 0 && W_OX % 4 == 0 && W_OL % 4 == 0 && W_MX % 4 == 0 && W_DX % 4 == 0 &&
+                  W_DL % 4 == 0 && W_KEYS % 2 == 0,
+              "16-byte chunks");
+
+struct BArgs {
+  const int32_t* tokens;
+  const int32_t* positions;
+  const uint16_t* embed;
+  const uint16_t* lm_head;
+  const uint16_t* final_norm;
+  const uint16_t* cos_tab;
+  const uint16_t* sin_tab;
+  uint16_t* k_cache;  // [B][L][8][max_seq][128]
+  uint16_t* v_cache;
+  float* logits;      // [B][vocab]
+  uint32_t* ws;
+  int B, L, vocab, max_seq, drain;
+  uint64_t* trace;  // optional phase stamps (mk_set_batch_trace), null in normal operation
+  mk_layer_weights lw[MAXL];
+};
+
+// Phase trace: per workgroup (j * 8 + x) and layer, TRACE_SLOTS s_memrealtime stamps (100 MHz) taken
+// by thread 0 (comm wave 0) at fixed points; row MAXL holds kernel start, LM-head start and end.
+constexpr int TRACE_SLOTS = 24;
+constexpr size_t TRACE_BYTES = (size_t)NWG * (MAXL + 1) * TRACE_SLOTS * 8;
+__device__ __forceinline__ void mark(const BArgs& a, int x, int j, int row, int slot, int who = 0) {
+  if (a.trace && threadIdx.x == who)
+    a.trace[((size_t)(j * NXCD + x) * (MAXL + 1) + row) * TRACE_SLOTS + slot] = __builtin_amdgcn_s_memrealtime();
+}
+
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+struct Smem {
+  float xres[BM][H];             // residual
+  uint16_t act[16][KST];         // MFMA B operand: column 2b = hi, 2b + 1 = lo of sequence b
+  float red[NMW][16][RST];       // per-wave MFMA results
+  float gacc[NG][2][D];          // attention group partials
+  float gml[NG][4];
+  float stg[WPX * APW];          // polled split partials
+  float raw[QX];                 // polled q/k/v sums of this workgroup's sequence
+  float ssw[NCW][BM];            // per comm wave sums of squares
+  uint16_t cs[2][D];             // cos, sin at this workgroup's split's position
+  uint16_t qkn[2][2][D];         // q_norm, k_norm weights, by layer parity
+  u64 wk[NWAVE][BM];             // LM head keys per wave
+  int pos[BM], tok[BM], f[BM], ns[BM], sb[WPX];
+  int x, j, nsplit, ks, bad;
+};
+
+// threadIdx.x with its origin hidden from the optimizer: lane offsets derived from it are recomputed
+// where they are used instead of being hoisted out of the layer loop and held in registers.
+__device__ __forceinline__ int tix() {
+  int v = threadIdx.x;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// LL word of v: v rounded at mantissa bit 8, epoch ep (1..255) in the low byte.
+__device__ __forceinline__ uint32_t llw(float v, uint32_t ep) { return ((__float_as_uint(v) + 0x80u) & 0xFFFFFF00u) | ep; }
+__device__ __forceinline__ float llv(uint32_t w) { return __uint_as_float(w & 0xFFFFFF00u); }
+
+// 4 LL words at word offset `off` (per lane) of the wave-uniform `base`: local words stay in the XCD's
+// L2, cross-XCD words are written through (device scope). The buffer descriptor is built from the
+// uniform base only; a per-lane base would make the compiler loop over the lanes' descriptors.
+template <bool CROSS>
+__device__ __forceinline__ void st4(uint32_t* base, int off, const float (&v)[4], uint32_t ep) {
+  const u4v w = {llw(v[0], ep), llw(v[1], ep), llw(v[2], ep), llw(v[3], ep)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, make_rsrc(base), off * 4, 0, CROSS ? CPOL_SC1 : 0);
+}
+__device__ __forceinline__ void st1(uint32_t* base, int off, float v, uint32_t ep) {
+  __builtin_amdgcn_raw_buffer_store_b32(llw(v, ep), make_rsrc(base), off * 4, 0, 0);
+}
+
+struct Ctl {
+  uint32_t* ws;
+  bool failed;
+};
+
+// Polls NK 16-byte chunks of LL words per lane, at byte offsets off[k] from base (device-scope loads),
+// until every epoch equals ep; the lanes of a wave wait together. Up to 4 chunks per lane two rounds
+// of loads are kept in flight, so data that lands while one round is out is seen by the next one. Bounded: past SPIN_LIMIT rounds, or once another workgroup has given
+// up (checked every 32 rounds), it sets the abort word and returns zeros.
+template <int NK>
+__device__ __forceinline__ void poll(Ctl& c, const uint32_t* base, const int (&off)[NK], uint32_t ep,
+                                     float (&v)[NK][4]) {
+  auto zero = [&]() {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0.f;
+  };
+  if (c.failed) { zero(); return; }
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
+  auto issue = [&](u4v (&r)[NK]) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) r[k] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, off[k], 0, CPOL_SC1));
+  };
+  auto ready = [&](const u4v (&r)[NK]) {
+    uint32_t bad = 0;
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bad |= (r[k][i] ^ ep) & 0xFFu;
+    return __ballot(bad != 0) == 0;
+  };
+  auto take = [&](const u4v (&r)[NK]) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[k][i] = llv(r[k][i]);
+  };
+  auto give_up = [&](uint32_t it) {
+    if ((it & 63u) == 62u && ld_dev_u32(c.ws + W_ABORT) != 0) { c.failed = true; return true; }
+    if (it > SPIN_LIMIT) {
+      st_dev_u32(c.ws + W_ABORT, 1u);
+      c.failed = true;
+      return true;
+    }
+    return false;
+  };
+  if constexpr (NK <= MKB_TWO_MAX) {
+    u4v r0[NK], r1[NK];
+    issue(r0);
+    for (uint32_t it = 0;; it += 2) {
+      issue(r1);
+      if (ready(r0)) { take(r0); return; }
+      issue(r0);
+      if (ready(r1)) { take(r1); return; }
+      if (give_up(it)) { zero(); return; }
+    }
+  } else {
+    u4v r0[NK];
+    for (uint32_t it = 0;; it += 2) {
+      issue(r0);
+      if (ready(r0)) { take(r0); return; }
+      if (give_up(it)) { zero(); return; }
+    }
+  }
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS operations only, weight loads stay in flight
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ---- comm-wave vector work ------------------------------------------------------------------------
+
+// The residual of every sequence after adding `src` (or, at layer 0, set to the embedding rows),
+// then x * w (w the RMSNorm weight) into the MFMA operand as bf16 hi/lo, and each comm wave's sums of
+// squares per sequence. Comm lane c holds elements 4c..4c+3 of every sequence.
+template <bool EMBED>
+__device__ __forceinline__ void residual_norm(Smem& sm, Ctl& c, const BArgs& a, const uint32_t* src, uint32_t ep,
+                                              const uint16_t* w) {
+  const int cl = tix(), e0 = 4 * cl;
+  float v[BM][4];
+  if constexpr (EMBED) {
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      const int tok = sm.tok[b < a.B ? b : 0];
+      const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)tok * H + e0);
+      v[b][0] = bf16_lo(e.x); v[b][1] = bf16_hi(e.x); v[b][2] = bf16_lo(e.y); v[b][3] = bf16_hi(e.y);
+    }
+  } else {
+    int off[BM];
+#pragma unroll
+    for (int b = 0; b < BM; ++b) off[b] = ((b < a.B ? b : a.B - 1) * H + e0) * 4;
+    poll<BM>(c, src, off, ep, v);
+  }
+  const uint2 wr = *reinterpret_cast<const uint2*>(w + e0);
+  const float wv[4] = {bf16_lo(wr.x), bf16_hi(wr.x), bf16_lo(wr.y), bf16_hi(wr.y)};
+  const int wave = cl >> 6, lane = cl & 63;
+#pragma unroll
+  for (int b = 0; b < BM; ++b) {
+    if (b >= a.B) break;
+    float4* xr = reinterpret_cast<float4*>(&sm.xres[b][e0]);
+    float4 xv = *xr;
+    if constexpr (EMBED) xv = make_float4(v[b][0], v[b][1], v[b][2], v[b][3]);
+    else { xv.x += v[b][0]; xv.y += v[b][1]; xv.z += v[b][2]; xv.w += v[b][3]; }
+    *xr = xv;
+    const float y[4] = {xv.x * wv[0], xv.y * wv[1], xv.z * wv[2], xv.w * wv[3]};
+    uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
+    uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
+    *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
+    *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
+    const float ss = wave_sum(xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w);
+    if (lane == 0) sm.ssw[wave][b] = ss;
+  }
+}
+
+__device__ __forceinline__ float norm_scale(const Smem& sm, int b) {
+  return rsqrtf((((sm.ssw[0][b] + sm.ssw[1][b]) + sm.ssw[2][b]) + sm.ssw[3][b]) / (float)H + EPS);
+}
+
+// Sum over the waves W0..W0+NW-1 of row r of the MFMA results, hi + lo columns of sequence b (all
+// LDS reads issued before the adds).
+template <int W0, int NW>
+__device__ __forceinline__ float red_sum(const Smem& sm, int r, int b) {
+  float v[NW][2];
+#pragma unroll
+  for (int m = 0; m < NW; ++m) {
+    v[m][0] = sm.red[W0 + m][r][2 * b];
+    v[m][1] = sm.red[W0 + m][r][2 * b + 1];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int m = 0; m < NW; ++m) s += v[m][0] + v[m][1];
+  return s;
+}
+
+// Workgroup j of XCD x sums row block j (OR rows of every sequence) over the 8 XCDs' partials at
+// `cross` in a fixed order and republishes it in its XCD at `local`. Comm wave 0, lane (b, quad).
+__device__ __forceinline__ void gather(Smem& sm, Ctl& c, const BArgs& a, size_t cross, size_t local, uint32_t ep) {
+  const int lane = tix();  // wave 0
+  const int q8 = min(lane, 8 * a.B - 1), b = q8 >> 3, q = q8 & 7;
+  int off[NXCD];
+#pragma unroll
+  for (int xs = 0; xs < NXCD; ++xs) off[xs] = (int)(((((size_t)sm.j * NXCD + xs) * BM + b) * OR + 4 * q) * 4);
+  float v[NXCD][4];
+  poll<NXCD>(c, a.ws + cross, off, ep, v);
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = v[0][i];
+#pragma unroll
+    for (int xs = 1; xs < NXCD; ++xs) s[i] += v[xs][i];
+  }
+  if (lane < 8 * a.B) st4<false>(a.ws + local + (size_t)sm.x * BM * H + sm.j * OR, b * H + 4 * q, s, ep);
+}
+
+// Publishes the workgroup's OR output rows of every sequence (waves 4t..4t+3 computed tile t) as
+// cross-XCD partials: comm lane (b, quad).
+__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep) {
+  const int cl = tix();
+  if (cl >= 8 * a.B) return;
+  const int b = cl >> 3, q = cl & 7, t = q >> 2;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = t ? red_sum<4, 4>(sm, 4 * (q & 3) + i, b) : red_sum<0, 4>(sm, 4 * (q & 3) + i, b);
+  st4<true>(a.ws + cross + ((size_t)sm.j * NXCD + sm.x) * BM * OR, b * OR + 4 * q, v, ep);
+}
+
+// ---- math-wave weight loads (lane: li = row of the tile, g = 8-element K group) -------------------
+
+struct MathLane {
+  int m, li, g;  // m: math wave index, wave-uniform (readfirstlane)
+};
+
+constexpr int CPOL_NT = 2;  // non-temporal: each weight byte is read once per step
+__device__ __forceinline__ uint4 ldnt(__amdgpu_buffer_rsrc_t rs, int off) {
+  const u4v v = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, CPOL_NT));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Weight rows are read through buffer descriptors with a wave-uniform base and a 32-bit lane offset
+// (row li of the tile, K group g): nothing 64-bit per lane stays live across the layer loop.
+// QKV: workgroup j's 16 rows of the XCD's 512 (all in one of q, k, v); wave m takes K steps 4m..4m+3.
+__device__ __forceinline__ void load_qkv(uint4 (&w)[4], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
+  const uint16_t* base = j < 16   ? (const uint16_t*)lw.q_weight + ((size_t)2 * D * x + QR * j) * H
+                         : j < 24 ? (const uint16_t*)lw.k_weight + ((size_t)D * x + QR * (j - 16)) * H
+                                  : (const uint16_t*)lw.v_weight + ((size_t)D * x + QR * (j - 24)) * H;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
+  const int off = (ml.li * H + 32 * 4 * ml.m + 8 * ml.g) * 2;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) w[s] = ldnt(rs, off + 64 * s);
+}
+// o_proj: rows 32j + 16 (m / 4) + li, the XCD's 256 input columns; K steps 2 (m % 4), +1.
+__device__ __forceinline__ void load_o(uint4 (&w)[2], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc((const uint16_t*)lw.o_proj_weight + (size_t)OR * j * (HQ * D) + 2 * D * x);
+  const int off = ((16 * (ml.m >> 2) + ml.li) * (HQ * D) + 64 * (ml.m & 3) + 8 * ml.g) * 2;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) w[s] = ldnt(rs, off + 64 * s);
+}
+// gate (waves 0-3) or up (waves 4-7) rows of the workgroup's 12 intermediates (rows 12-15 of the tile
+// are empty); K steps 8 (m % 4) .. +7.
+__device__ __forceinline__ void load_gu(uint4 (&w)[8], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
+  if (ml.li >= GI) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) w[s] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const uint16_t* m0 = (const uint16_t*)(ml.m < 4 ? lw.gate_proj_weight : lw.up_proj_weight);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(m0 + ((size_t)IX * x + GI * j) * H);
+  const int off = (ml.li * H + 256 * (ml.m & 3) + 8 * ml.g) * 2;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) w[s] = ldnt(rs, off + 64 * s);
+}
+// down_proj: rows 32j + 16 (m / 4) + li, the XCD's 384 intermediate columns; K steps 3 (m % 4) .. +2.
+__device__ __forceinline__ void load_down(uint4 (&w)[3], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc((const uint16_t*)lw.down_proj_weight + (size_t)OR * j * I + IX * x);
+  const int off = ((16 * (ml.m >> 2) + ml.li) * I + 96 * (ml.m & 3) + 8 * ml.g) * 2;
+#pragma unroll
+  for (int s = 0; s < 3; ++s) w[s] = ldnt(rs, off + 64 * s);
+}
+
+// MFMA over NS K steps starting at step ks0 of the LDS operand; result to the wave's reduction tile.
+template <int NS>
+__device__ __forceinline__ void mma_to_red(Smem& sm, const uint4 (&w)[NS], int ks0, const MathLane& ml) {
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint4 b = *reinterpret_cast<const uint4*>(&sm.act[ml.li][32 * (ks0 + s) + 8 * ml.g]);
+    c = mfma(w[s], b, c);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sm.red[ml.m][4 * ml.g + r][ml.li] = c[r];
+}
+
+// ---- attention ------------------------------------------------------------------------------------
+
+struct Split {
+  bool on;
+  int b, s, k0, k1, pos;
+};
+
+// K/V rows of round `round` of this group's keys (positions k0 + gi + NG (RB round + u)); keys past the
+// split are not loaded.
+__device__ __forceinline__ void load_kv(uint4 (&kw)[RB], uint4 (&vw)[RB], const BArgs& a, const Split& sp, int layer,
+                                        int x, int gi, int t, int round) {
+  const size_t head = (((size_t)sp.b * a.L + layer) * HKV + x) * a.max_seq * D;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + head), rv = make_rsrc(a.v_cache + head);
+#pragma unroll
+  for (int u = 0; u < RB; ++u) {
+    const int p = sp.k0 + gi + NG * (RB * round + u);
+    kw[u] = vw[u] = make_uint4(0, 0, 0, 0);
+    if (p < sp.k1) {
+      const int off = (p * D + 8 * t) * 2;
+      const u4v k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      const u4v v = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+      kw[u] = make_uint4(k[0], k[1], k[2], k[3]);
+      vw[u] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+
+__device__ __forceinline__ void softmax_step(float sc, const float (&v)[8], float& m, float& l, float (&acc)[8]) {
+  const float nm = fmaxf(m, sc);
+  const float cm = __expf(m - nm), e = __expf(sc - nm);
+  l = l * cm + e;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = acc[i] * cm + e * v[i];
+  m = nm;
+}
+
+
+// Merge of every sequence's split partials (polled into LDS) into the o_proj operand: output
+// (b, head h, dim d) per thread, all waves, max-first over the sequence's splits.
+__device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a) {
+  for (int o = tix(); o < a.B * 2 * D; o += NT) {
+    const int b = o >> 8, h = (o >> 7) & 1, d = o & (D - 1);
+    const float* p = sm.stg + (size_t)sm.f[b] * APW;
+    const int n = sm.ns[b];
+    float M = -INFINITY;
+    for (int s = 0; s < n; ++s) M = fmaxf(M, p[s * APW + 2 * D + 2 * h]);
+    float A = 0.f, Ls = 0.f;
+    for (int s = 0; s < n; ++s) {
+      const float e = __expf(p[s * APW + 2 * D + 2 * h] - M);
+      A = fmaf(p[s * APW + h * D + d], e, A);
+      Ls = fmaf(p[s * APW + 2 * D + 2 * h + 1], e, Ls);
+    }
+    const float val = A / Ls;
+    const uint16_t hi = f32_to_bf16(val);
+    sm.act[2 * b][h * D + d] = hi;
+    sm.act[2 * b + 1][h * D + d] = f32_to_bf16(val - bf16_to_f32(hi));
+  }
+}
+
+// Every split partial of the XCD into LDS (nsplit * 65 chunks of 16 bytes, NK per comm lane).
+template <int NK>
+__device__ __forceinline__ void poll_splits(Smem& sm, Ctl& c, const BArgs& a, int x, uint32_t ep) {
+  const int tid = tix(), nch = sm.nsplit * (APW / 4);
+  int off[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) off[k] = 16 * min(tid + CL * k, nch - 1);
+  float v[NK][4];
+  poll<NK>(c, a.ws + W_AX + (size_t)x * WPX * APW, off, ep, v);
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    if (tid + CL * k < nch)
+      *reinterpret_cast<float4*>(&sm.stg[4 * (tid + CL * k)]) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+}
+
+// The two roles run separate layer loops that meet at the same sequence of LDS barriers:
+// A1 A2 [B1 B2] C1 C2 C3 E1 E2 F1 F2 per layer (B1, B2 on workgroups with an attention split).
+
+// Comm waves (threads 0..255): polls, publishes, norms, reductions of the MFMA tiles.
+__device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, const Split& sp, int x, int j) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int l = 0; l < a.L; ++l) {
+    const mk_layer_weights& lw = a.lw[l];
+    const uint32_t ep = (uint32_t)l + 1;
+    const int tid = tix();
+    // ---- A: residual + input norm (x * w into the operand; the scale goes on the outputs)
+    mark(a, x, j, l, 0);
+    if (l == 0) residual_norm<true>(sm, c, a, nullptr, 0, (const uint16_t*)lw.norm_weight);
+    else residual_norm<false>(sm, c, a, a.ws + W_DL + (size_t)x * BM * H, ep - 1, (const uint16_t*)lw.norm_weight);
+    mark(a, x, j, l, 1);
+    uint4 qn = make_uint4(0, 0, 0, 0);  // this layer's q_norm / k_norm weights, into LDS before B1
+    if (sp.on && tid < 32)
+      qn = *reinterpret_cast<const uint4*>((const uint16_t*)(tid < 16 ? lw.q_norm_weight : lw.k_norm_weight) +
+                                           8 * (tid & 15));
+    lds_barrier();  // A1
+    lds_barrier();  // A2
+    mark(a, x, j, l, 2);
+    if (tid < 4 * a.B) {  // QKV rows: lane (b, 4 rows)
+      const int b = tid >> 2, r0 = 4 * (tid & 3);
+      const float rs = norm_scale(sm, b);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = red_sum<0, NMW>(sm, r0 + i, b) * rs;
+      st4<false>(a.ws + W_QX + (size_t)x * BM * QX + QR * j, b * QX + r0, v, ep);
+    }
+    mark(a, x, j, l, 3);
+    // ---- B: this workgroup's sequence's q/k/v sums for the attention
+    if (sp.on) {
+      if (tid < QX / 4) {
+        int off[1] = {(int)((((size_t)x * BM + sp.b) * QX + 4 * tid) * 4)};
+        float v[1][4];
+        poll<1>(c, a.ws + W_QX, off, ep, v);
+        *reinterpret_cast<float4*>(&sm.raw[4 * tid]) = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
+        if (tid < 32) *reinterpret_cast<uint4*>(&sm.qkn[l & 1][tid >> 4][8 * (tid & 15)]) = qn;
+      }
+      lds_barrier();  // B1
+      mark(a, x, j, l, 4);
+      lds_barrier();  // B2
+      mark(a, x, j, l, 5);
+    }
+    // ---- C: every split partial of the XCD into LDS
+    if (sm.nsplit * (APW / 4) <= 4 * CL) poll_splits<4>(sm, c, a, x, ep);
+    else poll_splits<(WPX * APW / 4 + CL - 1) / CL>(sm, c, a, x, ep);
+    mark(a, x, j, l, 6);
+    lds_barrier();  // C1
+    merge_splits(sm, a);
+    lds_barrier();  // C2
+    mark(a, x, j, l, 7);
+    lds_barrier();  // C3
+    mark(a, x, j, l, 8);
+    // ---- D, E: o_proj partials out, row block j summed over the XCDs, residual + post-attention norm
+    publish_rows(sm, a, W_OX, ep);
+    mark(a, x, j, l, 16);
+    if (wave == 0) gather(sm, c, a, W_OX, W_OL, ep);
+    mark(a, x, j, l, 9);
+    residual_norm<false>(sm, c, a, a.ws + W_OL + (size_t)x * BM * H, ep, (const uint16_t*)lw.post_attn_norm_weight);
+    mark(a, x, j, l, 10);
+    lds_barrier();  // E1
+    lds_barrier();  // E2
+    mark(a, x, j, l, 11);
+    // ---- F: SiLU outputs, then the XCD's SiLU outputs into the operand
+    if (tid < 3 * a.B) {
+      const int b = tid / 3, q = tid % 3;
+      const float rs = norm_scale(sm, b);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ii = 4 * q + i;
+        const float gt = red_sum<0, 4>(sm, ii, b) * rs, up = red_sum<4, 4>(sm, ii, b) * rs;
+        v[i] = gt / (1.f + expf(-gt)) * up;
+      }
+      st4<false>(a.ws + W_MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
+    }
+    {
+      constexpr int NK = (BM * IX / 4) / CL;  // 3
+      const int nch = a.B * (IX / 4);
+      int off[NK];
+#pragma unroll
+      for (int k = 0; k < NK; ++k) off[k] = (int)(((size_t)x * BM * IX + 4 * min(tid + CL * k, nch - 1)) * 4);
+      float v[NK][4];
+      poll<NK>(c, a.ws + W_MX, off, ep, v);
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        const int ci = tid + CL * k;
+        if (ci < nch) {
+          const int b = ci / (IX / 4), e0 = 4 * (ci % (IX / 4));
+          uint32_t h0 = pack_bf16x2(v[k][0], v[k][1]), h1 = pack_bf16x2(v[k][2], v[k][3]);
+          uint32_t l0 = pack_bf16x2(v[k][0] - bf16_lo(h0), v[k][1] - bf16_hi(h0));
+          uint32_t l1 = pack_bf16x2(v[k][2] - bf16_lo(h1), v[k][3] - bf16_hi(h1));
+          *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
+          *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
+        }
+      }
+    }
+    mark(a, x, j, l, 12);
+    lds_barrier();  // F1
+    lds_barrier();  // F2
+    mark(a, x, j, l, 13);
+    // ---- G: down partials out, row block j summed over the XCDs
+    publish_rows(sm, a, W_DX, ep);
+    mark(a, x, j, l, 17);
+    if (wave == 0) gather(sm, c, a, W_DX, W_DL, ep);
+    mark(a, x, j, l, 14);
+  }
+  // the last layer's sums, final norm
+  residual_norm<false>(sm, c, a, a.ws + W_DL + (size_t)x * BM * H, (uint32_t)a.L, a.final_norm);
+  lds_barrier();
+}
+
+// Math waves (threads 256..767): weights in registers (issued phases ahead), MFMA tiles, attention.
+__device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split& sp, int x, int j) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const MathLane ml{__builtin_amdgcn_readfirstlane(tid >> 6) - NCW, lane & 15, lane >> 4};
+  const int gi = 4 * ml.m + (lane >> 4), t = lane & 15;
+  const int nrounds = (sp.k1 - sp.k0 + NG * RB - 1) / (NG * RB);
+  uint4 wq[4], wo[2], wg[8], wd[3], kw[RB], vw[RB];
+  load_qkv(wq, a.lw[0], ml, x, j);
+  load_o(wo, a.lw[0], ml, x, j);
+  if (sp.on) load_kv(kw, vw, a, sp, 0, x, gi, t, 0);
+  for (int l = 0; l < a.L; ++l) {
+    const mk_layer_weights& lw = a.lw[l];
+    const uint32_t ep = (uint32_t)l + 1;
+    const bool next = l + 1 < a.L;
+    auto issue = [&](int p) {
+      if (p == MKB_GU_AT) load_gu(wg, lw, ml, x, j);
+      if (p == MKB_DN_AT) load_down(wd, lw, ml, x, j);
+      if (p == MKB_QKV_AT && next) load_qkv(wq, a.lw[l + 1], ml, x, j);
+      if (p == MKB_O_AT && next) load_o(wo, a.lw[l + 1], ml, x, j);
+      if (p == MKB_KV_AT && next && sp.on) load_kv(kw, vw, a, sp, l + 1, x, gi, t, 0);
+    };
+    lds_barrier();  // A1
+    issue(0);
+    mma_to_red<4>(sm, wq, 4 * ml.m, ml);
+    lds_barrier();  // A2
+    issue(1);
+    if (!sp.on) {
+      issue(2);
+      issue(3);
+    } else {
+      lds_barrier();  // B1
+      mark(a, x, j, l, 18, 64 * NCW);
+      issue(2);
+      float qa[8], qb[8], kn[8], vv[8];
+      {
+        float qw[8], kwn[8], cs[8], sn[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          qa[i] = sm.raw[8 * t + i];
+          qb[i] = sm.raw[D + 8 * t + i];
+          kn[i] = sm.raw[2 * D + 8 * t + i];
+          vv[i] = sm.raw[3 * D + 8 * t + i];
+        }
+        unpack8(*reinterpret_cast<const uint4*>(&sm.qkn[l & 1][0][8 * t]), qw);
+        unpack8(*reinterpret_cast<const uint4*>(&sm.qkn[l & 1][1][8 * t]), kwn);
+        unpack8(*reinterpret_cast<const uint4*>(&sm.cs[0][8 * (t & 7)]), cs);  // dims mod 64
+        unpack8(*reinterpret_cast<const uint4*>(&sm.cs[1][8 * (t & 7)]), sn);
+        head_norm_rope(qa, qw, cs, sn, t);
+        head_norm_rope(qb, qw, cs, sn, t);
+        head_norm_rope(kn, kwn, cs, sn, t);
+      }
+      const uint4 knew = make_uint4(pack_bf16x2(kn[0], kn[1]), pack_bf16x2(kn[2], kn[3]), pack_bf16x2(kn[4], kn[5]),
+                                    pack_bf16x2(kn[6], kn[7]));
+      const uint4 vnew = make_uint4(pack_bf16x2(vv[0], vv[1]), pack_bf16x2(vv[2], vv[3]), pack_bf16x2(vv[4], vv[5]),
+                                    pack_bf16x2(vv[6], vv[7]));
+      if (gi == 0 && sp.pos < sp.k1) {  // the split holding the new position writes its K/V rows
+        const size_t row = ((((size_t)sp.b * a.L + l) * HKV + x) * a.max_seq + sp.pos) * D + 8 * t;
+        *reinterpret_cast<uint4*>(a.k_cache + row) = knew;
+        *reinterpret_cast<uint4*>(a.v_cache + row) = vnew;
+      }
+      float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f, a0[8], a1[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { a0[i] = 0.f; a1[i] = 0.f; }
+      for (int rd = 0; rd < nrounds; ++rd) {
+        if (rd > 0) load_kv(kw, vw, a, sp, l, x, gi, t, rd);
+#pragma unroll
+        for (int u = 0; u < RB; ++u) {
+          const int p = sp.k0 + gi + NG * (RB * rd + u);
+          const bool own = p == sp.pos;
+          float kf[8], vf[8];
+          unpack8(own ? knew : kw[u], kf);
+          unpack8(own ? vnew : vw[u], vf);
+          float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) { d0 = fmaf(qa[i], kf[i], d0); d1 = fmaf(qb[i], kf[i], d1); }
+          d0 = row16_sum(d0) * ATT_SCALE;
+          d1 = row16_sum(d1) * ATT_SCALE;
+          if (p < sp.k1) {
+            softmax_step(d0, vf, m0, l0, a0);
+            softmax_step(d1, vf, m1, l1, a1);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { sm.gacc[gi][0][8 * t + i] = a0[i]; sm.gacc[gi][1][8 * t + i] = a1[i]; }
+      if (t == 0) { sm.gml[gi][0] = m0; sm.gml[gi][1] = l0; sm.gml[gi][2] = m1; sm.gml[gi][3] = l1; }
+      mark(a, x, j, l, 19, 64 * NCW);
+      lds_barrier();  // B2
+      // merge of the 32 group partials: output (head h, dim d) on two adjacent lanes, 16 groups each
+      const int lam = tid - 64 * NCW, o = lam >> 1, h = o >> 7, d = o & (D - 1), half = lam & 1;
+      float mg[NG / 2], M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NG / 2; ++q) mg[q] = sm.gml[16 * half + q][2 * h];
+#pragma unroll
+      for (int q = 0; q < NG / 2; ++q) M = fmaxf(M, mg[q]);
+      M = fmaxf(M, dpp<0xB1>(M));  // the other half's groups
+      float A = 0.f, Ls = 0.f;
+#pragma unroll
+      for (int q = 0; q < NG / 2; ++q) {
+        const float e = __expf(mg[q] - M);
+        A = fmaf(sm.gacc[16 * half + q][h][d], e, A);
+        Ls = fmaf(sm.gml[16 * half + q][2 * h + 1], e, Ls);
+      }
+      A += dpp<0xB1>(A);
+      Ls += dpp<0xB1>(Ls);
+      if (half == 0) {
+        uint32_t* base = a.ws + W_AX + ((size_t)x * WPX + j) * APW;
+        st1(base, o, A, ep);
+        if (d == 0) {
+          st1(base, 2 * D + 2 * h, M, ep);
+          st1(base, 2 * D + 2 * h + 1, Ls, ep);
+        }
+      }
+      mark(a, x, j, l, 15, 64 * NCW);
+      issue(3);
+    }
+    lds_barrier();  // C1
+    issue(4);
+    merge_splits(sm, a);
+    lds_barrier();  // C2
+    issue(5);
+    mma_to_red<2>(sm, wo, 2 * (ml.m & 3), ml);
+    lds_barrier();  // C3
+    issue(6);
+    lds_barrier();  // E1
+    issue(7);
+    mma_to_red<8>(sm, wg, 8 * (ml.m & 3), ml);
+    lds_barrier();  // E2
+    issue(8);
+    lds_barrier();  // F1
+    issue(9);
+    mma_to_red<3>(sm, wd, 3 * (ml.m & 3), ml);
+    lds_barrier();  // F2
+    issue(10);
+  }
+  lds_barrier();  // the final norm
+}
+
+// ------------------------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const bool comm = wave < NCW;
+  Ctl c{a.ws, a.drain != 0};
+
+  // ---- identity, inputs, split plan
+  if (tid == 0) {
+    const int x = (int)(xcc_id() & 7u);
+    sm.x = x;
+    sm.j = (int)__hip_atomic_fetch_add(a.ws + W_TICK + 64 * x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.bad = 0;
+  }
+  if (tid >= 64 && tid < 64 + BM) {
+    const int b = tid - 64;
+    int p = 0, t = 0;
+    if (b < a.B) {
+      p = a.positions[b];
+      t = a.tokens[b];
+    }
+    bool bad = false;
+    if (p < 0 || p >= a.max_seq) { bad = true; p = p < 0 ? 0 : a.max_seq - 1; }
+    if (t < 0 || t >= a.vocab) { bad = true; t = 0; }
+    sm.pos[b] = p;
+    sm.tok[b] = t;
+    if (bad && b < a.B) atomicOr(&sm.bad, 1);
+  }
+  for (int i = tid; i < 16 * KST / 8; i += NT) reinterpret_cast<uint4*>(&sm.act[0][0])[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  if (tid == 0) {
+    // key-range length: a multiple of 16 keeping the number of ranges below 32
+    int T = 0;
+    for (int b = 0; b < a.B; ++b) T += sm.pos[b] + 1;
+    const int ks = 16 * ((T + 16 * (WPX - a.B) - 1) / (16 * (WPX - a.B)));
+    int f = 0;
+    for (int b = 0; b < a.B; ++b) {
+      const int n = (sm.pos[b] + ks) / ks;  // ceil((pos + 1) / ks)
+      sm.f[b] = f;
+      sm.ns[b] = n;
+      for (int s = 0; s < n; ++s) sm.sb[f + s] = b;
+      f += n;
+    }
+    sm.nsplit = f;
+    sm.ks = ks;
+    if (sm.bad && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W_BAD, 1u);
+    if (a.drain && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W_ABORT, 1u);
+    if (sm.j >= WPX) st_dev_u32(a.ws + W_ABORT, 1u);  // more than 32 workgroups on one XCD: no role
+  }
+  __syncthreads();
+  const int x = sm.x, j = sm.j;
+  if (j >= WPX) return;
+  Split sp;
+  sp.on = j < sm.nsplit;
+  sp.b = sp.on ? sm.sb[j] : 0;
+  sp.s = sp.on ? j - sm.f[sp.b] : 0;
+  sp.pos = sm.pos[sp.b];
+  sp.k0 = sp.s * sm.ks;
+  sp.k1 = min(sp.k0 + sm.ks, sp.pos + 1);
+  if (tid < 32) {
+    const uint16_t* src = (tid < 16 ? a.cos_tab : a.sin_tab) + (size_t)sp.pos * D + 8 * (tid & 15);
+    *reinterpret_cast<uint4*>(&sm.cs[tid >> 4][8 * (tid & 15)]) = *reinterpret_cast<const uint4*>(src);
+  }
+  __syncthreads();
+
+  mark(a, x, j, MAXL, 0);
+  if (comm) comm_role(sm, c, a, sp, x, j);
+  else math_role(sm, a, sp, x, j);
+  mark(a, x, j, MAXL, 1);
+
+  // ---- tied LM head on all waves, greedy keys
+  {
+    const int li = lane & 15, g = lane >> 4, b = li >> 1;
+    const bool out = !(li & 1) && b < a.B;
+    const float rs = out ? norm_scale(sm, b) : 0.f;
+    const int gw = j * NXCD + x, ntiles = a.vocab / 16;
+    u64 best = 0;
+    const __amdgpu_buffer_rsrc_t rlm = make_rsrc(a.lm_head);
+    auto load_chunk = [&](uint4 (&w)[8], int tile, int ch) {
+      const int off = ((16 * tile + li) * H + 256 * ch + 8 * g) * 2;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) w[s] = ldnt(rlm, off + 64 * s);
+    };
+    auto mma_chunk = [&](const uint4 (&w)[8], int ch, f32x4& acc) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint4 bo = *reinterpret_cast<const uint4*>(&sm.act[li][256 * ch + 32 * s + 8 * g]);
+        acc = mfma(w[s], bo, acc);
+      }
+    };
+    int tile = gw + NWG * wave;
+    uint4 wa[8], wb[8];
+    if (tile < ntiles) {
+      load_chunk(wa, tile, 0);
+      load_chunk(wb, tile, 1);
+    }
+    while (tile < ntiles) {
+      // the operand is read from LDS per tile (held in registers it would take 128 of them)
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const int next = tile + NWG * NWAVE;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      mma_chunk(wa, 0, acc);
+      load_chunk(wa, tile, 2);
+      mma_chunk(wb, 1, acc);
+      load_chunk(wb, tile, 3);
+      mma_chunk(wa, 2, acc);
+      if (next < ntiles) load_chunk(wa, next, 0);
+      mma_chunk(wb, 3, acc);
+      if (next < ntiles) load_chunk(wb, next, 1);
+      float lg[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lg[r] = (acc[r] + dpp<0xB1>(acc[r])) * rs;  // hi + lo columns
+      if (out) {
+        const int v0 = 16 * tile + 4 * g;
+        *reinterpret_cast<float4*>(a.logits + (size_t)b * a.vocab + v0) = make_float4(lg[0], lg[1], lg[2], lg[3]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const u64 k = argmax_key(lg[r], v0 + r);
+          best = k > best ? k : best;
+        }
+      }
+      tile = next;
+    }
+    // reduce over the 4 row groups of the wave, then over the waves
+#pragma unroll
+    for (int sh = 16; sh < 64; sh <<= 1) {
+      const u64 o = ((u64)(uint32_t)__shfl_xor((int)(best >> 32), sh) << 32) | (uint32_t)__shfl_xor((int)best, sh);
+      best = o > best ? o : best;
+    }
+    if (g == 0 && out) sm.wk[wave][b] = best;
+    __syncthreads();
+    if (tid < a.B) {
+      u64 k = 0;
+      for (int w = 0; w < NWAVE; ++w) k = sm.wk[w][tid] > k ? sm.wk[w][tid] : k;
+      reinterpret_cast<u64*>(a.ws + W_KEYS)[gw * BM + tid] = k;
+    }
+    mark(a, x, j, MAXL, 2);
+  }
+}
+
+// Zeroes the exchange words (and the ticket, abort and bad words) before a launch.
+__global__ void __launch_bounds__(256) batch_zero_kernel(uint32_t* ws) {
+  uint4* p = reinterpret_cast<uint4*>(ws);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < W_ZERO / 4; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// Greedy tokens from the workgroups' keys; NaN logits and token -1 for every sequence if the launch
+// gave up or an input was out of range.
+__global__ void __launch_bounds__(256) batch_finish_kernel(const uint32_t* ws, int B, int vocab, float* logits,
+                                                           int32_t* out_tokens) {
+  const bool failed = ws[W_ABORT] != 0 || ws[W_BAD] != 0;
+  if (failed) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)B * vocab; i += (size_t)gridDim.x * blockDim.x)
+      logits[i] = __uint_as_float(0x7fc00000u);
+  }
+  if (blockIdx.x != 0 || !out_tokens) return;
+  const int lane = threadIdx.x & 63, b = threadIdx.x >> 6;  // 4 waves, sequences b, b + 4
+  const u64* keys = reinterpret_cast<const u64*>(ws + W_KEYS);
+  for (int s = b; s < B; s += 4) {
+    u64 k = 0;
+    for (int w = lane; w < NWG; w += 64) k = keys[w * BM + s] > k ? keys[w * BM + s] : k;
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+      const u64 o = ((u64)(uint32_t)__shfl_xor((int)(k >> 32), sh) << 32) | (uint32_t)__shfl_xor((int)k, sh);
+      k = o > k ? o : k;
+    }
+    if (lane == 0) out_tokens[s] = failed ? -1 : (int32_t)(0xffffffffu - (uint32_t)k);
+  }
+}
+
+// ---- host ----------------------------------------------------------------------------------------
+
+constexpr int MAX_DEVICES = 64;
+struct DevCheck {
+  bool done = false;
+  bool ok = false;
+};
+static DevCheck g_check[MAX_DEVICES];
+static std::mutex g_mu;
+static std::atomic<int> g_engine{0};    // 0 automatic, 1 layer-by-layer engine, 2 this kernel
+static std::atomic<bool> g_drain{false};
+static std::atomic<uint64_t*> g_trace{nullptr};
+
+// Can the current device run the kernel: 256 CUs and one 768-thread workgroup per CU.
+static bool device_ok() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return false;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevCheck& d = g_check[dev];
+  if (!d.done) {
+    int cus = 0, blocks = 0;
+    d.ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus == NWG &&
+           hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)batch_kernel, NT, 0) == hipSuccess &&
+           blocks >= 1;
+    d.done = true;
+  }
+  return d.ok;
+}
+
+}  // namespace mkb
+
+bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len) {
+  using namespace mkb;
+  const int e = g_engine.load();
+  if (e == 1) return false;
+  return dims->hidden == H && dims->intermediate == I && dims->num_layers >= 1 && dims->num_layers <= MAXL &&
+         dims->num_layers < 255 && batch >= 1 && batch <= BM && max_seq_len >= 1 && device_ok();
+}
+size_t mkb_workspace_bytes() { return mkb::WS_BYTES; }
+void mkb_set_drain(bool on) { mkb::g_drain.store(on); }
+
+hipError_t mkb_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens, const int32_t* positions,
+                            const void* embed_weight, const void* lm_head_weight, const void* final_norm_weight,
+                            const mk_layer_weights* layers, const void* cos_table, const void* sin_table,
+                            void* k_cache, void* v_cache, int max_seq_len, float* logits, int32_t* out_tokens,
+                            void* workspace, hipStream_t stream) {
+  using namespace mkb;
+  BArgs a{};
+  a.tokens = tokens;
+  a.positions = positions;
+  a.embed = (const uint16_t*)embed_weight;
+  a.lm_head = (const uint16_t*)lm_head_weight;
+  a.final_norm = (const uint16_t*)final_norm_weight;
+  a.cos_tab = (const uint16_t*)cos_table;
+  a.sin_tab = (const uint16_t*)sin_table;
+  a.k_cache = (uint16_t*)k_cache;
+  a.v_cache = (uint16_t*)v_cache;
+  a.logits = logits;
+  a.ws = (uint32_t*)workspace;
+  a.B = batch;
+  a.L = dims->num_layers;
+  a.vocab = dims->vocab;
+  a.max_seq = max_seq_len;
+  a.drain = g_drain.load() ? 1 : 0;
+  a.trace = g_trace.load();
+  for (int l = 0; l < a.L; ++l) a.lw[l] = layers[l];
+  hipLaunchKernelGGL(batch_zero_kernel, dim3(128), dim3(256), 0, stream, a.ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(batch_kernel, dim3(NWG), dim3(NT), 0, stream, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(batch_finish_kernel, dim3(64), dim3(256), 0, stream, (const uint32_t*)a.ws, batch, dims->vocab,
+                     logits, out_tokens);
+  return hipGetLastError();
+}
+
+extern "C" hipError_t mk_set_batch_engine(int engine) {
+  if (engine < 0 || engine > 2) return hipErrorInvalidValue;
+  mkb::g_engine.store(engine);
+  return hipSuccess;
+}
+
+extern "C" hipError_t mk_set_batch_trace(uint64_t* device_buffer, size_t bytes) {
+  if (device_buffer != nullptr && bytes < mkb::TRACE_BYTES) return hipErrorInvalidValue;
+  mkb::g_trace.store(device_buffer);
+  return hipSuccess;
+}
+
+extern "C" size_t mk_batch_trace_bytes(void) { return mkb::TRACE_BYTES; }

@@ -50,6 +50,7 @@
 #include <type_traits>
 #include <string.h>
 
+#include "mk_batch.h"
 #include "mk_device.h"
 #include "../../include/megakernel_amd.h"
 
@@ -1915,6 +1916,7 @@ extern "C" hipError_t mk_status(uint32_t* status) {
 extern "C" hipError_t mk_reset(void) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
+  mkb_set_drain(false);
   e = for_each_workspace([](void* ws) {
     hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, 0, static_cast<u64*>(ws));
     return hipGetLastError();
@@ -1926,6 +1928,7 @@ extern "C" hipError_t mk_reset(void) {
 extern "C" hipError_t mk_request_drain(void) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
+  mkb_set_drain(true);
   e = for_each_workspace([](void* ws) {
     hipLaunchKernelGGL(ws_raise_kernel, dim3(1), dim3(64), 0, 0, static_cast<u64*>(ws), ERR_HOST);
     return hipGetLastError();

@@ -35,40 +35,13 @@
 #include <stdint.h>
 
 #include "mk_device.h"
+#include "mk_batch.h"
+#include "mk_layers.h"
 #include "../../include/megakernel_amd.h"
 
 namespace mkp {
 using namespace mk;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned long long u64;
-
-constexpr int D = 128, HQ = 16, HKV = 8;
-constexpr float EPS = 1e-6f;
-constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
-
-__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                 0, 0, 0);
-}
-
-// hi = bf16(v), lo = bf16(v - hi) of 8 values, as two 16-byte chunks
-__device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    h[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
-    l[q] = pack_bf16x2(v[2 * q] - bf16_lo(h[q]), v[2 * q + 1] - bf16_hi(h[q]));
-  }
-  hi = make_uint4(h[0], h[1], h[2], h[3]);
-  lo = make_uint4(l[0], l[1], l[2], l[3]);
-}
-
-__device__ __forceinline__ void unpack8(uint4 w, float (&v)[8]) {
-  v[0] = bf16_lo(w.x); v[1] = bf16_hi(w.x); v[2] = bf16_lo(w.y); v[3] = bf16_hi(w.y);
-  v[4] = bf16_lo(w.z); v[5] = bf16_hi(w.z); v[6] = bf16_lo(w.w); v[7] = bf16_hi(w.w);
-}
 
 // Where the prefill's K/V rows live: the decode layout [L][8][max_seq][128], or (with a block table)
 // the paged layout [L][num_pages][8][page_size][128] of mk_decode_paged, position p in page
@@ -596,11 +569,6 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
 // the lowest index. Every workgroup normalises the row into LDS (bf16 hi/lo), then its 8 waves
 // stream vocabulary rows (row v to wave v % (8 * grid)), 4 rows in flight per wave.
 // ------------------------------------------------------------------------------------------------
-__device__ __forceinline__ u64 argmax_key(float logit, int idx) {
-  uint32_t u = (uint32_t)f32_to_bf16(logit) << 16;
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((u64)u << 32) | (0xffffffffu - (uint32_t)idx);
-}
 
 template <int H>
 __global__ void __launch_bounds__(512) lm_head_kernel(const float* x, int row, const uint16_t* final_norm,
@@ -976,24 +944,6 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, 
 // part: [B][8][S][2][D + 2].
 constexpr int APW = D + 2;
 
-// Per-head RMSNorm + rotate-half RoPE of 8 dims of one head row held by a 16-lane row (lane t: dims
-// 8t..8t+7; the RoPE partner of dim d is d +- 64, in lane t ^ 8), as the decode kernel applies them
-// (/root/reference/megakernel.cu:490-630, 548-555).
-__device__ __forceinline__ void head_norm_rope(float (&v)[8], const float (&wn)[8], const float (&cs)[8],
-                                               const float (&sn)[8], int t) {
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
-  const float rs = rsqrtf(row16_sum(ss) / (float)D + EPS);
-  float u[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) u[i] = v[i] * rs * wn[i];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float pr = dpp<0x128>(u[i]);  // row_ror:8 inside the 16-lane row: lane t ^ 8
-    v[i] = t < 8 ? u[i] * cs[i] - pr * sn[i] : u[i] * cs[i] + pr * sn[i];
-  }
-}
 
 constexpr int BU = 4;  // keys per 16-lane group and split: one round of loads
 static_assert(KS == 16 * BU, "a split is one round of loads");
@@ -1516,9 +1466,12 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
 
 }  // namespace mkp
 
+// The larger of the two engines' needs, so that the engine can be chosen per call.
 extern "C" size_t mk_decode_batch_workspace_bytes(const mk_model_dims* dims, int batch, int max_seq_len) {
   if (!dims || batch < 1 || batch > BMAX || max_seq_len < 1) return 0;
-  return blayout(dims->hidden, dims->intermediate, batch, max_seq_len).bytes;
+  const size_t n = blayout(dims->hidden, dims->intermediate, batch, max_seq_len).bytes;
+  const size_t p = mkb_workspace_bytes();
+  return batch <= 8 && p > n ? p : n;
 }
 
 extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens,
@@ -1538,6 +1491,12 @@ extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, cons
   const BLayout Lo = blayout(dims->hidden, dims->intermediate, batch, max_seq_len);
   if (workspace_bytes < Lo.bytes || reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return hipErrorInvalidValue;
   const mk_layer_weights* lw = static_cast<const mk_layer_weights*>(layer_weights);  // host array
+  if (mkb_applies(dims, batch, max_seq_len)) {
+    if (workspace_bytes < mkb_workspace_bytes()) return hipErrorInvalidValue;
+    return mkb_decode_batch(dims, batch, tokens, positions, embed_weight, lm_head_weight, final_norm_weight, lw,
+                            cos_table, sin_table, k_cache, v_cache, max_seq_len, logits, out_tokens, workspace,
+                            stream);
+  }
   char* ws = static_cast<char*>(workspace);
   if (s06)
     return run_batch<1024, 3072>(*dims, batch, tokens, positions, (const uint16_t*)embed_weight,

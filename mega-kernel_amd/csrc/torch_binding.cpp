@@ -374,6 +374,12 @@ void reset() { MK_HIP_CHECK(mk_reset()); }
 
 void request_drain() { MK_HIP_CHECK(mk_request_drain()); }
 
+// 0 automatic, 1 layer-by-layer engine, 2 persistent kernel (where it applies), for decode_batch
+void set_batch_engine(int64_t engine) {
+  TORCH_CHECK(engine >= 0 && engine <= 2, "set_batch_engine: expected 0, 1 or 2");
+  MK_HIP_CHECK(mk_set_batch_engine((int)engine));
+}
+
 // 0 = plain launch (default), 1 = cooperative launch, for the current device
 void set_launch_mode(int64_t cooperative) {
   TORCH_CHECK(cooperative == 0 || cooperative == 1, "set_launch_mode: expected 0 or 1");
@@ -412,6 +418,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_batch", &decode_batch,
         "batched decode of B <= 64 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
         "returns (fp32 logits [B, V], int32 greedy tokens [B] on device)");
+  m.def("set_batch_engine", &set_batch_engine,
+        "engine of decode_batch: 0 automatic (the persistent kernel for <= 8 sequences of the 0.6B shape), "
+        "1 layer by layer, 2 persistent where it applies");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
   m.def("reset", &reset, "clear the decode workspaces (exchange words, status words) and restart their launch sequences; synchronizes");

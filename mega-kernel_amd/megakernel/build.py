@@ -41,7 +41,7 @@ def _run(cmd, verbose):
 
 
 def build_library(verbose=True):
-    srcs = [os.path.join(CSRC, f) for f in ("decode_kernel.hip", "layers_kernel.hip")]
+    srcs = [os.path.join(CSRC, f) for f in ("decode_kernel.hip", "layers_kernel.hip", "batch_kernel.hip")]
     tmp = LIB + ".tmp"
     _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp], verbose)
     os.replace(tmp, LIB)

@@ -37,7 +37,7 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shape", default="qwen3-0.6b")
     ap.add_argument("--prefill", default="", help="comma-separated prompt lengths")
-    ap.add_argument("--batch", default="", help="comma-separated batch sizes (1..8)")
+    ap.add_argument("--batch", default="", help="comma-separated batch sizes (1..64)")
     ap.add_argument("--context", type=int, default=256, help="position of every sequence of a decode batch")
     ap.add_argument("--max-seq", type=int, default=4096)
     ap.add_argument("--runs", type=int, default=5)

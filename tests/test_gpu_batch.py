@@ -1,5 +1,7 @@
 """GPU parity tests of the batched decode (``decode_batch``, C ABI ``mk_decode_batch``): B sequences of
-different lengths advance one token each per call, each against its own cache.
+different lengths advance one token each per call, each against its own cache. Batches of up to 8
+sequences of the 0.6B shape run on either engine (``set_batch_engine``: 1 layer by layer, 2 the
+persistent kernel); both are checked.
 
 Per sequence, every step is checked against the fp32 restatement (``restate.decode_step``) run on the
 cache the kernel has written for that sequence -- the same tight check as the single-sequence
@@ -43,18 +45,34 @@ def _decode_batch(sess, toks, pos, kd, vd):
                                     kd, vd, sess.max_seq)
 
 
-@pytest.mark.parametrize("shape_fixture, lengths, steps", [
-    ("mini", (5, 40, 100, 300), 6),
-    ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4),
-    ("mini17", (33, 200, 90), 4),
-    ("mini", tuple(3 + 11 * i for i in range(20)), 2),  # 20 sequences: 3 column blocks of 8 (of 4)
-    ("mini", tuple(1 + 5 * i for i in range(64)), 1),   # the largest batch: 8 column blocks
-])
-def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, request):
+@pytest.fixture
+def engine(request):
+    """Forces decode_batch's engine for one test (0 = automatic is restored afterwards)."""
+    import megakernel
+    kernel = megakernel.load()
+    kernel.set_batch_engine(request.param)
+    yield request.param
+    kernel.set_batch_engine(0)
+
+
+@pytest.mark.parametrize("shape_fixture, lengths, steps, engine", [
+    ("mini", (5, 40, 100, 300), 6, 1),
+    ("mini", (5, 40, 100, 300), 6, 2),
+    ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4, 1),
+    ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4, 2),
+    ("mini", (495,), 3, 2),                              # one sequence: 31 key ranges of 16, then 16 of 32
+    ("mini", (509, 3, 260, 1, 400, 90, 128), 2, 2),      # 27 key ranges of 64 over 7 sequences
+    ("mini17", (33, 200, 90), 4, 1),
+    ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
+    ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
+], indirect=["engine"])
+def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, engine, request):
     """Sequences of different lengths in one batch (so their attention spans 1 to 8 key splits of
     64, and sequences end a split exactly at 64 and 256): every step, each sequence's logits and
     greedy token against the restatement on the kernel's cache for that sequence, and its new K/V
-    rows. Up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3 and 8."""
+    rows. Layer by layer, up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3
+    and 8. The persistent kernel (engine 2) cuts the batch's keys into at most 31 ranges, one per
+    workgroup of an XCD."""
     sess = request.getfixturevalue(shape_fixture)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
@@ -81,16 +99,22 @@ def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, reques
         assert sorted({(c[0], c[3]) for c in changed}) <= sorted({(b, pos[b]) for b in range(B)})
         toks = dev_toks
         pos = [p + 1 for p in pos]
-    print(f"[batch {shape_fixture} B={B}] {steps} steps, every sequence matches the restatement, "
+    print(f"[batch {shape_fixture} B={B} engine {engine}] {steps} steps, every sequence matches the restatement, "
           f"max|d| {worst:.3e}", flush=True)
 
 
-def test_batch_agrees_with_single_sequence_decode_at_0_6b():
+@pytest.fixture(scope="module")
+def q06():
+    return Session("qwen3-0.6b", 512)
+
+
+@pytest.mark.parametrize("engine", [1, 2], indirect=True)
+def test_batch_agrees_with_single_sequence_decode_at_0_6b(q06, engine):
     """The full Qwen3-0.6B shape, 8 sequences of lengths 32..480: each sequence's batched logits and
     token against the single-sequence decode kernel on an identical cache, for 6 steps (both are
     fp32-accurate, so they agree to the restatement tolerance), and against the restatement on the
     first step. Prints the batched step time."""
-    sess = Session("qwen3-0.6b", 512)
+    sess = q06
     lengths = (32, 64, 100, 150, 200, 256, 300, 480)
     B = len(lengths)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=20 + i)[0].tolist() for i, n in enumerate(lengths)]
@@ -126,11 +150,13 @@ def test_batch_agrees_with_single_sequence_decode_at_0_6b():
     ev1.record()
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / 20
-    print(f"[batch qwen3-0.6b B={B}] {ms * 1e3:.0f} us per batched step, {B / ms * 1e3:.0f} tokens/s", flush=True)
+    print(f"[batch qwen3-0.6b B={B} engine {engine}] {ms * 1e3:.0f} us per batched step, {B / ms * 1e3:.0f} tokens/s",
+          flush=True)
     assert sess.kernel.status() == 0
 
 
-def test_batch_bad_position_is_reported_in_band(mini):
+@pytest.mark.parametrize("engine", [1, 2], indirect=True)
+def test_batch_bad_position_is_reported_in_band(mini, engine):
     """A position outside [0, max_seq) cannot be checked on the host without a copy: the call reports
     NaN logits and token -1 for every sequence, and accesses stay inside the cache."""
     kd = torch.zeros(2, mini.shape.layers, 8, mini.max_seq, 128, dtype=torch.bfloat16, device=DEV)
@@ -138,4 +164,21 @@ def test_batch_bad_position_is_reported_in_band(mini):
     logits, toks = _decode_batch(mini, [3, 4], [10, mini.max_seq + 7], kd, vd)
     assert torch.isnan(logits).all() and toks.tolist() == [-1, -1]
     logits, toks = _decode_batch(mini, [3, 4], [10, 11], kd, vd)
+    assert torch.isfinite(logits).all() and min(toks.tolist()) >= 0
+
+
+@pytest.mark.parametrize("engine", [2], indirect=True)
+def test_persistent_batch_drains_on_request(mini, engine):
+    """After request_drain() the persistent kernel's waits give up at once (every workgroup still exits
+    normally): NaN logits and token -1 for every sequence, until reset(); then a normal step."""
+    kd = torch.zeros(3, mini.shape.layers, 8, mini.max_seq, 128, dtype=torch.bfloat16, device=DEV)
+    vd = torch.zeros_like(kd)
+    mini.kernel.request_drain()
+    try:
+        logits, toks = _decode_batch(mini, [3, 4, 5], [10, 20, 30], kd, vd)
+        torch.cuda.synchronize()
+        assert torch.isnan(logits).all() and toks.tolist() == [-1, -1, -1]
+    finally:
+        mini.kernel.reset()
+    logits, toks = _decode_batch(mini, [3, 4, 5], [10, 20, 30], kd, vd)
     assert torch.isfinite(logits).all() and min(toks.tolist()) >= 0
