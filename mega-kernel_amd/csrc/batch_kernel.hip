@@ -75,6 +75,10 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 // each goes where the comm waves' next poll is furthest away. Measured at 8 sequences of 257 keys
 // (0.6B): gate/up+down after the attention publish 797 us per step, gate/up after C1 729, and the
 // defaults below 708.
+// K steps per load chunk of the LM head (two chunks in flight per wave).
+#ifndef MKB_LM_CH
+#define MKB_LM_CH 8
+#endif
 // Polls of up to MKB_TWO_MAX chunks per lane keep two rounds of loads in flight.
 #ifndef MKB_TWO_MAX
 #define MKB_TWO_MAX 4
@@ -151,10 +155,10 @@ struct Smem {
   float gacc[NG][2][D];          // attention group partials
   float gml[NG][4];
   float stg[WPX * APW];          // polled split partials
-  float raw[QX];                 // polled q/k/v sums of this workgroup's sequence
+  alignas(16) float raw[2 * D];  // this workgroup's sequence's q (2 heads, normalised and rotated)
+  alignas(16) uint16_t kvn[2][D];  // its new K (normalised, rotated) and V rows, bf16
   float ssw[NCW][BM];            // per comm wave sums of squares
-  uint16_t cs[2][D];             // cos, sin at this workgroup's split's position
-  uint16_t qkn[2][2][D];         // q_norm, k_norm weights, by layer parity
+  alignas(16) uint16_t cs[2][D];  // cos, sin at this workgroup's split's position
   u64 wk[NWAVE][BM];             // LM head keys per wave
   int pos[BM], tok[BM], f[BM], ns[BM], sb[WPX];
   int x, j, nsplit, ks, bad;
@@ -282,21 +286,36 @@ __device__ __forceinline__ void residual_norm(Smem& sm, Ctl& c, const BArgs& a, 
   const uint2 wr = *reinterpret_cast<const uint2*>(w + e0);
   const float wv[4] = {bf16_lo(wr.x), bf16_hi(wr.x), bf16_lo(wr.y), bf16_hi(wr.y)};
   const int wave = cl >> 6, lane = cl & 63;
+  float ss[BM];
 #pragma unroll
   for (int b = 0; b < BM; ++b) {
-    if (b >= a.B) break;
-    float4* xr = reinterpret_cast<float4*>(&sm.xres[b][e0]);
-    float4 xv = *xr;
-    if constexpr (EMBED) xv = make_float4(v[b][0], v[b][1], v[b][2], v[b][3]);
-    else { xv.x += v[b][0]; xv.y += v[b][1]; xv.z += v[b][2]; xv.w += v[b][3]; }
-    *xr = xv;
-    const float y[4] = {xv.x * wv[0], xv.y * wv[1], xv.z * wv[2], xv.w * wv[3]};
-    uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
-    uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
-    *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
-    *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
-    const float ss = wave_sum(xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w);
-    if (lane == 0) sm.ssw[wave][b] = ss;
+    ss[b] = 0.f;
+    if (b < a.B) {
+      float4* xr = reinterpret_cast<float4*>(&sm.xres[b][e0]);
+      float4 xv = *xr;
+      if constexpr (EMBED) xv = make_float4(v[b][0], v[b][1], v[b][2], v[b][3]);
+      else { xv.x += v[b][0]; xv.y += v[b][1]; xv.z += v[b][2]; xv.w += v[b][3]; }
+      *xr = xv;
+      const float y[4] = {xv.x * wv[0], xv.y * wv[1], xv.z * wv[2], xv.w * wv[3]};
+      uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
+      uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
+      *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
+      *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
+      ss[b] = xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w;
+    }
+  }
+  // the 8 wave reductions side by side
+#pragma unroll
+  for (int b = 0; b < BM; ++b) ss[b] = row16_sum(ss[b]);
+#pragma unroll
+  for (int b = 0; b < BM; ++b) ss[b] = xsum16(ss[b]);
+#pragma unroll
+  for (int b = 0; b < BM; ++b) ss[b] = xsum32(ss[b]);
+  if (lane < BM) {
+    float mine = ss[0];
+#pragma unroll
+    for (int b = 1; b < BM; ++b) mine = lane == b ? ss[b] : mine;
+    sm.ssw[wave][lane] = mine;
   }
 }
 
@@ -322,14 +341,15 @@ __device__ __forceinline__ float red_sum(const Smem& sm, int r, int b) {
 
 // Workgroup j of XCD x sums row block j (OR rows of every sequence) over the 8 XCDs' partials at
 // `cross` in a fixed order and republishes it in its XCD at `local`. Comm wave 0, lane (b, quad).
-__device__ __forceinline__ void gather(Smem& sm, Ctl& c, const BArgs& a, size_t cross, size_t local, uint32_t ep) {
+__device__ __forceinline__ void gather(Ctl& c, const BArgs& a, size_t cross, size_t local, uint32_t ep, int x,
+                                       int j) {
   const int lane = tix();  // wave 0
   const int q8 = min(lane, 8 * a.B - 1), b = q8 >> 3, q = q8 & 7;
   int off[NXCD];
 #pragma unroll
-  for (int xs = 0; xs < NXCD; ++xs) off[xs] = (int)(((((size_t)sm.j * NXCD + xs) * BM + b) * OR + 4 * q) * 4);
+  for (int xs = 0; xs < NXCD; ++xs) off[xs] = ((xs * BM + b) * OR + 4 * q) * 4;
   float v[NXCD][4];
-  poll<NXCD>(c, a.ws + cross, off, ep, v);
+  poll<NXCD>(c, a.ws + cross + (size_t)j * NXCD * BM * OR, off, ep, v);
   float s[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -337,19 +357,58 @@ __device__ __forceinline__ void gather(Smem& sm, Ctl& c, const BArgs& a, size_t 
 #pragma unroll
     for (int xs = 1; xs < NXCD; ++xs) s[i] += v[xs][i];
   }
-  if (lane < 8 * a.B) st4<false>(a.ws + local + (size_t)sm.x * BM * H + sm.j * OR, b * H + 4 * q, s, ep);
+  if (lane < 8 * a.B) st4<false>(a.ws + local + (size_t)x * BM * H + j * OR, b * H + 4 * q, s, ep);
 }
 
-// Publishes the workgroup's OR output rows of every sequence (waves 4t..4t+3 computed tile t) as
-// cross-XCD partials: comm lane (b, quad).
-__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep) {
-  const int cl = tix();
-  if (cl >= 8 * a.B) return;
-  const int b = cl >> 3, q = cl & 7, t = q >> 2;
+// Publishes the workgroup's OR output rows of every sequence as cross-XCD partials: tile t (computed by
+// math waves 4t..4t+3) on comm wave t, lane (b, 4 rows).
+template <int T>
+__device__ __forceinline__ void publish_tile(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int x, int j) {
+  const int lane = tix() & 63;
+  if (lane >= 4 * a.B) return;
+  const int b = lane >> 2, r0 = 4 * (lane & 3);
   float v[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = t ? red_sum<4, 4>(sm, 4 * (q & 3) + i, b) : red_sum<0, 4>(sm, 4 * (q & 3) + i, b);
-  st4<true>(a.ws + cross + ((size_t)sm.j * NXCD + sm.x) * BM * OR, b * OR + 4 * q, v, ep);
+  for (int i = 0; i < 4; ++i) v[i] = red_sum<4 * T, 4>(sm, r0 + i, b);
+  st4<true>(a.ws + cross + ((size_t)j * NXCD + x) * BM * OR, b * OR + 16 * T + r0, v, ep);
+}
+__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int wave,
+                                             int x, int j) {
+  if (wave == 0) publish_tile<0>(sm, a, cross, ep, x, j);
+  else if (wave == 1) publish_tile<1>(sm, a, cross, ep, x, j);
+}
+
+// q/k RMSNorm + rotate-half RoPE of one head row held by 32 lanes (lane c % 32: dims 4c..4c+3; the RoPE
+// partner of dim d is d +- 64, 16 lanes away), as the single-sequence kernel applies them
+// (/root/reference/megakernel.cu:490-630, 548-555); row 3 (v) is only rounded. Writes q as fp32 into
+// raw[row][] and the new K/V rows as bf16 into kvn. Both waves' lanes take part in the swaps.
+__device__ __forceinline__ void head_norm_rope4(Smem& sm, const float (&v)[4], uint2 wn, int tid) {
+  const int row = tid >> 5, d0 = 4 * (tid & 31);
+  float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  ss = xsum16(row16_sum(ss));  // the 32 lanes of this row
+  const float rs = rsqrtf(ss / (float)D + EPS);
+  const float w[4] = {bf16_lo(wn.x), bf16_hi(wn.x), bf16_lo(wn.y), bf16_hi(wn.y)};
+  float u[4], o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) u[i] = v[i] * rs * w[i];
+  const uint2 cr = *reinterpret_cast<const uint2*>(&sm.cs[0][d0 & (D / 2 - 1)]);  // dims mod 64
+  const uint2 sr = *reinterpret_cast<const uint2*>(&sm.cs[1][d0 & (D / 2 - 1)]);
+  const float cs[4] = {bf16_lo(cr.x), bf16_hi(cr.x), bf16_lo(cr.y), bf16_hi(cr.y)};
+  const float sn[4] = {bf16_lo(sr.x), bf16_hi(sr.x), bf16_lo(sr.y), bf16_hi(sr.y)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // (own, partner) in row order: an even 16-lane row gets its partner second, an odd one first
+    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[i]), __float_as_uint(u[i]), false, false);
+    const float partner = __uint_as_float((tid & 16) ? pr[0] : pr[1]);
+    o[i] = d0 < D / 2 ? u[i] * cs[i] - partner * sn[i] : u[i] * cs[i] + partner * sn[i];
+  }
+  if (row < 2) {
+    *reinterpret_cast<float4*>(&sm.raw[row * D + d0]) = make_float4(o[0], o[1], o[2], o[3]);
+  } else {
+    const float* src = row == 2 ? o : v;
+    *reinterpret_cast<uint2*>(&sm.kvn[row - 2][d0]) =
+        make_uint2(pack_bf16x2(src[0], src[1]), pack_bf16x2(src[2], src[3]));
+  }
 }
 
 // ---- math-wave weight loads (lane: li = row of the tile, g = 8-element K group) -------------------
@@ -384,19 +443,23 @@ __device__ __forceinline__ void load_o(uint4 (&w)[2], const mk_layer_weights& lw
 #pragma unroll
   for (int s = 0; s < 2; ++s) w[s] = ldnt(rs, off + 64 * s);
 }
-// gate (waves 0-3) or up (waves 4-7) rows of the workgroup's 12 intermediates (rows 12-15 of the tile
-// are empty); K steps 8 (m % 4) .. +7.
+// gate (waves 0-3) or up (waves 4-7) rows of the workgroup's 12 intermediates; K steps 8 (m % 4) .. +7.
+// Rows 12-15 of the tile are empty: their lanes load row 11 again (every lane of the wave issues the
+// same loads, so the compiler's count of loads in flight stays exact and later waits need not wait
+// for the whole burst) and keep zeros.
 __device__ __forceinline__ void load_gu(uint4 (&w)[8], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
+  const uint16_t* m0 = (const uint16_t*)(ml.m < 4 ? lw.gate_proj_weight : lw.up_proj_weight);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(m0 + ((size_t)IX * x + GI * j) * H);
+  const int off = (min(ml.li, GI - 1) * H + 256 * (ml.m & 3) + 8 * ml.g) * 2;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) w[s] = ldnt(rs, off + 64 * s);
+}
+// zeros in the empty rows of the gate/up tile (applied just before the tile's MFMAs)
+__device__ __forceinline__ void mask_gu(uint4 (&w)[8], const MathLane& ml) {
   if (ml.li >= GI) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) w[s] = make_uint4(0, 0, 0, 0);
-    return;
   }
-  const uint16_t* m0 = (const uint16_t*)(ml.m < 4 ? lw.gate_proj_weight : lw.up_proj_weight);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(m0 + ((size_t)IX * x + GI * j) * H);
-  const int off = (ml.li * H + 256 * (ml.m & 3) + 8 * ml.g) * 2;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) w[s] = ldnt(rs, off + 64 * s);
 }
 // down_proj: rows 32j + 16 (m / 4) + li, the XCD's 384 intermediate columns; K steps 3 (m % 4) .. +2.
 __device__ __forceinline__ void load_down(uint4 (&w)[3], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
@@ -426,23 +489,21 @@ struct Split {
   int b, s, k0, k1, pos;
 };
 
-// K/V rows of round `round` of this group's keys (positions k0 + gi + NG (RB round + u)); keys past the
-// split are not loaded.
+// K/V rows of round `round` of this group's keys (positions k0 + gi + NG (RB round + u)); past the split
+// they re-read its last key (every lane issues the same loads, so the compiler's count of loads in
+// flight stays exact; the attention skips those keys).
 __device__ __forceinline__ void load_kv(uint4 (&kw)[RB], uint4 (&vw)[RB], const BArgs& a, const Split& sp, int layer,
                                         int x, int gi, int t, int round) {
   const size_t head = (((size_t)sp.b * a.L + layer) * HKV + x) * a.max_seq * D;
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_cache + head), rv = make_rsrc(a.v_cache + head);
 #pragma unroll
   for (int u = 0; u < RB; ++u) {
-    const int p = sp.k0 + gi + NG * (RB * round + u);
-    kw[u] = vw[u] = make_uint4(0, 0, 0, 0);
-    if (p < sp.k1) {
-      const int off = (p * D + 8 * t) * 2;
-      const u4v k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-      const u4v v = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-      kw[u] = make_uint4(k[0], k[1], k[2], k[3]);
-      vw[u] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
+    const int p = min(sp.k0 + gi + NG * (RB * round + u), sp.k1 - 1);
+    const int off = (p * D + 8 * t) * 2;
+    const u4v k = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    const u4v v = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    kw[u] = make_uint4(k[0], k[1], k[2], k[3]);
+    vw[u] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -456,26 +517,48 @@ __device__ __forceinline__ void softmax_step(float sc, const float (&v)[8], floa
 }
 
 
-// Merge of every sequence's split partials (polled into LDS) into the o_proj operand: output
-// (b, head h, dim d) per thread, all waves, max-first over the sequence's splits.
+// Merge of every sequence's split partials (polled into LDS) into the o_proj operand: thread (b, head
+// h, 4 dims) for b < B (one pass of B * 64 threads), max-first over the sequence's splits.
 __device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a) {
-  for (int o = tix(); o < a.B * 2 * D; o += NT) {
-    const int b = o >> 8, h = (o >> 7) & 1, d = o & (D - 1);
-    const float* p = sm.stg + (size_t)sm.f[b] * APW;
-    const int n = sm.ns[b];
+  const int o = tix();
+  if (o >= a.B * 64) return;
+  const int b = o >> 6, h = (o >> 5) & 1, d0 = 4 * (o & 31);
+  const float* p = sm.stg + (size_t)sm.f[b] * APW;
+  const int n = sm.ns[b];
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  float Ls = 0.f;
+  auto add = [&](float4 acc, float l, float e) {
+    A.x = fmaf(acc.x, e, A.x); A.y = fmaf(acc.y, e, A.y); A.z = fmaf(acc.z, e, A.z); A.w = fmaf(acc.w, e, A.w);
+    Ls = fmaf(l, e, Ls);
+  };
+  if (n <= 4) {  // every load first, then the arithmetic
+    float2 ml[4];
+    float4 acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float* q = p + (s < n ? s : 0) * APW;
+      ml[s] = *reinterpret_cast<const float2*>(q + 2 * D + 2 * h);
+      acc[s] = *reinterpret_cast<const float4*>(q + h * D + d0);
+    }
+    float M = ml[0].x;
+#pragma unroll
+    for (int s = 1; s < 4; ++s) M = s < n ? fmaxf(M, ml[s].x) : M;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) add(acc[s], ml[s].y, s < n ? __expf(ml[s].x - M) : 0.f);
+  } else {
     float M = -INFINITY;
     for (int s = 0; s < n; ++s) M = fmaxf(M, p[s * APW + 2 * D + 2 * h]);
-    float A = 0.f, Ls = 0.f;
     for (int s = 0; s < n; ++s) {
-      const float e = __expf(p[s * APW + 2 * D + 2 * h] - M);
-      A = fmaf(p[s * APW + h * D + d], e, A);
-      Ls = fmaf(p[s * APW + 2 * D + 2 * h + 1], e, Ls);
+      const float* q = p + s * APW;
+      add(*reinterpret_cast<const float4*>(q + h * D + d0), q[2 * D + 2 * h + 1], __expf(q[2 * D + 2 * h] - M));
     }
-    const float val = A / Ls;
-    const uint16_t hi = f32_to_bf16(val);
-    sm.act[2 * b][h * D + d] = hi;
-    sm.act[2 * b + 1][h * D + d] = f32_to_bf16(val - bf16_to_f32(hi));
   }
+  const float r = 1.f / Ls;
+  const float y[4] = {A.x * r, A.y * r, A.z * r, A.w * r};
+  const uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
+  const uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
+  *reinterpret_cast<uint2*>(&sm.act[2 * b][h * D + d0]) = make_uint2(h0, h1);
+  *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][h * D + d0]) = make_uint2(l0, l1);
 }
 
 // Every split partial of the XCD into LDS (nsplit * 65 chunks of 16 bytes, NK per comm lane).
@@ -508,10 +591,10 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     if (l == 0) residual_norm<true>(sm, c, a, nullptr, 0, (const uint16_t*)lw.norm_weight);
     else residual_norm<false>(sm, c, a, a.ws + W_DL + (size_t)x * BM * H, ep - 1, (const uint16_t*)lw.norm_weight);
     mark(a, x, j, l, 1);
-    uint4 qn = make_uint4(0, 0, 0, 0);  // this layer's q_norm / k_norm weights, into LDS before B1
-    if (sp.on && tid < 32)
-      qn = *reinterpret_cast<const uint4*>((const uint16_t*)(tid < 16 ? lw.q_norm_weight : lw.k_norm_weight) +
-                                           8 * (tid & 15));
+    uint2 qn = make_uint2(0, 0);  // this layer's q_norm / k_norm weights of lane tid's 4 dims (rows 0-2)
+    if (sp.on && tid < 3 * D / 4)
+      qn = *reinterpret_cast<const uint2*>((const uint16_t*)(tid < D / 2 ? lw.q_norm_weight : lw.k_norm_weight) +
+                                           4 * (tid & 31));
     lds_barrier();  // A1
     lds_barrier();  // A2
     mark(a, x, j, l, 2);
@@ -526,12 +609,11 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     mark(a, x, j, l, 3);
     // ---- B: this workgroup's sequence's q/k/v sums for the attention
     if (sp.on) {
-      if (tid < QX / 4) {
+      if (tid < QX / 4) {  // waves 0-1: lane tid holds dims 4 (tid % 32) .. +3 of row tid / 32 (q0, q1, k, v)
         int off[1] = {(int)((((size_t)x * BM + sp.b) * QX + 4 * tid) * 4)};
         float v[1][4];
         poll<1>(c, a.ws + W_QX, off, ep, v);
-        *reinterpret_cast<float4*>(&sm.raw[4 * tid]) = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
-        if (tid < 32) *reinterpret_cast<uint4*>(&sm.qkn[l & 1][tid >> 4][8 * (tid & 15)]) = qn;
+        head_norm_rope4(sm, v[0], qn, tid);
       }
       lds_barrier();  // B1
       mark(a, x, j, l, 4);
@@ -543,15 +625,16 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     else poll_splits<(WPX * APW / 4 + CL - 1) / CL>(sm, c, a, x, ep);
     mark(a, x, j, l, 6);
     lds_barrier();  // C1
+    mark(a, x, j, l, 20);
     merge_splits(sm, a);
     lds_barrier();  // C2
     mark(a, x, j, l, 7);
     lds_barrier();  // C3
     mark(a, x, j, l, 8);
     // ---- D, E: o_proj partials out, row block j summed over the XCDs, residual + post-attention norm
-    publish_rows(sm, a, W_OX, ep);
+    publish_rows(sm, a, W_OX, ep, wave, x, j);
     mark(a, x, j, l, 16);
-    if (wave == 0) gather(sm, c, a, W_OX, W_OL, ep);
+    if (wave == 0) gather(c, a, W_OX, W_OL, ep, x, j);
     mark(a, x, j, l, 9);
     residual_norm<false>(sm, c, a, a.ws + W_OL + (size_t)x * BM * H, ep, (const uint16_t*)lw.post_attn_norm_weight);
     mark(a, x, j, l, 10);
@@ -571,6 +654,7 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
       }
       st4<false>(a.ws + W_MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
     }
+    mark(a, x, j, l, 21);
     {
       constexpr int NK = (BM * IX / 4) / CL;  // 3
       const int nch = a.B * (IX / 4);
@@ -597,9 +681,9 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // F2
     mark(a, x, j, l, 13);
     // ---- G: down partials out, row block j summed over the XCDs
-    publish_rows(sm, a, W_DX, ep);
+    publish_rows(sm, a, W_DX, ep, wave, x, j);
     mark(a, x, j, l, 17);
-    if (wave == 0) gather(sm, c, a, W_DX, W_DL, ep);
+    if (wave == 0) gather(c, a, W_DX, W_DL, ep, x, j);
     mark(a, x, j, l, 14);
   }
   // the last layer's sums, final norm
@@ -640,28 +724,14 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
       lds_barrier();  // B1
       mark(a, x, j, l, 18, 64 * NCW);
       issue(2);
-      float qa[8], qb[8], kn[8], vv[8];
-      {
-        float qw[8], kwn[8], cs[8], sn[8];
+      float qa[8], qb[8];  // normalised, rotated queries of the head pair (lane t: dims 8t..8t+7)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          qa[i] = sm.raw[8 * t + i];
-          qb[i] = sm.raw[D + 8 * t + i];
-          kn[i] = sm.raw[2 * D + 8 * t + i];
-          vv[i] = sm.raw[3 * D + 8 * t + i];
-        }
-        unpack8(*reinterpret_cast<const uint4*>(&sm.qkn[l & 1][0][8 * t]), qw);
-        unpack8(*reinterpret_cast<const uint4*>(&sm.qkn[l & 1][1][8 * t]), kwn);
-        unpack8(*reinterpret_cast<const uint4*>(&sm.cs[0][8 * (t & 7)]), cs);  // dims mod 64
-        unpack8(*reinterpret_cast<const uint4*>(&sm.cs[1][8 * (t & 7)]), sn);
-        head_norm_rope(qa, qw, cs, sn, t);
-        head_norm_rope(qb, qw, cs, sn, t);
-        head_norm_rope(kn, kwn, cs, sn, t);
+      for (int i = 0; i < 8; ++i) {
+        qa[i] = sm.raw[8 * t + i];
+        qb[i] = sm.raw[D + 8 * t + i];
       }
-      const uint4 knew = make_uint4(pack_bf16x2(kn[0], kn[1]), pack_bf16x2(kn[2], kn[3]), pack_bf16x2(kn[4], kn[5]),
-                                    pack_bf16x2(kn[6], kn[7]));
-      const uint4 vnew = make_uint4(pack_bf16x2(vv[0], vv[1]), pack_bf16x2(vv[2], vv[3]), pack_bf16x2(vv[4], vv[5]),
-                                    pack_bf16x2(vv[6], vv[7]));
+      const uint4 knew = *reinterpret_cast<const uint4*>(&sm.kvn[0][8 * t]);
+      const uint4 vnew = *reinterpret_cast<const uint4*>(&sm.kvn[1][8 * t]);
       if (gi == 0 && sp.pos < sp.k1) {  // the split holding the new position writes its K/V rows
         const size_t row = ((((size_t)sp.b * a.L + l) * HKV + x) * a.max_seq + sp.pos) * D + 8 * t;
         *reinterpret_cast<uint4*>(a.k_cache + row) = knew;
@@ -703,12 +773,18 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
 #pragma unroll
       for (int q = 0; q < NG / 2; ++q) M = fmaxf(M, mg[q]);
       M = fmaxf(M, dpp<0xB1>(M));  // the other half's groups
+      float ga[NG / 2], gl[NG / 2];
+#pragma unroll
+      for (int q = 0; q < NG / 2; ++q) {
+        ga[q] = sm.gacc[16 * half + q][h][d];
+        gl[q] = sm.gml[16 * half + q][2 * h + 1];
+      }
       float A = 0.f, Ls = 0.f;
 #pragma unroll
       for (int q = 0; q < NG / 2; ++q) {
         const float e = __expf(mg[q] - M);
-        A = fmaf(sm.gacc[16 * half + q][h][d], e, A);
-        Ls = fmaf(sm.gml[16 * half + q][2 * h + 1], e, Ls);
+        A = fmaf(ga[q], e, A);
+        Ls = fmaf(gl[q], e, Ls);
       }
       A += dpp<0xB1>(A);
       Ls += dpp<0xB1>(Ls);
@@ -733,6 +809,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     issue(6);
     lds_barrier();  // E1
     issue(7);
+    mask_gu(wg, ml);
     mma_to_red<8>(sm, wg, 8 * (ml.m & 3), ml);
     lds_barrier();  // E2
     issue(8);
@@ -796,15 +873,17 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     if (sm.j >= WPX) st_dev_u32(a.ws + W_ABORT, 1u);  // more than 32 workgroups on one XCD: no role
   }
   __syncthreads();
-  const int x = sm.x, j = sm.j;
+  const int x = __builtin_amdgcn_readfirstlane(sm.x), j = __builtin_amdgcn_readfirstlane(sm.j);
   if (j >= WPX) return;
+  // the split plan, wave-uniform (read from LDS, so made scalar for the compiler: branches on it are
+  // then uniform, and its count of loads in flight stays exact across them)
   Split sp;
-  sp.on = j < sm.nsplit;
-  sp.b = sp.on ? sm.sb[j] : 0;
-  sp.s = sp.on ? j - sm.f[sp.b] : 0;
-  sp.pos = sm.pos[sp.b];
-  sp.k0 = sp.s * sm.ks;
-  sp.k1 = min(sp.k0 + sm.ks, sp.pos + 1);
+  sp.on = __builtin_amdgcn_readfirstlane(j < sm.nsplit ? 1 : 0) != 0;
+  sp.b = __builtin_amdgcn_readfirstlane(sp.on ? sm.sb[j] : 0);
+  sp.s = __builtin_amdgcn_readfirstlane(sp.on ? j - sm.f[sp.b] : 0);
+  sp.pos = __builtin_amdgcn_readfirstlane(sm.pos[sp.b]);
+  sp.k0 = sp.s * __builtin_amdgcn_readfirstlane(sm.ks);
+  sp.k1 = min(sp.k0 + __builtin_amdgcn_readfirstlane(sm.ks), sp.pos + 1);
   if (tid < 32) {
     const uint16_t* src = (tid < 16 ? a.cos_tab : a.sin_tab) + (size_t)sp.pos * D + 8 * (tid & 15);
     *reinterpret_cast<uint4*>(&sm.cs[tid >> 4][8 * (tid & 15)]) = *reinterpret_cast<const uint4*>(src);
@@ -824,20 +903,23 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     const int gw = j * NXCD + x, ntiles = a.vocab / 16;
     u64 best = 0;
     const __amdgpu_buffer_rsrc_t rlm = make_rsrc(a.lm_head);
-    auto load_chunk = [&](uint4 (&w)[8], int tile, int ch) {
-      const int off = ((16 * tile + li) * H + 256 * ch + 8 * g) * 2;
+    // a tile (16 rows x H) in NC chunks of CH K steps, two chunk buffers in flight
+    constexpr int CH = MKB_LM_CH, NC = H / 32 / CH;
+    static_assert(NC >= 2 && NC % 2 == 0, "LM head chunks");
+    auto load_chunk = [&](uint4 (&w)[CH], int tile, int ch) {
+      const int off = ((16 * tile + li) * H + 32 * CH * ch + 8 * g) * 2;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) w[s] = ldnt(rlm, off + 64 * s);
+      for (int s = 0; s < CH; ++s) w[s] = ldnt(rlm, off + 64 * s);
     };
-    auto mma_chunk = [&](const uint4 (&w)[8], int ch, f32x4& acc) {
+    auto mma_chunk = [&](const uint4 (&w)[CH], int ch, f32x4& acc) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint4 bo = *reinterpret_cast<const uint4*>(&sm.act[li][256 * ch + 32 * s + 8 * g]);
+      for (int s = 0; s < CH; ++s) {
+        const uint4 bo = *reinterpret_cast<const uint4*>(&sm.act[li][32 * CH * ch + 32 * s + 8 * g]);
         acc = mfma(w[s], bo, acc);
       }
     };
     int tile = gw + NWG * wave;
-    uint4 wa[8], wb[8];
+    uint4 wa[CH], wb[CH];
     if (tile < ntiles) {
       load_chunk(wa, tile, 0);
       load_chunk(wb, tile, 1);
@@ -847,14 +929,15 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       const int next = tile + NWG * NWAVE;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      mma_chunk(wa, 0, acc);
-      load_chunk(wa, tile, 2);
-      mma_chunk(wb, 1, acc);
-      load_chunk(wb, tile, 3);
-      mma_chunk(wa, 2, acc);
-      if (next < ntiles) load_chunk(wa, next, 0);
-      mma_chunk(wb, 3, acc);
-      if (next < ntiles) load_chunk(wb, next, 1);
+#pragma unroll
+      for (int ch = 0; ch < NC; ch += 2) {
+        mma_chunk(wa, ch, acc);
+        if (ch + 2 < NC) load_chunk(wa, tile, ch + 2);
+        else if (next < ntiles) load_chunk(wa, next, 0);
+        mma_chunk(wb, ch + 1, acc);
+        if (ch + 3 < NC) load_chunk(wb, tile, ch + 3);
+        else if (next < ntiles) load_chunk(wb, next, 1);
+      }
       float lg[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) lg[r] = (acc[r] + dpp<0xB1>(acc[r])) * rs;  // hi + lo columns

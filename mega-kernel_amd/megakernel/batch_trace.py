@@ -11,10 +11,11 @@ workgroup), so the gaps between consecutive points show where a layer's time goe
 The points (thread 0 of each workgroup, comm wave 0, unless marked math: thread 0 of the first math
 wave): A start; residual + input norm done (the previous layer's down sums polled); QKV tile done;
 QKV rows published; [attention workgroups: q/k/v polled; math: attention start, scores done;
-attention done; math: split partial published]; split partials polled; splits merged; o_proj tile
-done; o_proj rows published; o_proj row block summed over the XCDs and republished; residual +
-post-attention norm done (sums polled); gate/up tile done; SiLU outputs polled; down tile done;
-down rows published; down row block summed and republished.
+attention done; math: split partial published]; split partials polled; all comm waves' polls done
+(barrier C1); splits merged; o_proj tile done; o_proj rows published; o_proj row block summed over
+the XCDs and republished; residual + post-attention norm done (sums polled); gate/up tile done;
+SiLU outputs published; SiLU outputs polled; down tile done; down rows published; down row block
+summed and republished.
 """
 import argparse
 import ctypes
@@ -26,8 +27,8 @@ MAXL, SLOTS, GRID = 32, 24, 256
 NAMES = ("A start", "A residual+norm", "A qkv tile", "A qkv pub", "B qkv polled", "B attention",
          "C splits polled", "C merged", "C o tile", "D gather+pub", "E residual+norm", "E gate/up tile",
          "F silu polled", "F down tile", "G gather+pub", "B partial pub (math)", "D o rows pub",
-         "G down rows pub", "B start (math)", "B scores done (math)")
-ORDER = (0, 1, 2, 3, 4, 18, 19, 5, 15, 6, 7, 8, 16, 9, 10, 11, 12, 13, 17, 14)
+         "G down rows pub", "B start (math)", "B scores done (math)", "C1 passed", "F silu pub")
+ORDER = (0, 1, 2, 3, 4, 18, 19, 5, 15, 6, 20, 7, 8, 16, 9, 10, 11, 21, 12, 13, 17, 14)
 ATT_SLOTS = (4, 5, 15, 18, 19)
 
 
@@ -39,8 +40,11 @@ def report(t, layers, att_mask):
     kernel_us = t[:, MAXL, 2].max() * TICK_US
     lm_us = (t[:, MAXL, 2].max() - t[:, MAXL, 1].min()) * TICK_US
     per_layer = [(t[:, l + 1, 0].mean() - t[:, l, 0].mean()) * TICK_US for l in range(lo, min(hi, layers - 1))]
+    lm_wg = (t[:, MAXL, 2] - t[:, MAXL, 1]) * TICK_US
     lines.append(f"kernel {kernel_us:.1f} us; mean layer {np.mean(per_layer):.2f} us (layers {lo}..{hi - 1}); "
-                 f"LM head {lm_us:.1f} us; first layer starts {t[:, 0, 0].mean() * TICK_US:.1f} us after kernel start")
+                 f"LM head {lm_us:.1f} us (per workgroup mean {lm_wg.mean():.1f}, max {lm_wg.max():.1f}; starts "
+                 f"spread over {(t[:, MAXL, 1].max() - t[:, MAXL, 1].min()) * TICK_US:.1f}); first layer starts "
+                 f"{t[:, 0, 0].mean() * TICK_US:.1f} us after kernel start")
     lines.append(f"{'point':22s} {'mean us':>8s} {'max us':>8s}   (since the layer's A start, mean over layers)")
     for s in ORDER:
         name = NAMES[s]
