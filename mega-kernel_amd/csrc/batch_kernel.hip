@@ -75,6 +75,10 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 // each goes where the comm waves' next poll is furthest away. Measured at 8 sequences of 257 keys
 // (0.6B): gate/up+down after the attention publish 797 us per step, gate/up after C1 729, and the
 // defaults below 708.
+// The split merge on all waves (1) or on the comm waves only (0), the math waves issuing loads meanwhile.
+#ifndef MKB_MERGE_ALL
+#define MKB_MERGE_ALL 1
+#endif
 // K steps per load chunk of the LM head (two chunks in flight per wave).
 #ifndef MKB_LM_CH
 #define MKB_LM_CH 8
@@ -85,6 +89,9 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 #endif
 #ifndef MKB_GU_AT
 #define MKB_GU_AT 4
+#endif
+#ifndef MKB_GU2_AT
+#define MKB_GU2_AT 6  // >= 0: the second half of the gate/up rows at this point (-1: all at GU_AT)
 #endif
 #ifndef MKB_DN_AT
 #define MKB_DN_AT 8
@@ -361,7 +368,9 @@ __device__ __forceinline__ void gather(Ctl& c, const BArgs& a, size_t cross, siz
 }
 
 // Publishes the workgroup's OR output rows of every sequence as cross-XCD partials: tile t (computed by
-// math waves 4t..4t+3) on comm wave t, lane (b, 4 rows).
+// math waves 4t..4t+3) on math wave t, lane (b, 4 rows). The math waves publish every product (they
+// poll nothing): on this GPU one counter tracks a wave's loads and stores, so a wave that polls after
+// storing would wait for its store to be acknowledged first.
 template <int T>
 __device__ __forceinline__ void publish_tile(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int x, int j) {
   const int lane = tix() & 63;
@@ -372,10 +381,38 @@ __device__ __forceinline__ void publish_tile(const Smem& sm, const BArgs& a, siz
   for (int i = 0; i < 4; ++i) v[i] = red_sum<4 * T, 4>(sm, r0 + i, b);
   st4<true>(a.ws + cross + ((size_t)j * NXCD + x) * BM * OR, b * OR + 16 * T + r0, v, ep);
 }
-__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int wave,
+__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int m,
                                              int x, int j) {
-  if (wave == 0) publish_tile<0>(sm, a, cross, ep, x, j);
-  else if (wave == 1) publish_tile<1>(sm, a, cross, ep, x, j);
+  if (m == 0) publish_tile<0>(sm, a, cross, ep, x, j);
+  else if (m == 1) publish_tile<1>(sm, a, cross, ep, x, j);
+}
+// QKV rows (all 8 math waves computed the tile over K): math wave 0, lane (b, 4 rows), scaled by the
+// input norm's scale.
+__device__ __forceinline__ void publish_qkv(const Smem& sm, const BArgs& a, uint32_t ep, int x, int j) {
+  const int lane = tix() & 63;
+  if (lane >= 4 * a.B) return;
+  const int b = lane >> 2, r0 = 4 * (lane & 3);
+  const float rs = norm_scale(sm, b);
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = red_sum<0, NMW>(sm, r0 + i, b) * rs;
+  st4<false>(a.ws + W_QX + (size_t)x * BM * QX + QR * j, b * QX + r0, v, ep);
+}
+// silu(gate) * up of the workgroup's intermediates (gate tile on math waves 0-3, up on 4-7), scaled by
+// the post-attention norm's scale: math wave 0, lane (b, 4 intermediates).
+__device__ __forceinline__ void publish_silu(const Smem& sm, const BArgs& a, uint32_t ep, int x, int j) {
+  const int lane = tix() & 63;
+  if (lane >= 3 * a.B) return;
+  const int b = lane / 3, q = lane % 3;
+  const float rs = norm_scale(sm, b);
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ii = 4 * q + i;
+    const float gt = red_sum<0, 4>(sm, ii, b) * rs, up = red_sum<4, 4>(sm, ii, b) * rs;
+    v[i] = gt / (1.f + expf(-gt)) * up;
+  }
+  st4<false>(a.ws + W_MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
 }
 
 // q/k RMSNorm + rotate-half RoPE of one head row held by 32 lanes (lane c % 32: dims 4c..4c+3; the RoPE
@@ -447,12 +484,13 @@ __device__ __forceinline__ void load_o(uint4 (&w)[2], const mk_layer_weights& lw
 // Rows 12-15 of the tile are empty: their lanes load row 11 again (every lane of the wave issues the
 // same loads, so the compiler's count of loads in flight stays exact and later waits need not wait
 // for the whole burst) and keep zeros.
+template <int S0 = 0, int S1 = 8>
 __device__ __forceinline__ void load_gu(uint4 (&w)[8], const mk_layer_weights& lw, const MathLane& ml, int x, int j) {
   const uint16_t* m0 = (const uint16_t*)(ml.m < 4 ? lw.gate_proj_weight : lw.up_proj_weight);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(m0 + ((size_t)IX * x + GI * j) * H);
   const int off = (min(ml.li, GI - 1) * H + 256 * (ml.m & 3) + 8 * ml.g) * 2;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) w[s] = ldnt(rs, off + 64 * s);
+  for (int s = S0; s < S1; ++s) w[s] = ldnt(rs, off + 64 * s);
 }
 // zeros in the empty rows of the gate/up tile (applied just before the tile's MFMAs)
 __device__ __forceinline__ void mask_gu(uint4 (&w)[8], const MathLane& ml) {
@@ -519,8 +557,7 @@ __device__ __forceinline__ void softmax_step(float sc, const float (&v)[8], floa
 
 // Merge of every sequence's split partials (polled into LDS) into the o_proj operand: thread (b, head
 // h, 4 dims) for b < B (one pass of B * 64 threads), max-first over the sequence's splits.
-__device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a) {
-  const int o = tix();
+__device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a, int o) {
   if (o >= a.B * 64) return;
   const int b = o >> 6, h = (o >> 5) & 1, d0 = 4 * (o & 31);
   const float* p = sm.stg + (size_t)sm.f[b] * APW;
@@ -545,12 +582,26 @@ __device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a) {
     for (int s = 1; s < 4; ++s) M = s < n ? fmaxf(M, ml[s].x) : M;
 #pragma unroll
     for (int s = 0; s < 4; ++s) add(acc[s], ml[s].y, s < n ? __expf(ml[s].x - M) : 0.f);
-  } else {
+  } else {  // many key ranges (a long sequence in a small batch): four at a time, loads first
     float M = -INFINITY;
-    for (int s = 0; s < n; ++s) M = fmaxf(M, p[s * APW + 2 * D + 2 * h]);
-    for (int s = 0; s < n; ++s) {
-      const float* q = p + s * APW;
-      add(*reinterpret_cast<const float4*>(q + h * D + d0), q[2 * D + 2 * h + 1], __expf(q[2 * D + 2 * h] - M));
+    for (int s0 = 0; s0 < n; s0 += 4) {
+      float mm[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) mm[s] = p[min(s0 + s, n - 1) * APW + 2 * D + 2 * h];  // repeats: same max
+#pragma unroll
+      for (int s = 0; s < 4; ++s) M = fmaxf(M, mm[s]);
+    }
+    for (int s0 = 0; s0 < n; s0 += 4) {
+      float2 ml[4];
+      float4 acc[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* q = p + min(s0 + s, n - 1) * APW;
+        ml[s] = *reinterpret_cast<const float2*>(q + 2 * D + 2 * h);
+        acc[s] = *reinterpret_cast<const float4*>(q + h * D + d0);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) add(acc[s], ml[s].y, s0 + s < n ? __expf(ml[s].x - M) : 0.f);
     }
   }
   const float r = 1.f / Ls;
@@ -598,15 +649,6 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // A1
     lds_barrier();  // A2
     mark(a, x, j, l, 2);
-    if (tid < 4 * a.B) {  // QKV rows: lane (b, 4 rows)
-      const int b = tid >> 2, r0 = 4 * (tid & 3);
-      const float rs = norm_scale(sm, b);
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = red_sum<0, NMW>(sm, r0 + i, b) * rs;
-      st4<false>(a.ws + W_QX + (size_t)x * BM * QX + QR * j, b * QX + r0, v, ep);
-    }
-    mark(a, x, j, l, 3);
     // ---- B: this workgroup's sequence's q/k/v sums for the attention
     if (sp.on) {
       if (tid < QX / 4) {  // waves 0-1: lane tid holds dims 4 (tid % 32) .. +3 of row tid / 32 (q0, q1, k, v)
@@ -626,14 +668,12 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     mark(a, x, j, l, 6);
     lds_barrier();  // C1
     mark(a, x, j, l, 20);
-    merge_splits(sm, a);
+    for (int o = tid; o < a.B * 64; o += MKB_MERGE_ALL ? NT : CL) merge_splits(sm, a, o);
     lds_barrier();  // C2
     mark(a, x, j, l, 7);
     lds_barrier();  // C3
     mark(a, x, j, l, 8);
-    // ---- D, E: o_proj partials out, row block j summed over the XCDs, residual + post-attention norm
-    publish_rows(sm, a, W_OX, ep, wave, x, j);
-    mark(a, x, j, l, 16);
+    // ---- D, E: row block j of the o_proj partials summed over the XCDs, residual + post-attention norm
     if (wave == 0) gather(c, a, W_OX, W_OL, ep, x, j);
     mark(a, x, j, l, 9);
     residual_norm<false>(sm, c, a, a.ws + W_OL + (size_t)x * BM * H, ep, (const uint16_t*)lw.post_attn_norm_weight);
@@ -641,20 +681,7 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // E1
     lds_barrier();  // E2
     mark(a, x, j, l, 11);
-    // ---- F: SiLU outputs, then the XCD's SiLU outputs into the operand
-    if (tid < 3 * a.B) {
-      const int b = tid / 3, q = tid % 3;
-      const float rs = norm_scale(sm, b);
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ii = 4 * q + i;
-        const float gt = red_sum<0, 4>(sm, ii, b) * rs, up = red_sum<4, 4>(sm, ii, b) * rs;
-        v[i] = gt / (1.f + expf(-gt)) * up;
-      }
-      st4<false>(a.ws + W_MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
-    }
-    mark(a, x, j, l, 21);
+    // ---- F: the XCD's SiLU outputs into the operand
     {
       constexpr int NK = (BM * IX / 4) / CL;  // 3
       const int nch = a.B * (IX / 4);
@@ -680,9 +707,7 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // F1
     lds_barrier();  // F2
     mark(a, x, j, l, 13);
-    // ---- G: down partials out, row block j summed over the XCDs
-    publish_rows(sm, a, W_DX, ep, wave, x, j);
-    mark(a, x, j, l, 17);
+    // ---- G: row block j of the down partials summed over the XCDs
     if (wave == 0) gather(c, a, W_DX, W_DL, ep, x, j);
     mark(a, x, j, l, 14);
   }
@@ -706,7 +731,9 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     const uint32_t ep = (uint32_t)l + 1;
     const bool next = l + 1 < a.L;
     auto issue = [&](int p) {
-      if (p == MKB_GU_AT) load_gu(wg, lw, ml, x, j);
+      if (MKB_GU2_AT < 0 && p == MKB_GU_AT) load_gu(wg, lw, ml, x, j);
+      if (MKB_GU2_AT >= 0 && p == MKB_GU_AT) load_gu<0, 4>(wg, lw, ml, x, j);
+      if (MKB_GU2_AT >= 0 && p == MKB_GU2_AT) load_gu<4, 8>(wg, lw, ml, x, j);
       if (p == MKB_DN_AT) load_down(wd, lw, ml, x, j);
       if (p == MKB_QKV_AT && next) load_qkv(wq, a.lw[l + 1], ml, x, j);
       if (p == MKB_O_AT && next) load_o(wo, a.lw[l + 1], ml, x, j);
@@ -716,6 +743,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     issue(0);
     mma_to_red<4>(sm, wq, 4 * ml.m, ml);
     lds_barrier();  // A2
+    if (ml.m == 0) publish_qkv(sm, a, ep, x, j);
     issue(1);
     if (!sp.on) {
       issue(2);
@@ -801,22 +829,27 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     }
     lds_barrier();  // C1
     issue(4);
-    merge_splits(sm, a);
+    mark(a, x, j, l, 22, 64 * NCW);
+    if (MKB_MERGE_ALL) merge_splits(sm, a, tid);
+    mark(a, x, j, l, 23, 64 * NCW);
     lds_barrier();  // C2
     issue(5);
     mma_to_red<2>(sm, wo, 2 * (ml.m & 3), ml);
     lds_barrier();  // C3
+    publish_rows(sm, a, W_OX, ep, ml.m, x, j);
     issue(6);
     lds_barrier();  // E1
     issue(7);
     mask_gu(wg, ml);
     mma_to_red<8>(sm, wg, 8 * (ml.m & 3), ml);
     lds_barrier();  // E2
+    if (ml.m == 0) publish_silu(sm, a, ep, x, j);
     issue(8);
     lds_barrier();  // F1
     issue(9);
     mma_to_red<3>(sm, wd, 3 * (ml.m & 3), ml);
     lds_barrier();  // F2
+    publish_rows(sm, a, W_DX, ep, ml.m, x, j);
     issue(10);
   }
   lds_barrier();  // the final norm

@@ -9,13 +9,13 @@ workgroup), so the gaps between consecutive points show where a layer's time goe
     python -m megakernel.batch_trace --shape qwen3-0.6b --batch 8 --context 256
 
 The points (thread 0 of each workgroup, comm wave 0, unless marked math: thread 0 of the first math
-wave): A start; residual + input norm done (the previous layer's down sums polled); QKV tile done;
-QKV rows published; [attention workgroups: q/k/v polled; math: attention start, scores done;
-attention done; math: split partial published]; split partials polled; all comm waves' polls done
-(barrier C1); splits merged; o_proj tile done; o_proj rows published; o_proj row block summed over
-the XCDs and republished; residual + post-attention norm done (sums polled); gate/up tile done;
-SiLU outputs published; SiLU outputs polled; down tile done; down rows published; down row block
-summed and republished.
+wave): A start; residual + input norm done (the previous layer's down sums polled); QKV tile done
+(the math waves publish the rows); [attention workgroups: q/k/v polled and normalised; math:
+attention start, scores done; attention done; math: split partial published]; split partials
+polled; all comm waves' polls done (barrier C1); math: gate/up rows issued, merge done; splits
+merged; o_proj tile done; o_proj row block summed over the XCDs and republished; residual +
+post-attention norm done (sums polled); gate/up tile done; SiLU outputs polled; down tile done;
+down row block summed and republished.
 """
 import argparse
 import ctypes
@@ -24,11 +24,11 @@ import numpy as np
 
 TICK_US = 0.01
 MAXL, SLOTS, GRID = 32, 24, 256
-NAMES = ("A start", "A residual+norm", "A qkv tile", "A qkv pub", "B qkv polled", "B attention",
+NAMES = ("A start", "A residual+norm", "A qkv tile", "", "B qkv polled", "B attention",
          "C splits polled", "C merged", "C o tile", "D gather+pub", "E residual+norm", "E gate/up tile",
-         "F silu polled", "F down tile", "G gather+pub", "B partial pub (math)", "D o rows pub",
-         "G down rows pub", "B start (math)", "B scores done (math)", "C1 passed", "F silu pub")
-ORDER = (0, 1, 2, 3, 4, 18, 19, 5, 15, 6, 20, 7, 8, 16, 9, 10, 11, 21, 12, 13, 17, 14)
+         "F silu polled", "F down tile", "G gather+pub", "B partial pub (math)", "", "", "B start (math)",
+         "B scores done (math)", "C1 passed", "", "C gate/up issued (math)", "C merge done (math)")
+ORDER = (0, 1, 2, 4, 18, 19, 5, 15, 6, 20, 22, 23, 7, 8, 9, 10, 11, 12, 13, 14)
 ATT_SLOTS = (4, 5, 15, 18, 19)
 
 
