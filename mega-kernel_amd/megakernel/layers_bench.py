@@ -1,5 +1,5 @@
 """Timing of the layer-by-layer engine: the batched prefill (``prefill``) and the batched decode
-(``decode_batch``), on random-init bf16 weights of a Qwen3 shape (``model.build_model``, seed 0),
+(``decode_batch``, either engine), on random-init bf16 weights of a Qwen3 shape (``model.build_model``, seed 0),
 with HIP events around each call on the current stream.
 
     cd mega-kernel_amd
@@ -42,6 +42,8 @@ def main(argv=None):
     ap.add_argument("--max-seq", type=int, default=4096)
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--engine", type=int, default=0, choices=(0, 1, 2),
+                    help="decode_batch engine: 0 automatic, 1 layer by layer, 2 persistent kernel (where it applies)")
     ap.add_argument("--transformers", action="store_true",
                     help="also time the reference path: Transformers' GPU prefill plus the cache copy")
     a = ap.parse_args(argv)
@@ -50,6 +52,7 @@ def main(argv=None):
     from model import build_model
 
     kernel = megakernel.load()
+    kernel.set_batch_engine(a.engine)
     dev = torch.device("cuda:0")
     model = build_model(a.shape, a.max_seq)
     lw = [t.to(dev) for t in megakernel.layer_weight_list(model)]
@@ -91,7 +94,7 @@ def main(argv=None):
         pos = torch.full((B,), a.context, dtype=torch.int32, device=dev)
         med, runs = _time(lambda: kernel.decode_batch(toks, pos, embed, embed, fn, lw, cos, sin, kc, vc, a.max_seq),
                           a.warmup, a.runs)
-        print(f"[decode_batch {a.shape} B={B} context={a.context}] {med * 1e3:.1f} us per step median of "
+        print(f"[decode_batch {a.shape} B={B} context={a.context} engine {a.engine}] {med * 1e3:.1f} us per step median of "
               f"{len(runs)} ({B / med * 1e3:,.0f} tokens/s)", flush=True)
         del kc, vc
     if kernel.status() != 0:

@@ -322,3 +322,19 @@ def test_batch_entry_point_rejects_bad_arguments_before_launch(lib):
     assert call(nbytes=1024) == HIP_ERROR_INVALID_VALUE
     assert call(workspace=vp(256 + 64)) == HIP_ERROR_INVALID_VALUE
     assert call(workspace=None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_batch_engine_and_trace_entry_points_check_their_arguments(lib):
+    """mk_set_batch_engine takes 0, 1 or 2 only; mk_set_batch_trace refuses a buffer smaller than
+    mk_batch_trace_bytes() (one stamp row per workgroup and layer) and accepts NULL (trace off).
+    Neither launches anything."""
+    assert lib.mk_set_batch_engine(3) == HIP_ERROR_INVALID_VALUE
+    assert lib.mk_set_batch_engine(-1) == HIP_ERROR_INVALID_VALUE
+    for e in (1, 2, 0):
+        assert lib.mk_set_batch_engine(e) == HIP_SUCCESS
+    lib.mk_batch_trace_bytes.restype = ctypes.c_size_t
+    lib.mk_set_batch_trace.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    need = lib.mk_batch_trace_bytes()
+    assert need == 256 * 33 * 24 * 8
+    assert lib.mk_set_batch_trace(ctypes.c_void_p(16), need - 8) == HIP_ERROR_INVALID_VALUE
+    assert lib.mk_set_batch_trace(None, 0) == HIP_SUCCESS
