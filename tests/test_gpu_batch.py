@@ -26,6 +26,11 @@ def mini17():
     return Session("mini-1.7b", 512)
 
 
+@pytest.fixture(scope="module")
+def mini2k():
+    return Session("mini", 2048)
+
+
 def _batched_cache(sess, prompts):
     """Oracle prefill of each prompt into its slot of a [B, L, 8, max_seq, 128] cache (CPU), and each
     prompt's greedy next token."""
@@ -62,6 +67,8 @@ def engine(request):
     ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4, 2),
     ("mini", (495,), 3, 2),                              # one sequence: 31 key ranges of 16, then 16 of 32
     ("mini", (509, 3, 260, 1, 400, 90, 128), 2, 2),      # 27 key ranges of 64 over 7 sequences
+    ("mini2k", (1900, 1300, 2000, 700), 2, 2),             # ranges of 224 keys: 2 rounds of K/V loads, 9 ranges
+    ("mini2k", (2000,), 2, 2),                             # one sequence in 26 ranges of 80 keys
     ("mini17", (33, 200, 90), 4, 1),
     ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
     ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
