@@ -357,6 +357,7 @@ __device__ __forceinline__ void gather(Ctl& c, const BArgs& a, size_t cross, siz
   for (int xs = 0; xs < NXCD; ++xs) off[xs] = ((xs * BM + b) * OR + 4 * q) * 4;
   float v[NXCD][4];
   poll<NXCD>(c, a.ws + cross + (size_t)j * NXCD * BM * OR, off, ep, v);
+  if (cross == W_OX) mark(a, x, j, ep - 1, 17);
   float s[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -837,6 +838,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     mma_to_red<2>(sm, wo, 2 * (ml.m & 3), ml);
     lds_barrier();  // C3
     publish_rows(sm, a, W_OX, ep, ml.m, x, j);
+    mark(a, x, j, l, 16, 64 * NCW);
     issue(6);
     lds_barrier();  // E1
     issue(7);

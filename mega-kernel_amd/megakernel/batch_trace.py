@@ -13,7 +13,8 @@ wave): A start; residual + input norm done (the previous layer's down sums polle
 (the math waves publish the rows); [attention workgroups: q/k/v polled and normalised; math:
 attention start, scores done; attention done; math: split partial published]; split partials
 polled; all comm waves' polls done (barrier C1); math: gate/up rows issued, merge done; splits
-merged; o_proj tile done; o_proj row block summed over the XCDs and republished; residual +
+merged; o_proj tile done; math: o_proj rows published; the 8 XCDs' partials of row block j polled;
+its sum republished; residual +
 post-attention norm done (sums polled); gate/up tile done; SiLU outputs polled; down tile done;
 down row block summed and republished.
 """
@@ -26,9 +27,10 @@ TICK_US = 0.01
 MAXL, SLOTS, GRID = 32, 24, 256
 NAMES = ("A start", "A residual+norm", "A qkv tile", "", "B qkv polled", "B attention",
          "C splits polled", "C merged", "C o tile", "D gather+pub", "E residual+norm", "E gate/up tile",
-         "F silu polled", "F down tile", "G gather+pub", "B partial pub (math)", "", "", "B start (math)",
+         "F silu polled", "F down tile", "G gather+pub", "B partial pub (math)", "D o rows pub (math)",
+         "D gather polled", "B start (math)",
          "B scores done (math)", "C1 passed", "", "C gate/up issued (math)", "C merge done (math)")
-ORDER = (0, 1, 2, 4, 18, 19, 5, 15, 6, 20, 22, 23, 7, 8, 9, 10, 11, 12, 13, 14)
+ORDER = (0, 1, 2, 4, 18, 19, 5, 15, 6, 20, 22, 23, 7, 8, 16, 17, 9, 10, 11, 12, 13, 14)
 ATT_SLOTS = (4, 5, 15, 18, 19)
 
 
