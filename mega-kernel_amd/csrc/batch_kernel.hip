@@ -1,4 +1,4 @@
-// Persistent batched decode on MI355X (gfx950): up to 8 sequences of the Qwen3-0.6B shape advance
+// Persistent batched decode on MI355X (gfx950): up to 16 sequences of the Qwen3-0.6B shape advance
 // one token each in one launch of 256 workgroups, one per CU, with no grid barrier and no kernel
 // boundary between layers.
 //
@@ -6,8 +6,9 @@
 // grid with grid.sync() between phases). The layer-by-layer engine of this library runs a batch as
 // ~220 short kernels per step, and on MI355X every kernel boundary costs a few microseconds (launch,
 // cache write-back and invalidation across the 8 XCDs) on top of each kernel's own ramp. Here the
-// batch is the 16 columns of the matrix-core tile instead (sequence b's activations as bf16 hi in
-// column 2b and lo in column 2b + 1), and workgroups hand data to each other through 32-bit
+// batch is the columns of the matrix-core tiles instead (sequence b's activations as bf16 hi in
+// column 2b and lo in column 2b + 1: one block of 16 columns for up to 8 sequences, two for up to
+// 16), and workgroups hand data to each other through 32-bit
 // "LL" words (value and epoch in one word) as the single-sequence decode kernel does:
 //
 //   XCD x owns K/V head x: its 512 q/k/v rows (16 per workgroup), its attention, its 256 input
@@ -17,22 +18,25 @@
 //     B  split-K attention of one (sequence, key range) per workgroup, q/k norm + RoPE, cache write
 //                                                               -> publish partial (local)
 //     C  merge of every sequence's splits -> o_proj partial      -> publish (cross-XCD)
-//     D  workgroup j sums row block j over the 8 XCDs            -> republish (local)
-//     E  residual, post-attention RMSNorm -> gate/up + SiLU      -> publish (local)
+//     D  workgroup j adds row block j over the 8 XCDs to the residual -> republish (local)
+//     E  post-attention RMSNorm -> gate/up + SiLU                -> publish (local)
 //     F  down_proj partial                                       -> publish (cross-XCD)
-//     G  workgroup j sums row block j over the 8 XCDs            -> republish (local)
+//     G  workgroup j adds row block j over the 8 XCDs to the residual -> republish (local)
 //   then the final norm and the tied LM head with the greedy keys (finish kernel: tokens).
 //
-// Every workgroup keeps the whole residual [B][1024] in LDS, bitwise identical across workgroups
-// (same data, same order). Waves 0-3 (comm) poll, publish and do the vector work; waves 4-11
+// The fp32 residual of row block j lives in the registers of the lanes that sum that block (each
+// XCD's workgroup j holds a bitwise identical copy: same data, same order); every workgroup reads
+// the whole residual back from its XCD's republished words before a norm. Waves 0-3 (comm) poll,
+// publish and do the vector work; waves 4-11
 // (math) hold weights in registers, issued phases ahead, and run the MFMA tiles and the attention.
 // Workgroups learn their XCD from the hardware register and their index in it from a ticket counter,
 // so the exchange layout never depends on how the dispatcher placed the grid. Every wait is
 // bounded; a timeout (or a host drain request) aborts the launch, which then reports NaN logits
 // and token -1 for every sequence.
 //
-// Numerics are the single-sequence kernel's: fp32 residual, fp32 RMSNorm (scale applied to the
-// product outputs, a linear map), fp32 softmax, exchanged values rounded to 24 bits, bf16 new K/V.
+// Numerics: fp32 residual, fp32 RMSNorm (scale applied to the product outputs, a linear map), fp32
+// softmax, exchanged values (partials, and the residual as read for a norm) rounded to 24 bits, bf16
+// new K/V.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,7 +54,7 @@ using namespace mkp;
 constexpr int NXCD = 8, WPX = 32, NWG = NXCD * WPX;
 constexpr int NCW = 4, NMW = 8, NWAVE = NCW + NMW, NT = 64 * NWAVE;  // 768 threads
 constexpr int CL = 64 * NCW;            // comm lanes
-constexpr int BM = 8;                   // sequences per launch (hi and lo of 8 fill the 16 columns)
+constexpr int BMAX = 16;                // sequences per launch: CB column blocks of 8 (hi and lo of 8 fill 16 columns)
 constexpr int H = 1024, I = 3072, IX = I / NXCD;
 constexpr int QX = 4 * D;               // q (2 heads), k, v rows of one K/V head: 512
 constexpr int QR = QX / WPX;            // 16 rows per workgroup
@@ -58,7 +62,7 @@ constexpr int OR = H / WPX;             // 32 o_proj rows (and down_proj rows) p
 constexpr int GI = IX / WPX;            // 12 intermediates per workgroup
 constexpr int APW = 2 * D + 4;          // attention partial: acc[2][128], m0, l0, m1, l1
 constexpr int KST = H + 8;              // LDS row stride of the MFMA B operand (bf16): conflict-free reads
-constexpr int RST = 20;                 // LDS row stride of the reduction tiles (floats): conflict-free writes
+template <int CB> constexpr int rst() { return 16 * CB + 4; }  // reduction tile row stride (floats): conflict-free
 constexpr int MAXL = 32;
 constexpr int NG = 4 * NMW;             // 16-lane attention groups per workgroup
 constexpr int RB = 4;                   // keys per group and round of K/V loads
@@ -108,24 +112,28 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 static_assert(MKB_GU_AT <= 6 && MKB_DN_AT <= 8 && MKB_QKV_AT >= 1 && MKB_O_AT >= 6 && MKB_KV_AT >= 3,
               "load schedule");
 
-// Exchange area (32-bit words), zeroed before every launch: epoch 0 never matches.
-constexpr size_t W_QX = 0;                                   // [8][BM][512]    q/k/v sums (local)
-constexpr size_t W_AX = W_QX + (size_t)NXCD * BM * QX;       // [8][32][260]    split partials (local)
-constexpr size_t W_OX = W_AX + (size_t)NXCD * WPX * APW;     // [32][8][BM][32] o_proj partials (cross)
-constexpr size_t W_OL = W_OX + (size_t)WPX * NXCD * BM * OR; // [8][BM][H]      o_proj sums (local)
-constexpr size_t W_MX = W_OL + (size_t)NXCD * BM * H;        // [8][BM][IX]     silu(gate) * up (local)
-constexpr size_t W_DX = W_MX + (size_t)NXCD * BM * IX;       // [32][8][BM][32] down partials (cross)
-constexpr size_t W_DL = W_DX + (size_t)WPX * NXCD * BM * OR; // [8][BM][H]      down sums (local)
-constexpr size_t W_TICK = W_DL + (size_t)NXCD * BM * H;      // [8] ticket counters, 64 words apart
-constexpr size_t W_ABORT = W_TICK + NXCD * 64;               // nonzero: the launch gave up
-constexpr size_t W_BAD = W_ABORT + 64;                       // nonzero: a token or position was out of range
-constexpr size_t W_ZERO = W_BAD + 64;                        // words zeroed per launch
-constexpr size_t W_KEYS = W_ZERO;                            // u64 [NWG][BM] greedy keys per workgroup
-constexpr size_t W_END = W_KEYS + 2 * (size_t)NWG * BM;
-constexpr size_t WS_BYTES = W_END * 4;
-static_assert(W_AX % 4 == 0 && W_OX % 4 == 0 && W_OL % 4 == 0 && W_MX % 4 == 0 && W_DX % 4 == 0 &&
-                  W_DL % 4 == 0 && W_KEYS % 2 == 0,
-              "16-byte chunks");
+// Exchange area (32-bit words) of a launch with up to BM sequences, zeroed before every launch
+// (epoch 0 never matches).
+template <int BM>
+struct WL {
+  static constexpr size_t QX_ = 0;                                     // [8][BM][512]    q/k/v sums (local)
+  static constexpr size_t AX = QX_ + (size_t)NXCD * BM * QX;           // [8][32][260]    split partials (local)
+  static constexpr size_t OX = AX + (size_t)NXCD * WPX * APW;          // [32][8][BM][32] o_proj partials (cross)
+  static constexpr size_t OL = OX + (size_t)WPX * NXCD * BM * OR;      // [8][BM][H]      o_proj sums (local)
+  static constexpr size_t MX = OL + (size_t)NXCD * BM * H;             // [8][BM][IX]     silu(gate) * up (local)
+  static constexpr size_t DX = MX + (size_t)NXCD * BM * IX;            // [32][8][BM][32] down partials (cross)
+  static constexpr size_t DL = DX + (size_t)WPX * NXCD * BM * OR;      // [8][BM][H]      down sums (local)
+  static constexpr size_t TICK = DL + (size_t)NXCD * BM * H;           // [8] ticket counters, 64 words apart
+  static constexpr size_t ABORT = TICK + NXCD * 64;                    // nonzero: the launch gave up
+  static constexpr size_t BAD = ABORT + 64;                            // nonzero: a token or position was out of range
+  static constexpr size_t ZERO = BAD + 64;                             // words zeroed per launch
+  static constexpr size_t KEYS = ZERO;                                 // u64 [NWG][BM] greedy keys per workgroup
+  static constexpr size_t END = KEYS + 2 * (size_t)NWG * BM;
+  static_assert(AX % 4 == 0 && OX % 4 == 0 && OL % 4 == 0 && MX % 4 == 0 && DX % 4 == 0 && DL % 4 == 0 &&
+                    KEYS % 2 == 0,
+                "16-byte chunks");
+};
+constexpr size_t WS_BYTES = WL<BMAX>::END * 4;
 
 struct BArgs {
   const int32_t* tokens;
@@ -155,10 +163,12 @@ __device__ __forceinline__ void mark(const BArgs& a, int x, int j, int row, int 
 
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
+// LDS of a launch with NCB column blocks of the MFMA operand (up to 8 NCB sequences).
+template <int NCB>
 struct Smem {
-  float xres[BM][H];             // residual
-  uint16_t act[16][KST];         // MFMA B operand: column 2b = hi, 2b + 1 = lo of sequence b
-  float red[NMW][16][RST];       // per-wave MFMA results
+  static constexpr int CB = NCB, BM = 8 * NCB;
+  uint16_t act[16 * CB][KST];    // MFMA B operand: column 2b = hi, 2b + 1 = lo of sequence b
+  float red[NMW][16][rst<CB>()];  // per-wave MFMA results (columns as in act)
   float gacc[NG][2][D];          // attention group partials
   float gml[NG][4];
   float stg[WPX * APW];          // polled split partials
@@ -196,7 +206,7 @@ __device__ __forceinline__ void st1(uint32_t* base, int off, float v, uint32_t e
 }
 
 struct Ctl {
-  uint32_t* ws;
+  uint32_t* abort;  // the launch's abort word
   bool failed;
 };
 
@@ -232,9 +242,9 @@ __device__ __forceinline__ void poll(Ctl& c, const uint32_t* base, const int (&o
       for (int i = 0; i < 4; ++i) v[k][i] = llv(r[k][i]);
   };
   auto give_up = [&](uint32_t it) {
-    if ((it & 63u) == 62u && ld_dev_u32(c.ws + W_ABORT) != 0) { c.failed = true; return true; }
+    if ((it & 63u) == 62u && ld_dev_u32(c.abort) != 0) { c.failed = true; return true; }
     if (it > SPIN_LIMIT) {
-      st_dev_u32(c.ws + W_ABORT, 1u);
+      st_dev_u32(c.abort, 1u);
       c.failed = true;
       return true;
     }
@@ -269,49 +279,49 @@ __device__ __forceinline__ void lds_barrier() {
 
 // ---- comm-wave vector work ------------------------------------------------------------------------
 
-// The residual of every sequence after adding `src` (or, at layer 0, set to the embedding rows),
-// then x * w (w the RMSNorm weight) into the MFMA operand as bf16 hi/lo, and each comm wave's sums of
-// squares per sequence. Comm lane c holds elements 4c..4c+3 of every sequence.
-template <bool EMBED>
-__device__ __forceinline__ void residual_norm(Smem& sm, Ctl& c, const BArgs& a, const uint32_t* src, uint32_t ep,
+// x * w (w the RMSNorm weight) of every sequence's residual, polled from `src` (or, at layer 0, the
+// embedding rows), into the MFMA operand as bf16 hi/lo, and each comm wave's sums of squares per
+// sequence. Comm lane c holds elements 4c..4c+3 of every sequence; 8 sequences per poll.
+template <bool EMBED, class S>
+__device__ __forceinline__ void residual_norm(S& sm, Ctl& c, const BArgs& a, const uint32_t* src, uint32_t ep,
                                               const uint16_t* w) {
+  constexpr int BM = S::BM;
   const int cl = tix(), e0 = 4 * cl;
-  float v[BM][4];
-  if constexpr (EMBED) {
-#pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      const int tok = sm.tok[b < a.B ? b : 0];
-      const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)tok * H + e0);
-      v[b][0] = bf16_lo(e.x); v[b][1] = bf16_hi(e.x); v[b][2] = bf16_lo(e.y); v[b][3] = bf16_hi(e.y);
-    }
-  } else {
-    int off[BM];
-#pragma unroll
-    for (int b = 0; b < BM; ++b) off[b] = ((b < a.B ? b : a.B - 1) * H + e0) * 4;
-    poll<BM>(c, src, off, ep, v);
-  }
   const uint2 wr = *reinterpret_cast<const uint2*>(w + e0);
   const float wv[4] = {bf16_lo(wr.x), bf16_hi(wr.x), bf16_lo(wr.y), bf16_hi(wr.y)};
   const int wave = cl >> 6, lane = cl & 63;
   float ss[BM];
 #pragma unroll
-  for (int b = 0; b < BM; ++b) {
-    ss[b] = 0.f;
-    if (b < a.B) {
-      float4* xr = reinterpret_cast<float4*>(&sm.xres[b][e0]);
-      float4 xv = *xr;
-      if constexpr (EMBED) xv = make_float4(v[b][0], v[b][1], v[b][2], v[b][3]);
-      else { xv.x += v[b][0]; xv.y += v[b][1]; xv.z += v[b][2]; xv.w += v[b][3]; }
-      *xr = xv;
-      const float y[4] = {xv.x * wv[0], xv.y * wv[1], xv.z * wv[2], xv.w * wv[3]};
-      uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
-      uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
-      *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
-      *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
-      ss[b] = xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w;
+  for (int h = 0; h < S::CB; ++h) {
+    float v[8][4];
+    if constexpr (EMBED) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int tok = sm.tok[8 * h + b < a.B ? 8 * h + b : 0];
+        const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)tok * H + e0);
+        v[b][0] = bf16_lo(e.x); v[b][1] = bf16_hi(e.x); v[b][2] = bf16_lo(e.y); v[b][3] = bf16_hi(e.y);
+      }
+    } else {
+      int off[8];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) off[b] = (min(8 * h + b, a.B - 1) * H + e0) * 4;
+      poll<8>(c, src, off, ep, v);
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int s = 8 * h + b;
+      ss[s] = 0.f;
+      if (s < a.B) {
+        const float y[4] = {v[b][0] * wv[0], v[b][1] * wv[1], v[b][2] * wv[2], v[b][3] * wv[3]};
+        uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
+        uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
+        *reinterpret_cast<uint2*>(&sm.act[2 * s][e0]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&sm.act[2 * s + 1][e0]) = make_uint2(l0, l1);
+        ss[s] = v[b][0] * v[b][0] + v[b][1] * v[b][1] + v[b][2] * v[b][2] + v[b][3] * v[b][3];
+      }
     }
   }
-  // the 8 wave reductions side by side
+  // the BM wave reductions side by side
 #pragma unroll
   for (int b = 0; b < BM; ++b) ss[b] = row16_sum(ss[b]);
 #pragma unroll
@@ -326,14 +336,15 @@ __device__ __forceinline__ void residual_norm(Smem& sm, Ctl& c, const BArgs& a, 
   }
 }
 
-__device__ __forceinline__ float norm_scale(const Smem& sm, int b) {
+template <class S>
+__device__ __forceinline__ float norm_scale(const S& sm, int b) {
   return rsqrtf((((sm.ssw[0][b] + sm.ssw[1][b]) + sm.ssw[2][b]) + sm.ssw[3][b]) / (float)H + EPS);
 }
 
 // Sum over the waves W0..W0+NW-1 of row r of the MFMA results, hi + lo columns of sequence b (all
 // LDS reads issued before the adds).
-template <int W0, int NW>
-__device__ __forceinline__ float red_sum(const Smem& sm, int r, int b) {
+template <int W0, int NW, class S>
+__device__ __forceinline__ float red_sum(const S& sm, int r, int b) {
   float v[NW][2];
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
@@ -347,49 +358,54 @@ __device__ __forceinline__ float red_sum(const Smem& sm, int r, int b) {
 }
 
 // Workgroup j of XCD x sums row block j (OR rows of every sequence) over the 8 XCDs' partials at
-// `cross` in a fixed order and republishes it in its XCD at `local`. Comm wave 0, lane (b, quad).
+// `cross` in a fixed order, adds it to its residual rows xr and republishes them in its XCD at
+// `local`. Comm waves 0..BM/8-1, thread t: sequence t / 8, rows 4 (t % 8) .. +3 of the block.
+template <int BM>
 __device__ __forceinline__ void gather(Ctl& c, const BArgs& a, size_t cross, size_t local, uint32_t ep, int x,
-                                       int j) {
-  const int lane = tix();  // wave 0
-  const int q8 = min(lane, 8 * a.B - 1), b = q8 >> 3, q = q8 & 7;
+                                       int j, float (&xr)[4]) {
+  const int t = tix();
+  const int q8 = min(t, 8 * a.B - 1), b = q8 >> 3, q = q8 & 7;
   int off[NXCD];
 #pragma unroll
   for (int xs = 0; xs < NXCD; ++xs) off[xs] = ((xs * BM + b) * OR + 4 * q) * 4;
   float v[NXCD][4];
   poll<NXCD>(c, a.ws + cross + (size_t)j * NXCD * BM * OR, off, ep, v);
-  if (cross == W_OX) mark(a, x, j, ep - 1, 17);
-  float s[4];
+  if (cross == WL<BM>::OX) mark(a, x, j, ep - 1, 17);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    s[i] = v[0][i];
+    float s = v[0][i];
 #pragma unroll
-    for (int xs = 1; xs < NXCD; ++xs) s[i] += v[xs][i];
+    for (int xs = 1; xs < NXCD; ++xs) s += v[xs][i];
+    xr[i] += s;
   }
-  if (lane < 8 * a.B) st4<false>(a.ws + local + (size_t)x * BM * H + j * OR, b * H + 4 * q, s, ep);
+  if (t < 8 * a.B) st4<false>(a.ws + local + (size_t)x * BM * H + j * OR, b * H + 4 * q, xr, ep);
 }
 
 // Publishes the workgroup's OR output rows of every sequence as cross-XCD partials: tile t (computed by
 // math waves 4t..4t+3) on math wave t, lane (b, 4 rows). The math waves publish every product (they
 // poll nothing): on this GPU one counter tracks a wave's loads and stores, so a wave that polls after
 // storing would wait for its store to be acknowledged first.
-template <int T>
-__device__ __forceinline__ void publish_tile(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int x, int j) {
+template <int T, class S>
+__device__ __forceinline__ void publish_tile(const S& sm, const BArgs& a, size_t cross, uint32_t ep, int x, int j) {
   const int lane = tix() & 63;
   if (lane >= 4 * a.B) return;
   const int b = lane >> 2, r0 = 4 * (lane & 3);
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = red_sum<4 * T, 4>(sm, r0 + i, b);
-  st4<true>(a.ws + cross + ((size_t)j * NXCD + x) * BM * OR, b * OR + 16 * T + r0, v, ep);
+  st4<true>(a.ws + cross + ((size_t)j * NXCD + x) * S::BM * OR, b * OR + 16 * T + r0, v, ep);
 }
-__device__ __forceinline__ void publish_rows(const Smem& sm, const BArgs& a, size_t cross, uint32_t ep, int m,
+template <class S>
+__device__ __forceinline__ void publish_rows(const S& sm, const BArgs& a, size_t cross, uint32_t ep, int m,
                                              int x, int j) {
   if (m == 0) publish_tile<0>(sm, a, cross, ep, x, j);
   else if (m == 1) publish_tile<1>(sm, a, cross, ep, x, j);
 }
 // QKV rows (all 8 math waves computed the tile over K): math wave 0, lane (b, 4 rows), scaled by the
 // input norm's scale.
-__device__ __forceinline__ void publish_qkv(const Smem& sm, const BArgs& a, uint32_t ep, int x, int j) {
+template <class S>
+__device__ __forceinline__ void publish_qkv(const S& sm, const BArgs& a, uint32_t ep, int x, int j) {
+  constexpr int BM = S::BM;
   const int lane = tix() & 63;
   if (lane >= 4 * a.B) return;
   const int b = lane >> 2, r0 = 4 * (lane & 3);
@@ -397,11 +413,13 @@ __device__ __forceinline__ void publish_qkv(const Smem& sm, const BArgs& a, uint
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = red_sum<0, NMW>(sm, r0 + i, b) * rs;
-  st4<false>(a.ws + W_QX + (size_t)x * BM * QX + QR * j, b * QX + r0, v, ep);
+  st4<false>(a.ws + WL<BM>::QX_ + (size_t)x * BM * QX + QR * j, b * QX + r0, v, ep);
 }
 // silu(gate) * up of the workgroup's intermediates (gate tile on math waves 0-3, up on 4-7), scaled by
 // the post-attention norm's scale: math wave 0, lane (b, 4 intermediates).
-__device__ __forceinline__ void publish_silu(const Smem& sm, const BArgs& a, uint32_t ep, int x, int j) {
+template <class S>
+__device__ __forceinline__ void publish_silu(const S& sm, const BArgs& a, uint32_t ep, int x, int j) {
+  constexpr int BM = S::BM;
   const int lane = tix() & 63;
   if (lane >= 3 * a.B) return;
   const int b = lane / 3, q = lane % 3;
@@ -413,14 +431,15 @@ __device__ __forceinline__ void publish_silu(const Smem& sm, const BArgs& a, uin
     const float gt = red_sum<0, 4>(sm, ii, b) * rs, up = red_sum<4, 4>(sm, ii, b) * rs;
     v[i] = gt / (1.f + expf(-gt)) * up;
   }
-  st4<false>(a.ws + W_MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
+  st4<false>(a.ws + WL<BM>::MX + (size_t)x * BM * IX + GI * j, b * IX + 4 * q, v, ep);
 }
 
 // q/k RMSNorm + rotate-half RoPE of one head row held by 32 lanes (lane c % 32: dims 4c..4c+3; the RoPE
 // partner of dim d is d +- 64, 16 lanes away), as the single-sequence kernel applies them
 // (/root/reference/megakernel.cu:490-630, 548-555); row 3 (v) is only rounded. Writes q as fp32 into
 // raw[row][] and the new K/V rows as bf16 into kvn. Both waves' lanes take part in the swaps.
-__device__ __forceinline__ void head_norm_rope4(Smem& sm, const float (&v)[4], uint2 wn, int tid) {
+template <class S>
+__device__ __forceinline__ void head_norm_rope4(S& sm, const float (&v)[4], uint2 wn, int tid) {
   const int row = tid >> 5, d0 = 4 * (tid & 31);
   float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
   ss = xsum16(row16_sum(ss));  // the 32 lanes of this row
@@ -508,17 +527,24 @@ __device__ __forceinline__ void load_down(uint4 (&w)[3], const mk_layer_weights&
   for (int s = 0; s < 3; ++s) w[s] = ldnt(rs, off + 64 * s);
 }
 
-// MFMA over NS K steps starting at step ks0 of the LDS operand; result to the wave's reduction tile.
-template <int NS>
-__device__ __forceinline__ void mma_to_red(Smem& sm, const uint4 (&w)[NS], int ks0, const MathLane& ml) {
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+// MFMA over NS K steps starting at step ks0 of the LDS operand, every column block with the same
+// weight fragment; result to the wave's reduction tile.
+template <int NS, class S>
+__device__ __forceinline__ void mma_to_red(S& sm, const uint4 (&w)[NS], int ks0, const MathLane& ml) {
+  f32x4 c[S::CB];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint4 b = *reinterpret_cast<const uint4*>(&sm.act[ml.li][32 * (ks0 + s) + 8 * ml.g]);
-    c = mfma(w[s], b, c);
-  }
+  for (int cb = 0; cb < S::CB; ++cb) c[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) sm.red[ml.m][4 * ml.g + r][ml.li] = c[r];
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int cb = 0; cb < S::CB; ++cb) {
+      const uint4 b = *reinterpret_cast<const uint4*>(&sm.act[16 * cb + ml.li][32 * (ks0 + s) + 8 * ml.g]);
+      c[cb] = mfma(w[s], b, c[cb]);
+    }
+#pragma unroll
+  for (int cb = 0; cb < S::CB; ++cb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.red[ml.m][4 * ml.g + r][16 * cb + ml.li] = c[cb][r];
 }
 
 // ---- attention ------------------------------------------------------------------------------------
@@ -557,8 +583,9 @@ __device__ __forceinline__ void softmax_step(float sc, const float (&v)[8], floa
 
 
 // Merge of every sequence's split partials (polled into LDS) into the o_proj operand: thread (b, head
-// h, 4 dims) for b < B (one pass of B * 64 threads), max-first over the sequence's splits.
-__device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a, int o) {
+// h, 4 dims) for b < B (B * 64 items over the workgroup), max-first over the sequence's splits.
+template <class S>
+__device__ __forceinline__ void merge_splits(S& sm, const BArgs& a, int o) {
   if (o >= a.B * 64) return;
   const int b = o >> 6, h = (o >> 5) & 1, d0 = 4 * (o & 31);
   const float* p = sm.stg + (size_t)sm.f[b] * APW;
@@ -614,14 +641,14 @@ __device__ __forceinline__ void merge_splits(Smem& sm, const BArgs& a, int o) {
 }
 
 // Every split partial of the XCD into LDS (nsplit * 65 chunks of 16 bytes, NK per comm lane).
-template <int NK>
-__device__ __forceinline__ void poll_splits(Smem& sm, Ctl& c, const BArgs& a, int x, uint32_t ep) {
+template <int NK, class S>
+__device__ __forceinline__ void poll_splits(S& sm, Ctl& c, const BArgs& a, int x, uint32_t ep) {
   const int tid = tix(), nch = sm.nsplit * (APW / 4);
   int off[NK];
 #pragma unroll
   for (int k = 0; k < NK; ++k) off[k] = 16 * min(tid + CL * k, nch - 1);
   float v[NK][4];
-  poll<NK>(c, a.ws + W_AX + (size_t)x * WPX * APW, off, ep, v);
+  poll<NK>(c, a.ws + WL<S::BM>::AX + (size_t)x * WPX * APW, off, ep, v);
 #pragma unroll
   for (int k = 0; k < NK; ++k)
     if (tid + CL * k < nch)
@@ -631,9 +658,19 @@ __device__ __forceinline__ void poll_splits(Smem& sm, Ctl& c, const BArgs& a, in
 // The two roles run separate layer loops that meet at the same sequence of LDS barriers:
 // A1 A2 [B1 B2] C1 C2 C3 E1 E2 F1 F2 per layer (B1, B2 on workgroups with an attention split).
 
-// Comm waves (threads 0..255): polls, publishes, norms, reductions of the MFMA tiles.
-__device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, const Split& sp, int x, int j) {
+// Comm waves (threads 0..255): polls, publishes, norms, reductions of the MFMA tiles; waves 0..BM/8-1
+// hold the residual of row block j (thread t: sequence t / 8, rows 4 (t % 8) .. +3).
+template <class S>
+__device__ __forceinline__ void comm_role(S& sm, Ctl& c, const BArgs& a, const Split& sp, int x, int j) {
+  constexpr int BM = S::BM;
+  using W = WL<BM>;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float xr[4];
+  {
+    const int q8 = min((int)threadIdx.x, 8 * a.B - 1);
+    const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)sm.tok[q8 >> 3] * H + OR * j + 4 * (q8 & 7));
+    xr[0] = bf16_lo(e.x); xr[1] = bf16_hi(e.x); xr[2] = bf16_lo(e.y); xr[3] = bf16_hi(e.y);
+  }
   for (int l = 0; l < a.L; ++l) {
     const mk_layer_weights& lw = a.lw[l];
     const uint32_t ep = (uint32_t)l + 1;
@@ -641,7 +678,7 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     // ---- A: residual + input norm (x * w into the operand; the scale goes on the outputs)
     mark(a, x, j, l, 0);
     if (l == 0) residual_norm<true>(sm, c, a, nullptr, 0, (const uint16_t*)lw.norm_weight);
-    else residual_norm<false>(sm, c, a, a.ws + W_DL + (size_t)x * BM * H, ep - 1, (const uint16_t*)lw.norm_weight);
+    else residual_norm<false>(sm, c, a, a.ws + W::DL + (size_t)x * BM * H, ep - 1, (const uint16_t*)lw.norm_weight);
     mark(a, x, j, l, 1);
     uint2 qn = make_uint2(0, 0);  // this layer's q_norm / k_norm weights of lane tid's 4 dims (rows 0-2)
     if (sp.on && tid < 3 * D / 4)
@@ -655,7 +692,7 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
       if (tid < QX / 4) {  // waves 0-1: lane tid holds dims 4 (tid % 32) .. +3 of row tid / 32 (q0, q1, k, v)
         int off[1] = {(int)((((size_t)x * BM + sp.b) * QX + 4 * tid) * 4)};
         float v[1][4];
-        poll<1>(c, a.ws + W_QX, off, ep, v);
+        poll<1>(c, a.ws + W::QX_, off, ep, v);
         head_norm_rope4(sm, v[0], qn, tid);
       }
       lds_barrier();  // B1
@@ -675,22 +712,22 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // C3
     mark(a, x, j, l, 8);
     // ---- D, E: row block j of the o_proj partials summed over the XCDs, residual + post-attention norm
-    if (wave == 0) gather(c, a, W_OX, W_OL, ep, x, j);
+    if (wave < BM / 8) gather<BM>(c, a, W::OX, W::OL, ep, x, j, xr);
     mark(a, x, j, l, 9);
-    residual_norm<false>(sm, c, a, a.ws + W_OL + (size_t)x * BM * H, ep, (const uint16_t*)lw.post_attn_norm_weight);
+    residual_norm<false>(sm, c, a, a.ws + W::OL + (size_t)x * BM * H, ep, (const uint16_t*)lw.post_attn_norm_weight);
     mark(a, x, j, l, 10);
     lds_barrier();  // E1
     lds_barrier();  // E2
     mark(a, x, j, l, 11);
     // ---- F: the XCD's SiLU outputs into the operand
     {
-      constexpr int NK = (BM * IX / 4) / CL;  // 3
+      constexpr int NK = (BM * IX / 4) / CL;  // 3 per 8 sequences
       const int nch = a.B * (IX / 4);
       int off[NK];
 #pragma unroll
       for (int k = 0; k < NK; ++k) off[k] = (int)(((size_t)x * BM * IX + 4 * min(tid + CL * k, nch - 1)) * 4);
       float v[NK][4];
-      poll<NK>(c, a.ws + W_MX, off, ep, v);
+      poll<NK>(c, a.ws + W::MX, off, ep, v);
 #pragma unroll
       for (int k = 0; k < NK; ++k) {
         const int ci = tid + CL * k;
@@ -709,16 +746,18 @@ __device__ __forceinline__ void comm_role(Smem& sm, Ctl& c, const BArgs& a, cons
     lds_barrier();  // F2
     mark(a, x, j, l, 13);
     // ---- G: row block j of the down partials summed over the XCDs
-    if (wave == 0) gather(c, a, W_DX, W_DL, ep, x, j);
+    if (wave < BM / 8) gather<BM>(c, a, W::DX, W::DL, ep, x, j, xr);
     mark(a, x, j, l, 14);
   }
-  // the last layer's sums, final norm
-  residual_norm<false>(sm, c, a, a.ws + W_DL + (size_t)x * BM * H, (uint32_t)a.L, a.final_norm);
+  // the last layer's residual, final norm
+  residual_norm<false>(sm, c, a, a.ws + W::DL + (size_t)x * BM * H, (uint32_t)a.L, a.final_norm);
   lds_barrier();
 }
 
 // Math waves (threads 256..767): weights in registers (issued phases ahead), MFMA tiles, attention.
-__device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split& sp, int x, int j) {
+template <class S>
+__device__ __forceinline__ void math_role(S& sm, const BArgs& a, const Split& sp, int x, int j) {
+  using W = WL<S::BM>;
   const int tid = threadIdx.x, lane = tid & 63;
   const MathLane ml{__builtin_amdgcn_readfirstlane(tid >> 6) - NCW, lane & 15, lane >> 4};
   const int gi = 4 * ml.m + (lane >> 4), t = lane & 15;
@@ -818,7 +857,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
       A += dpp<0xB1>(A);
       Ls += dpp<0xB1>(Ls);
       if (half == 0) {
-        uint32_t* base = a.ws + W_AX + ((size_t)x * WPX + j) * APW;
+        uint32_t* base = a.ws + W::AX + ((size_t)x * WPX + j) * APW;
         st1(base, o, A, ep);
         if (d == 0) {
           st1(base, 2 * D + 2 * h, M, ep);
@@ -837,7 +876,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     issue(5);
     mma_to_red<2>(sm, wo, 2 * (ml.m & 3), ml);
     lds_barrier();  // C3
-    publish_rows(sm, a, W_OX, ep, ml.m, x, j);
+    publish_rows(sm, a, W::OX, ep, ml.m, x, j);
     mark(a, x, j, l, 16, 64 * NCW);
     issue(6);
     lds_barrier();  // E1
@@ -851,7 +890,7 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
     issue(9);
     mma_to_red<3>(sm, wd, 3 * (ml.m & 3), ml);
     lds_barrier();  // F2
-    publish_rows(sm, a, W_DX, ep, ml.m, x, j);
+    publish_rows(sm, a, W::DX, ep, ml.m, x, j);
     issue(10);
   }
   lds_barrier();  // the final norm
@@ -859,17 +898,20 @@ __device__ __forceinline__ void math_role(Smem& sm, const BArgs& a, const Split&
 
 // ------------------------------------------------------------------------------------------------
 
+template <int CB>
 __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
-  __shared__ __attribute__((aligned(16))) Smem sm;
+  constexpr int BM = 8 * CB;
+  using W = WL<BM>;
+  __shared__ __attribute__((aligned(16))) Smem<CB> sm;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const bool comm = wave < NCW;
-  Ctl c{a.ws, a.drain != 0};
+  Ctl c{a.ws + W::ABORT, a.drain != 0};
 
   // ---- identity, inputs, split plan
   if (tid == 0) {
     const int x = (int)(xcc_id() & 7u);
     sm.x = x;
-    sm.j = (int)__hip_atomic_fetch_add(a.ws + W_TICK + 64 * x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.j = (int)__hip_atomic_fetch_add(a.ws + W::TICK + 64 * x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sm.bad = 0;
   }
   if (tid >= 64 && tid < 64 + BM) {
@@ -886,7 +928,7 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     sm.tok[b] = t;
     if (bad && b < a.B) atomicOr(&sm.bad, 1);
   }
-  for (int i = tid; i < 16 * KST / 8; i += NT) reinterpret_cast<uint4*>(&sm.act[0][0])[i] = make_uint4(0, 0, 0, 0);
+  for (int i = tid; i < 16 * CB * KST / 8; i += NT) reinterpret_cast<uint4*>(&sm.act[0][0])[i] = make_uint4(0, 0, 0, 0);
   __syncthreads();
   if (tid == 0) {
     // key-range length: a multiple of 16 keeping the number of ranges below 32
@@ -903,9 +945,9 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     }
     sm.nsplit = f;
     sm.ks = ks;
-    if (sm.bad && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W_BAD, 1u);
-    if (a.drain && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W_ABORT, 1u);
-    if (sm.j >= WPX) st_dev_u32(a.ws + W_ABORT, 1u);  // more than 32 workgroups on one XCD: no role
+    if (sm.bad && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::BAD, 1u);
+    if (a.drain && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::ABORT, 1u);
+    if (sm.j >= WPX) st_dev_u32(a.ws + W::ABORT, 1u);  // more than 32 workgroups on one XCD: no role
   }
   __syncthreads();
   const int x = __builtin_amdgcn_readfirstlane(sm.x), j = __builtin_amdgcn_readfirstlane(sm.j);
@@ -930,13 +972,20 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
   else math_role(sm, a, sp, x, j);
   mark(a, x, j, MAXL, 1);
 
-  // ---- tied LM head on all waves, greedy keys
+  // ---- tied LM head on all waves, greedy keys (lane li of column block cb: sequence 8 cb + li / 2)
   {
-    const int li = lane & 15, g = lane >> 4, b = li >> 1;
-    const bool out = !(li & 1) && b < a.B;
-    const float rs = out ? norm_scale(sm, b) : 0.f;
+    const int li = lane & 15, g = lane >> 4;
+    bool out[CB];
+    float rs[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      out[cb] = !(li & 1) && 8 * cb + (li >> 1) < a.B;
+      rs[cb] = out[cb] ? norm_scale(sm, 8 * cb + (li >> 1)) : 0.f;
+    }
     const int gw = j * NXCD + x, ntiles = a.vocab / 16;
-    u64 best = 0;
+    u64 best[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) best[cb] = 0;
     const __amdgpu_buffer_rsrc_t rlm = make_rsrc(a.lm_head);
     // a tile (16 rows x H) in NC chunks of CH K steps, two chunk buffers in flight
     constexpr int CH = MKB_LM_CH, NC = H / 32 / CH;
@@ -946,12 +995,14 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
 #pragma unroll
       for (int s = 0; s < CH; ++s) w[s] = ldnt(rlm, off + 64 * s);
     };
-    auto mma_chunk = [&](const uint4 (&w)[CH], int ch, f32x4& acc) {
+    auto mma_chunk = [&](const uint4 (&w)[CH], int ch, f32x4 (&acc)[CB]) {
 #pragma unroll
-      for (int s = 0; s < CH; ++s) {
-        const uint4 bo = *reinterpret_cast<const uint4*>(&sm.act[li][32 * CH * ch + 32 * s + 8 * g]);
-        acc = mfma(w[s], bo, acc);
-      }
+      for (int s = 0; s < CH; ++s)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const uint4 bo = *reinterpret_cast<const uint4*>(&sm.act[16 * cb + li][32 * CH * ch + 32 * s + 8 * g]);
+          acc[cb] = mfma(w[s], bo, acc[cb]);
+        }
     };
     int tile = gw + NWG * wave;
     uint4 wa[CH], wb[CH];
@@ -963,7 +1014,9 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
       // the operand is read from LDS per tile (held in registers it would take 128 of them)
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       const int next = tile + NWG * NWAVE;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ch = 0; ch < NC; ch += 2) {
         mma_chunk(wa, ch, acc);
@@ -973,56 +1026,67 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
         if (ch + 3 < NC) load_chunk(wb, tile, ch + 3);
         else if (next < ntiles) load_chunk(wb, next, 1);
       }
-      float lg[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) lg[r] = (acc[r] + dpp<0xB1>(acc[r])) * rs;  // hi + lo columns
-      if (out) {
-        const int v0 = 16 * tile + 4 * g;
-        *reinterpret_cast<float4*>(a.logits + (size_t)b * a.vocab + v0) = make_float4(lg[0], lg[1], lg[2], lg[3]);
+      for (int cb = 0; cb < CB; ++cb) {
+        float lg[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const u64 k = argmax_key(lg[r], v0 + r);
-          best = k > best ? k : best;
+        for (int r = 0; r < 4; ++r) lg[r] = (acc[cb][r] + dpp<0xB1>(acc[cb][r])) * rs[cb];  // hi + lo columns
+        if (out[cb]) {
+          const int v0 = 16 * tile + 4 * g;
+          *reinterpret_cast<float4*>(a.logits + (size_t)(8 * cb + (li >> 1)) * a.vocab + v0) =
+              make_float4(lg[0], lg[1], lg[2], lg[3]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const u64 k = argmax_key(lg[r], v0 + r);
+            best[cb] = k > best[cb] ? k : best[cb];
+          }
         }
       }
       tile = next;
     }
     // reduce over the 4 row groups of the wave, then over the waves
 #pragma unroll
-    for (int sh = 16; sh < 64; sh <<= 1) {
-      const u64 o = ((u64)(uint32_t)__shfl_xor((int)(best >> 32), sh) << 32) | (uint32_t)__shfl_xor((int)best, sh);
-      best = o > best ? o : best;
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+      for (int sh = 16; sh < 64; sh <<= 1) {
+        const u64 o = ((u64)(uint32_t)__shfl_xor((int)(best[cb] >> 32), sh) << 32) |
+                      (uint32_t)__shfl_xor((int)best[cb], sh);
+        best[cb] = o > best[cb] ? o : best[cb];
+      }
+      if (g == 0 && out[cb]) sm.wk[wave][8 * cb + (li >> 1)] = best[cb];
     }
-    if (g == 0 && out) sm.wk[wave][b] = best;
     __syncthreads();
     if (tid < a.B) {
       u64 k = 0;
       for (int w = 0; w < NWAVE; ++w) k = sm.wk[w][tid] > k ? sm.wk[w][tid] : k;
-      reinterpret_cast<u64*>(a.ws + W_KEYS)[gw * BM + tid] = k;
+      reinterpret_cast<u64*>(a.ws + W::KEYS)[gw * BM + tid] = k;
     }
     mark(a, x, j, MAXL, 2);
   }
 }
 
-// Zeroes the exchange words (and the ticket, abort and bad words) before a launch.
-__global__ void __launch_bounds__(256) batch_zero_kernel(uint32_t* ws) {
+// Zeroes the exchange words (and the ticket, abort and bad words) before a launch: `words`, a
+// multiple of 4.
+__global__ void __launch_bounds__(256) batch_zero_kernel(uint32_t* ws, size_t words) {
   uint4* p = reinterpret_cast<uint4*>(ws);
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < W_ZERO / 4; i += (size_t)gridDim.x * blockDim.x)
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words / 4; i += (size_t)gridDim.x * blockDim.x)
     p[i] = make_uint4(0, 0, 0, 0);
 }
 
 // Greedy tokens from the workgroups' keys; NaN logits and token -1 for every sequence if the launch
 // gave up or an input was out of range.
+template <int BM>
 __global__ void __launch_bounds__(256) batch_finish_kernel(const uint32_t* ws, int B, int vocab, float* logits,
                                                            int32_t* out_tokens) {
-  const bool failed = ws[W_ABORT] != 0 || ws[W_BAD] != 0;
+  using W = WL<BM>;
+  const bool failed = ws[W::ABORT] != 0 || ws[W::BAD] != 0;
   if (failed) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)B * vocab; i += (size_t)gridDim.x * blockDim.x)
       logits[i] = __uint_as_float(0x7fc00000u);
   }
   if (blockIdx.x != 0 || !out_tokens) return;
   const int lane = threadIdx.x & 63, b = threadIdx.x >> 6;  // 4 waves, sequences b, b + 4
-  const u64* keys = reinterpret_cast<const u64*>(ws + W_KEYS);
+  const u64* keys = reinterpret_cast<const u64*>(ws + W::KEYS);
   for (int s = b; s < B; s += 4) {
     u64 k = 0;
     for (int w = lane; w < NWG; w += 64) k = keys[w * BM + s] > k ? keys[w * BM + s] : k;
@@ -1040,7 +1104,7 @@ __global__ void __launch_bounds__(256) batch_finish_kernel(const uint32_t* ws, i
 constexpr int MAX_DEVICES = 64;
 struct DevCheck {
   bool done = false;
-  bool ok = false;
+  bool ok[2] = {false, false};  // one and two column blocks
 };
 static DevCheck g_check[MAX_DEVICES];
 static std::mutex g_mu;
@@ -1048,20 +1112,37 @@ static std::atomic<int> g_engine{0};    // 0 automatic, 1 layer-by-layer engine,
 static std::atomic<bool> g_drain{false};
 static std::atomic<uint64_t*> g_trace{nullptr};
 
-// Can the current device run the kernel: 256 CUs and one 768-thread workgroup per CU.
-static bool device_ok() {
+// Can the current device run the kernel with cb column blocks: 256 CUs and one 768-thread workgroup
+// per CU.
+static bool device_ok(int cb) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return false;
   std::lock_guard<std::mutex> lk(g_mu);
   DevCheck& d = g_check[dev];
   if (!d.done) {
-    int cus = 0, blocks = 0;
-    d.ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus == NWG &&
-           hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)batch_kernel, NT, 0) == hipSuccess &&
-           blocks >= 1;
+    int cus = 0;
+    const bool cus_ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus == NWG;
+    const void* fns[2] = {(const void*)batch_kernel<1>, (const void*)batch_kernel<2>};
+    for (int i = 0; i < 2; ++i) {
+      int blocks = 0;
+      d.ok[i] = cus_ok && hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fns[i], NT, 0) == hipSuccess && blocks >= 1;
+    }
     d.done = true;
   }
-  return d.ok;
+  return d.ok[cb - 1];
+}
+
+template <int CB>
+static hipError_t launch(const BArgs& a, int32_t* out_tokens, hipStream_t stream) {
+  using W = WL<8 * CB>;
+  hipLaunchKernelGGL(batch_zero_kernel, dim3(128), dim3(256), 0, stream, a.ws, W::ZERO);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(batch_kernel<CB>, dim3(NWG), dim3(NT), 0, stream, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(batch_finish_kernel<8 * CB>, dim3(64), dim3(256), 0, stream, (const uint32_t*)a.ws, a.B, a.vocab,
+                     a.logits, out_tokens);
+  return hipGetLastError();
 }
 
 }  // namespace mkb
@@ -1071,7 +1152,7 @@ bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len) {
   const int e = g_engine.load();
   if (e == 1) return false;
   return dims->hidden == H && dims->intermediate == I && dims->num_layers >= 1 && dims->num_layers <= MAXL &&
-         dims->num_layers < 255 && batch >= 1 && batch <= BM && max_seq_len >= 1 && device_ok();
+         dims->num_layers < 255 && batch >= 1 && batch <= BMAX && max_seq_len >= 1 && device_ok(batch <= 8 ? 1 : 2);
 }
 size_t mkb_workspace_bytes() { return mkb::WS_BYTES; }
 void mkb_set_drain(bool on) { mkb::g_drain.store(on); }
@@ -1101,14 +1182,7 @@ hipError_t mkb_decode_batch(const mk_model_dims* dims, int batch, const int32_t*
   a.drain = g_drain.load() ? 1 : 0;
   a.trace = g_trace.load();
   for (int l = 0; l < a.L; ++l) a.lw[l] = layers[l];
-  hipLaunchKernelGGL(batch_zero_kernel, dim3(128), dim3(256), 0, stream, a.ws);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(batch_kernel, dim3(NWG), dim3(NT), 0, stream, a);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(batch_finish_kernel, dim3(64), dim3(256), 0, stream, (const uint32_t*)a.ws, batch, dims->vocab,
-                     logits, out_tokens);
-  return hipGetLastError();
+  return batch <= 8 ? launch<1>(a, out_tokens, stream) : launch<2>(a, out_tokens, stream);
 }
 
 extern "C" hipError_t mk_set_batch_engine(int engine) {

@@ -1471,7 +1471,7 @@ extern "C" size_t mk_decode_batch_workspace_bytes(const mk_model_dims* dims, int
   if (!dims || batch < 1 || batch > BMAX || max_seq_len < 1) return 0;
   const size_t n = blayout(dims->hidden, dims->intermediate, batch, max_seq_len).bytes;
   const size_t p = mkb_workspace_bytes();
-  return batch <= 8 && p > n ? p : n;
+  return batch <= 16 && p > n ? p : n;
 }
 
 extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens,

@@ -8,7 +8,7 @@
 
 #include "../../include/megakernel_amd.h"
 
-// Whether mk_decode_batch runs this batch on the persistent kernel: the Qwen3-0.6B shape, at most 8
+// Whether mk_decode_batch runs this batch on the persistent kernel: the Qwen3-0.6B shape, at most 16
 // sequences, at most 32 layers, a device with 256 CUs, and the engine not forced to the
 // layer-by-layer one (mk_set_batch_engine).
 bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len);

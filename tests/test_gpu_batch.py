@@ -1,5 +1,5 @@
 """GPU parity tests of the batched decode (``decode_batch``, C ABI ``mk_decode_batch``): B sequences of
-different lengths advance one token each per call, each against its own cache. Batches of up to 8
+different lengths advance one token each per call, each against its own cache. Batches of up to 16
 sequences of the 0.6B shape run on either engine (``set_batch_engine``: 1 layer by layer, 2 the
 persistent kernel); both are checked.
 
@@ -69,6 +69,9 @@ def engine(request):
     ("mini", (509, 3, 260, 1, 400, 90, 128), 2, 2),      # 27 key ranges of 64 over 7 sequences
     ("mini2k", (1900, 1300, 2000, 700), 2, 2),             # ranges of 224 keys: 2 rounds of K/V loads, 9 ranges
     ("mini2k", (2000,), 2, 2),                             # one sequence in 26 ranges of 80 keys
+    ("mini", (7, 300, 45, 128, 256, 99, 1, 410, 64), 3, 2),  # 9 sequences: a second column block of one
+    ("mini", tuple(2 + 31 * i for i in range(16)), 3, 2),  # 16 sequences: two full column blocks
+    ("mini2k", (1900, 50, 1000, 1500, 300, 2000, 17, 800, 1200, 640, 1, 1750), 2, 2),  # 12 long: 28 ranges of 560
     ("mini17", (33, 200, 90), 4, 1),
     ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
     ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
@@ -78,8 +81,8 @@ def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, engine
     64, and sequences end a split exactly at 64 and 256): every step, each sequence's logits and
     greedy token against the restatement on the kernel's cache for that sequence, and its new K/V
     rows. Layer by layer, up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3
-    and 8. The persistent kernel (engine 2) cuts the batch's keys into at most 31 ranges, one per
-    workgroup of an XCD."""
+    and 8. The persistent kernel (engine 2) runs up to 8 sequences in one column block and up to 16
+    in two, and cuts the batch's keys into at most 31 ranges, one per workgroup of an XCD."""
     sess = request.getfixturevalue(shape_fixture)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
@@ -115,21 +118,24 @@ def q06():
     return Session("qwen3-0.6b", 512)
 
 
-@pytest.mark.parametrize("engine", [1, 2], indirect=True)
-def test_batch_agrees_with_single_sequence_decode_at_0_6b(q06, engine):
-    """The full Qwen3-0.6B shape, 8 sequences of lengths 32..480: each sequence's batched logits and
-    token against the single-sequence decode kernel on an identical cache, for 6 steps (both are
-    fp32-accurate, so they agree to the restatement tolerance), and against the restatement on the
-    first step. Prints the batched step time."""
+@pytest.mark.parametrize("engine, lengths, steps", [
+    (1, (32, 64, 100, 150, 200, 256, 300, 480), 6),
+    (2, (32, 64, 100, 150, 200, 256, 300, 480), 6),
+    (2, tuple(16 + 16 * i for i in range(16)), 4),   # two column blocks of the persistent kernel
+], indirect=["engine"])
+def test_batch_agrees_with_single_sequence_decode_at_0_6b(q06, engine, lengths, steps):
+    """The full Qwen3-0.6B shape, 8 sequences of lengths 32..480 (and 16 of 16..256): each sequence's
+    batched logits and token against the single-sequence decode kernel on an identical cache, for
+    several steps (both are fp32-accurate, so they agree to the restatement tolerance), and against
+    the restatement on the first step. Prints the batched step time."""
     sess = q06
-    lengths = (32, 64, 100, 150, 200, 256, 300, 480)
     B = len(lengths)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=20 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
     kd, vd = kc.to(DEV), vc.to(DEV)
     singles = [(kc[b].to(DEV), vc[b].to(DEV)) for b in range(B)]
     pos = list(lengths)
-    for t in range(6):
+    for t in range(steps):
         if t == 0:
             want0 = [sess.oracle_step(kc[b].clone(), vc[b].clone(), toks[b], pos[b]) for b in range(B)]
         logits, dev_toks = _decode_batch(sess, toks, pos, kd, vd)
