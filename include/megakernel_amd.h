@@ -167,7 +167,7 @@ hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, in
 
 /*
  * Batched decode: `batch` (1..64) independent sequences advance by one token each in one call.
- * Two engines: up to 8 sequences of the Qwen3-0.6B shape run as one persistent kernel (256
+ * Two engines: up to 16 sequences of the Qwen3-0.6B shape run as one persistent kernel (256
  * workgroups exchanging data through epoch-tagged words, the batch as the columns of the matrix-core
  * tiles); other batches run layer by layer (a few kernels per layer). mk_set_batch_engine chooses.
  * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a

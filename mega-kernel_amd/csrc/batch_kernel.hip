@@ -77,8 +77,10 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 // in the layer that uses them (at most 6 and 8), QKV, o_proj and the first K/V round for the next
 // layer (at least 1, 6 and 3). A burst of loads delays any poll of the same CU issued after it, so
 // each goes where the comm waves' next poll is furthest away. Measured at 8 sequences of 257 keys
-// (0.6B): gate/up+down after the attention publish 797 us per step, gate/up after C1 729, and the
-// defaults below 708.
+// (0.6B): gate/up+down after the attention publish 797 us per step, gate/up after C1 729, and
+// gate/up after C1 and C3 with down after E2 708. Later, at 8 and 16 sequences: down after E1 613
+// and 840 us, after E2 618 and 856; the next layer's first K/V round after F1 641 and 875, after F2
+// 627 and 857.
 // The split merge on all waves (1) or on the comm waves only (0), the math waves issuing loads meanwhile.
 #ifndef MKB_MERGE_ALL
 #define MKB_MERGE_ALL 1
@@ -98,7 +100,7 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 #define MKB_GU2_AT 6  // >= 0: the second half of the gate/up rows at this point (-1: all at GU_AT)
 #endif
 #ifndef MKB_DN_AT
-#define MKB_DN_AT 8
+#define MKB_DN_AT 7
 #endif
 #ifndef MKB_QKV_AT
 #define MKB_QKV_AT 6
@@ -281,7 +283,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 // x * w (w the RMSNorm weight) of every sequence's residual, polled from `src` (or, at layer 0, the
 // embedding rows), into the MFMA operand as bf16 hi/lo, and each comm wave's sums of squares per
-// sequence. Comm lane c holds elements 4c..4c+3 of every sequence; 8 sequences per poll.
+// sequence. Comm lane c holds elements 4c..4c+3 of every sequence.
 template <bool EMBED, class S>
 __device__ __forceinline__ void residual_norm(S& sm, Ctl& c, const BArgs& a, const uint32_t* src, uint32_t ep,
                                               const uint16_t* w) {
@@ -290,35 +292,31 @@ __device__ __forceinline__ void residual_norm(S& sm, Ctl& c, const BArgs& a, con
   const uint2 wr = *reinterpret_cast<const uint2*>(w + e0);
   const float wv[4] = {bf16_lo(wr.x), bf16_hi(wr.x), bf16_lo(wr.y), bf16_hi(wr.y)};
   const int wave = cl >> 6, lane = cl & 63;
+  float v[BM][4];
+  if constexpr (EMBED) {
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      const int tok = sm.tok[b < a.B ? b : 0];
+      const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)tok * H + e0);
+      v[b][0] = bf16_lo(e.x); v[b][1] = bf16_hi(e.x); v[b][2] = bf16_lo(e.y); v[b][3] = bf16_hi(e.y);
+    }
+  } else {
+    int off[BM];
+#pragma unroll
+    for (int b = 0; b < BM; ++b) off[b] = (min(b, a.B - 1) * H + e0) * 4;
+    poll<BM>(c, src, off, ep, v);
+  }
   float ss[BM];
 #pragma unroll
-  for (int h = 0; h < S::CB; ++h) {
-    float v[8][4];
-    if constexpr (EMBED) {
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const int tok = sm.tok[8 * h + b < a.B ? 8 * h + b : 0];
-        const uint2 e = *reinterpret_cast<const uint2*>(a.embed + (size_t)tok * H + e0);
-        v[b][0] = bf16_lo(e.x); v[b][1] = bf16_hi(e.x); v[b][2] = bf16_lo(e.y); v[b][3] = bf16_hi(e.y);
-      }
-    } else {
-      int off[8];
-#pragma unroll
-      for (int b = 0; b < 8; ++b) off[b] = (min(8 * h + b, a.B - 1) * H + e0) * 4;
-      poll<8>(c, src, off, ep, v);
-    }
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const int s = 8 * h + b;
-      ss[s] = 0.f;
-      if (s < a.B) {
-        const float y[4] = {v[b][0] * wv[0], v[b][1] * wv[1], v[b][2] * wv[2], v[b][3] * wv[3]};
-        uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
-        uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
-        *reinterpret_cast<uint2*>(&sm.act[2 * s][e0]) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2*>(&sm.act[2 * s + 1][e0]) = make_uint2(l0, l1);
-        ss[s] = v[b][0] * v[b][0] + v[b][1] * v[b][1] + v[b][2] * v[b][2] + v[b][3] * v[b][3];
-      }
+  for (int b = 0; b < BM; ++b) {
+    ss[b] = 0.f;
+    if (b < a.B) {
+      const float y[4] = {v[b][0] * wv[0], v[b][1] * wv[1], v[b][2] * wv[2], v[b][3] * wv[3]};
+      uint32_t h0 = pack_bf16x2(y[0], y[1]), h1 = pack_bf16x2(y[2], y[3]);
+      uint32_t l0 = pack_bf16x2(y[0] - bf16_lo(h0), y[1] - bf16_hi(h0)), l1 = pack_bf16x2(y[2] - bf16_lo(h1), y[3] - bf16_hi(h1));
+      *reinterpret_cast<uint2*>(&sm.act[2 * b][e0]) = make_uint2(h0, h1);
+      *reinterpret_cast<uint2*>(&sm.act[2 * b + 1][e0]) = make_uint2(l0, l1);
+      ss[b] = v[b][0] * v[b][0] + v[b][1] * v[b][1] + v[b][2] * v[b][2] + v[b][3] * v[b][3];
     }
   }
   // the BM wave reductions side by side
@@ -930,24 +928,38 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
   }
   for (int i = tid; i < 16 * CB * KST / 8; i += NT) reinterpret_cast<uint4*>(&sm.act[0][0])[i] = make_uint4(0, 0, 0, 0);
   __syncthreads();
-  if (tid == 0) {
-    // key-range length: a multiple of 16 keeping the number of ranges below 32
+  if (tid < 64) {
+    // Key-range length ks: one range per workgroup of an XCD at most (32), and each range's keys
+    // spread over the NG groups as evenly as the batch allows. Lane i tries ks0 + step i (ks0 =
+    // 16 ceil(T / 512) for T keys; the last candidate is at least 16 ceil(T / (16 (32 - B))), which
+    // always fits); the smallest that fits is rounded up to a multiple of NG (same keys per group,
+    // fewer ranges to merge).
     int T = 0;
     for (int b = 0; b < a.B; ++b) T += sm.pos[b] + 1;
-    const int ks = 16 * ((T + 16 * (WPX - a.B) - 1) / (16 * (WPX - a.B)));
-    int f = 0;
-    for (int b = 0; b < a.B; ++b) {
-      const int n = (sm.pos[b] + ks) / ks;  // ceil((pos + 1) / ks)
-      sm.f[b] = f;
-      sm.ns[b] = n;
-      for (int s = 0; s < n; ++s) sm.sb[f + s] = b;
-      f += n;
+    const int ks0 = 16 * ((T + 16 * WPX - 1) / (16 * WPX));
+    const int kfit = 16 * ((T + 16 * (WPX - a.B) - 1) / (16 * (WPX - a.B)));
+    const int step = 16 * max(1, (kfit - ks0 + 16 * 63 - 1) / (16 * 63));
+    const int cand = lane == 63 ? max(kfit, ks0 + step * 63) : ks0 + step * lane;
+    int n = 0;
+    for (int b = 0; b < a.B; ++b) n += (sm.pos[b] + cand) / cand;
+    const int first = __builtin_ctzll(__ballot(n <= WPX));  // lane 63 always fits
+    const int kmin = __shfl(cand, first);
+    const int ks = NG * ((kmin + NG - 1) / NG);
+    if (tid == 0) {
+      int f = 0;
+      for (int b = 0; b < a.B; ++b) {
+        const int nb = (sm.pos[b] + ks) / ks;  // ceil((pos + 1) / ks)
+        sm.f[b] = f;
+        sm.ns[b] = nb;
+        for (int s = 0; s < nb; ++s) sm.sb[f + s] = b;
+        f += nb;
+      }
+      sm.nsplit = f;
+      sm.ks = ks;
+      if (sm.bad && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::BAD, 1u);
+      if (a.drain && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::ABORT, 1u);
+      if (sm.j >= WPX) st_dev_u32(a.ws + W::ABORT, 1u);  // more than 32 workgroups on one XCD: no role
     }
-    sm.nsplit = f;
-    sm.ks = ks;
-    if (sm.bad && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::BAD, 1u);
-    if (a.drain && sm.j == 0 && sm.x == 0) st_dev_u32(a.ws + W::ABORT, 1u);
-    if (sm.j >= WPX) st_dev_u32(a.ws + W::ABORT, 1u);  // more than 32 workgroups on one XCD: no role
   }
   __syncthreads();
   const int x = __builtin_amdgcn_readfirstlane(sm.x), j = __builtin_amdgcn_readfirstlane(sm.j);

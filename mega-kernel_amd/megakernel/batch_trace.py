@@ -34,6 +34,22 @@ ORDER = (0, 1, 2, 4, 18, 19, 5, 15, 6, 20, 22, 23, 7, 8, 16, 17, 9, 10, 11, 12, 
 ATT_SLOTS = (4, 5, 15, 18, 19)
 
 
+def split_plan(positions):
+    """The kernel's key-range length and number of ranges for sequences at these positions: the
+    smallest candidate length (16 ceil(T / 512) + a multiple of a step) that gives at most 32 ranges,
+    rounded up to a multiple of 32 keys."""
+    B, T = len(positions), sum(p + 1 for p in positions)
+    ks0 = 16 * -(-T // 512)
+    kfit = 16 * -(-T // (16 * (32 - B)))
+    step = 16 * max(1, -(-(kfit - ks0) // (16 * 63)))
+    for i in range(64):
+        cand = max(kfit, ks0 + step * 63) if i == 63 else ks0 + step * i
+        if sum((p + cand) // cand for p in positions) <= 32:
+            break
+    ks = 32 * -(-cand // 32)
+    return ks, sum((p + ks) // ks for p in positions)
+
+
 def report(t, layers, att_mask):
     """t: int64 [GRID][MAXL + 1][SLOTS] stamps."""
     t = t - t[:, MAXL, 0].min()
@@ -98,10 +114,8 @@ def main(argv=None):
     torch.cuda.synchronize()
     lib.mk_set_batch_trace(None, 0)
     t = buf.cpu().numpy().reshape(GRID, MAXL + 1, SLOTS)
-    # workgroups with an attention split: the split plan of the kernel (key ranges of a multiple of 16)
-    T = B * (a.context + 1)
-    ks = 16 * ((T + 16 * (32 - B) - 1) // (16 * (32 - B)))
-    nsplit = B * ((a.context + ks) // ks)
+    # workgroups with an attention split: the split plan of the kernel
+    ks, nsplit = split_plan([a.context] * B)
     att = np.array([(w // 8) < nsplit for w in range(GRID)])
     print(f"[batch trace {a.shape} B={B} context={a.context}] {nsplit} key ranges of {ks}")
     print(report(t, L, att))

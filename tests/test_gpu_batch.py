@@ -65,13 +65,13 @@ def engine(request):
     ("mini", (5, 40, 100, 300), 6, 2),
     ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4, 1),
     ("mini", (1, 17, 64, 130, 255, 256, 257, 480), 4, 2),
-    ("mini", (495,), 3, 2),                              # one sequence: 31 key ranges of 16, then 16 of 32
+    ("mini", (495,), 3, 2),                              # one sequence: 16 key ranges of 32
     ("mini", (509, 3, 260, 1, 400, 90, 128), 2, 2),      # 27 key ranges of 64 over 7 sequences
-    ("mini2k", (1900, 1300, 2000, 700), 2, 2),             # ranges of 224 keys: 2 rounds of K/V loads, 9 ranges
-    ("mini2k", (2000,), 2, 2),                             # one sequence in 26 ranges of 80 keys
+    ("mini2k", (1900, 1300, 2000, 700), 2, 2),             # 32 ranges of 192 keys: 2 rounds of K/V loads
+    ("mini2k", (2000,), 2, 2),                             # one sequence in 32 ranges of 64 keys
     ("mini", (7, 300, 45, 128, 256, 99, 1, 410, 64), 3, 2),  # 9 sequences: a second column block of one
     ("mini", tuple(2 + 31 * i for i in range(16)), 3, 2),  # 16 sequences: two full column blocks
-    ("mini2k", (1900, 50, 1000, 1500, 300, 2000, 17, 800, 1200, 640, 1, 1750), 2, 2),  # 12 long: 28 ranges of 560
+    ("mini2k", (1900, 50, 1000, 1500, 300, 2000, 17, 800, 1200, 640, 1, 1750), 2, 2),  # 12 long: 32 ranges of 448
     ("mini17", (33, 200, 90), 4, 1),
     ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
     ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
@@ -82,7 +82,7 @@ def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, engine
     greedy token against the restatement on the kernel's cache for that sequence, and its new K/V
     rows. Layer by layer, up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3
     and 8. The persistent kernel (engine 2) runs up to 8 sequences in one column block and up to 16
-    in two, and cuts the batch's keys into at most 31 ranges, one per workgroup of an XCD."""
+    in two, and cuts the batch's keys into at most 32 ranges, one per workgroup of an XCD."""
     sess = request.getfixturevalue(shape_fixture)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
