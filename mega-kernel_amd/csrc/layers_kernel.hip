@@ -369,7 +369,7 @@ struct AttnSmem {
 __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) AttnSmem sm;
   __shared__ int32_t pages[ATT_MAX_PAGES];  // a paged cache's table entries (-1: out of range)
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int kvh = blockIdx.y, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
   const int nqb = (a.M + QB - 1) / QB;
@@ -416,30 +416,30 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrun = -INFINITY, lrun = 0.f;  // running max and sum of query qrow (replicated on its 4 lanes)
 
-    uint4 pk[2], pv[2];  // the next block's K chunks and V rows, in flight during the current block
-    auto load_block = [&](int kb) {
-      const int kp0 = kb * KB;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int c = tid + 512 * r, kp = kp0 + (c >> 4);
-        pk[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.k_cache + key_row(kp) + 8 * (c & 15))
-                           : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int kp = kp0 + 2 * vp + r;
-        pv[r] = kp <= last ? *reinterpret_cast<const uint4*>(a.v_cache + key_row(kp) + 8 * vc)
-                           : make_uint4(0, 0, 0, 0);
-      }
+    // K chunks and V rows of a block, loaded into registers ahead of use. Keys past `last` load key
+    // `last` again (finite data; the causal mask gives them probability 0): every lane issues the
+    // same loads, so the compiler's count of loads in flight stays exact and each wait below covers
+    // only the block it stores.
+    struct Blk {
+      uint4 k0, k1, v0, v1;
     };
-    auto store_block = [&](int buf) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int c = tid + 512 * r;
-        *reinterpret_cast<uint4*>(&sm.kv.ks[buf][c >> 4][8 * (c & 15)]) = pk[r];
-      }
-      const uint32_t x0[4] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w};
-      const uint32_t x1[4] = {pv[1].x, pv[1].y, pv[1].z, pv[1].w};
+    auto ld = [&](const uint16_t* base, int kp, int e) __attribute__((always_inline)) {
+      return ld_global16(reinterpret_cast<const uint4*>(base + key_row(kp) + e));  // a value, not a copy
+    };
+    auto load_block = [&](Blk& b, int kb) __attribute__((always_inline)) {
+      const int kp0 = kb * KB;
+      b.k0 = ld(a.k_cache, min(kp0 + (tid >> 4), last), 8 * (tid & 15));
+      b.k1 = ld(a.k_cache, min(kp0 + 32 + (tid >> 4), last), 8 * (tid & 15));
+      b.v0 = ld(a.v_cache, min(kp0 + 2 * vp, last), 8 * vc);
+      b.v1 = ld(a.v_cache, min(kp0 + 2 * vp + 1, last), 8 * vc);
+    };
+    auto store_block = [&](const Blk& b, int buf) __attribute__((always_inline)) {
+      uint32_t* k0 = reinterpret_cast<uint32_t*>(&sm.kv.ks[buf][tid >> 4][8 * (tid & 15)]);
+      uint32_t* k1 = reinterpret_cast<uint32_t*>(&sm.kv.ks[buf][32 + (tid >> 4)][8 * (tid & 15)]);
+      *reinterpret_cast<uint4*>(k0) = make_uint4(b.k0.x, b.k0.y, b.k0.z, b.k0.w);
+      *reinterpret_cast<uint4*>(k1) = make_uint4(b.k1.x, b.k1.y, b.k1.z, b.k1.w);
+      const uint32_t x0[4] = {b.v0.x, b.v0.y, b.v0.z, b.v0.w};
+      const uint32_t x1[4] = {b.v1.x, b.v1.y, b.v1.z, b.v1.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         uint32_t* lo = reinterpret_cast<uint32_t*>(&sm.kv.vt[buf][8 * vc + 2 * q][2 * vp]);
@@ -448,94 +448,105 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
         *hi = (x0[q] >> 16) | (x1[q] & 0xFFFF0000u);
       }
     };
-
-    if (pass == 1) __syncthreads();  // the first pass's output staging (which aliases the tiles) is read
-    load_block(0);
-    store_block(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int kp0 = kb * KB, buf = kb & 1;
-      if (kb + 1 < nkb) load_block(kb + 1);
-      if (kp0 <= wlast) {  // a block entirely after this wave's queries adds nothing
-        // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
-        f32x4 st[4];
+    // one block of 64 keys from LDS buffer `buf` into the running softmax and output rows
+    auto consume = [&](int kb, int buf) __attribute__((always_inline)) {
+      const int kp0 = kb * KB;
+      if (kp0 > wlast) return;  // a block entirely after this wave's queries adds nothing
+      // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
+      f32x4 st[4];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      for (int mb = 0; mb < 4; ++mb) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const uint4 fk = *reinterpret_cast<const uint4*>(&sm.kv.ks[buf][16 * mb + li][32 * s + 8 * lg]);
-            c = mfma(fk, fq[0][s], c);
-            c = mfma(fk, fq[1][s], c);
-          }
-          st[mb] = c;
+        for (int s = 0; s < 4; ++s) {
+          const uint4 fk = *reinterpret_cast<const uint4*>(&sm.kv.ks[buf][16 * mb + li][32 * s + 8 * lg]);
+          c = mfma(fk, fq[0][s], c);
+          c = mfma(fk, fq[1][s], c);
         }
-        // causal mask (only on blocks that reach past the wave's first query) and scale; block
-        // maximum of this lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip)
-        float bmax = -INFINITY;
-        if (kp0 + KB - 1 <= a.position + q0 + wq) {
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              st[mb][j] *= ATT_SCALE;
-              bmax = fmaxf(bmax, st[mb][j]);
-            }
-        } else {
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int kp = kp0 + 16 * mb + 4 * lg + j;
-              const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
-              st[mb][j] = sv;
-              bmax = fmaxf(bmax, sv);
-            }
-        }
-        bmax = xmax32(xmax16(bmax));
-        const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
-        const float alpha = __expf(mrun - mnew);
-        float psum = 0.f;
+        st[mb] = c;
+      }
+      // causal mask (only on blocks that reach past the wave's first query) and scale; block
+      // maximum of this lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip)
+      float bmax = -INFINITY;
+      if (kp0 + KB - 1 <= a.position + q0 + wq) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float p = __expf(st[mb][j] - mnew);
-            st[mb][j] = p;
-            psum += p;
+            st[mb][j] *= ATT_SCALE;
+            bmax = fmaxf(bmax, st[mb][j]);
           }
-        psum = xsum32(xsum16(psum));
-        lrun = lrun * alpha + psum;
-        mrun = mnew;
-        // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits
-        // in lane 4g + j (and its copies)
-        float ar[4];
+      } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
-        // O += P . V over two 32-key steps
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          float pw[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) { pw[j] = st[2 * t][j]; pw[4 + j] = st[2 * t + 1][j]; }
-          uint4 ph, pl;
-          split8(pw, ph, pl);
-#pragma unroll
-          for (int nb = 0; nb < 8; ++nb) {
-            const uint16_t* vr = &sm.kv.vt[buf][16 * nb + li][32 * t + 4 * lg];
-            const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
-            const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
-            const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
-            acc[nb] = mfma(ph, fv, acc[nb]);
-            acc[nb] = mfma(pl, fv, acc[nb]);
+          for (int j = 0; j < 4; ++j) {
+            const int kp = kp0 + 16 * mb + 4 * lg + j;
+            const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
+            st[mb][j] = sv;
+            bmax = fmaxf(bmax, sv);
           }
+      }
+      bmax = xmax32(xmax16(bmax));
+      const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
+      const float alpha = __expf(mrun - mnew);
+      float psum = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = __expf(st[mb][j] - mnew);
+          st[mb][j] = p;
+          psum += p;
+        }
+      psum = xsum32(xsum16(psum));
+      lrun = lrun * alpha + psum;
+      mrun = mnew;
+      // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits
+      // in lane 4g + j (and its copies)
+      float ar[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
+      // O += P . V over two 32-key steps
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float pw[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { pw[j] = st[2 * t][j]; pw[4 + j] = st[2 * t + 1][j]; }
+        uint4 ph, pl;
+        split8(pw, ph, pl);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const uint16_t* vr = &sm.kv.vt[buf][16 * nb + li][32 * t + 4 * lg];
+          const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
+          const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
+          const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+          acc[nb] = mfma(ph, fv, acc[nb]);
+          acc[nb] = mfma(pl, fv, acc[nb]);
         }
       }
-      if (kb + 1 < nkb) store_block(buf ^ 1);
+    };
+
+    if (pass == 1) __syncthreads();  // the first pass's output staging (which aliases the tiles) is read
+    // Earlier stores (the first pass's output rows, a paged table's error flag) complete first: with
+    // loads alone in flight the compiler's waits below cover single loads (a store in flight with them
+    // makes every wait a full one, loads and stores completing out of order relative to each other).
+    wait_vmem();
+    Blk A;
+    load_block(A, 0);
+    store_block(A, 0);
+    __syncthreads();
+    // the next block in flight while the current one is consumed (a second block in flight, or no
+    // streaming at all, times the same: the loop is bound by its MFMA, VALU and LDS work)
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int buf = kb & 1;
+      if (kb + 1 < nkb) load_block(A, kb + 1);
+      consume(kb, buf);
+      if (kb + 1 < nkb) store_block(A, buf ^ 1);
       __syncthreads();  // block kb consumed by every wave; block kb + 1 staged
     }
     // normalise by each row's sum (query 4g + j's, from lane 4g + j), stage this wave's 16 rows as

@@ -195,3 +195,37 @@ def test_persistent_batch_drains_on_request(mini, engine):
         mini.kernel.reset()
     logits, toks = _decode_batch(mini, [3, 4, 5], [10, 20, 30], kd, vd)
     assert torch.isfinite(logits).all() and min(toks.tolist()) >= 0
+
+
+@pytest.mark.parametrize("engine", [2], indirect=True)
+def test_persistent_engine_is_the_one_that_runs(mini, engine):
+    """Engine 2 falls back to the layer-by-layer engine where the persistent kernel does not apply, so
+    the other engine-2 cases would pass on the wrong engine if the device check failed. With its phase
+    trace on, the persistent kernel stamps every workgroup's kernel start, LM-head start and end (a
+    100 MHz counter, in order); the layer-by-layer engine writes nothing there. Checked at 8
+    sequences (one MFMA column block) and 16 (two), and not at 17 (layer by layer)."""
+    import ctypes
+
+    from megakernel import build as mkbuild
+    lib = ctypes.CDLL(mkbuild.LIB)
+    lib.mk_batch_trace_bytes.restype = ctypes.c_size_t
+    lib.mk_set_batch_trace.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    nbytes = lib.mk_batch_trace_bytes()
+    maxl, slots, grid = 32, 24, 256
+    for B, persistent in ((8, True), (16, True), (17, False)):
+        kd = torch.zeros(B, mini.shape.layers, 8, mini.max_seq, 128, dtype=torch.bfloat16, device=DEV)
+        vd = torch.zeros_like(kd)
+        buf = torch.zeros(nbytes // 8, dtype=torch.int64, device=DEV)
+        assert lib.mk_set_batch_trace(ctypes.c_void_p(buf.data_ptr()), nbytes) == 0
+        try:
+            logits, toks = _decode_batch(mini, [3 + b for b in range(B)], [10 + 7 * b for b in range(B)], kd, vd)
+            torch.cuda.synchronize()
+        finally:
+            lib.mk_set_batch_trace(None, 0)
+        assert torch.isfinite(logits).all() and min(toks.tolist()) >= 0
+        t = buf.cpu().view(grid, maxl + 1, slots)[:, maxl, :3]
+        if persistent:
+            assert (t > 0).all() and (t[:, 1] >= t[:, 0]).all() and (t[:, 2] >= t[:, 1]).all(), B
+        else:
+            assert (buf == 0).all(), B
+    assert mini.kernel.status() == 0
