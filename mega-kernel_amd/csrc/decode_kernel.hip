@@ -793,8 +793,11 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
     if (p < st.p1) attend(p == st.position ? knew : kK[r], p == st.position ? vnew : kV[r], r == 0);
   }
   // positions beyond the register-held ones (long contexts) stream here, KV_BATCH keys of the group
-  // per round trip (positions past the split re-read its first row and are skipped)
-  constexpr int KV_BATCH = 4;
+  // per round trip (positions past the split re-read its first row and are skipped). At the 1024
+  // width six rows fit the register budget and cover the ~5.5 streamed keys per group of a 16-split
+  // context near 4K in one round trip (MI355X, prompt 3584: 527 -> 515 us per token); at 2048 the
+  // wider batch costs 8 us per token at prompt 512. NKV == 1 never streams (split_plan).
+  constexpr int KV_BATCH = (H <= 1024 && NKV == 2) ? 6 : 4;
   for (int p = st.p0 + g + MG * NKV; p < st.p1; p += KV_BATCH * MG) {
     uint4 kw[KV_BATCH], vw[KV_BATCH];
 #pragma unroll
