@@ -574,11 +574,16 @@ struct Geo {
   static constexpr int HPW = H / WPX;     // o_proj / down_proj rows per workgroup
   static constexpr bool SMALL = H <= 1024;
   // phase tiles: A = QKV rows, C = o_proj partial, D = gate/up rows, E = down_proj partial; the
-  // last argument caps the steps held in registers ahead (the larger shape streams the rest)
-  typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 1> TA;
-  typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 1> TC;
+  // last argument caps the steps held in registers ahead (the rest stream inside the phase). The
+  // 1024 width holds every phase. At 2048 the register budget (168 VGPRs, 3 waves on one SIMD)
+  // holds QKV and o_proj whole (2 steps each) and 2 of the 4 down steps, whose rows take 32 lanes so
+  // that the down phase's activation slice needs 3 chunks per lane instead of 6; gate/up (8 steps,
+  // 50 MB chip-wide) streams at bandwidth. Measured on MI355X at config 5: one step each, 843 us
+  // per token; o_proj whole, 814; plus QKV whole and the 32-lane down rows, 805.
+  typedef Tile<QKV_WG, H, 64, SMALL ? 8 : 2> TA;
+  typedef Tile<HPW, 2 * D, 16, SMALL ? 8 : 2> TC;
   typedef Tile<2 * DPW, H, 64, SMALL ? 8 : 1> TD;
-  typedef Tile<HPW, IX, 16, SMALL ? 8 : 1> TE;
+  typedef Tile<HPW, IX, SMALL ? 16 : 32, SMALL ? 8 : 2> TE;
   static constexpr int XN = (H > IX ? H : IX);
   static constexpr int UMAX = 2 * DPW > HPW ? 2 * DPW : HPW;
   static constexpr int NSLOT = 2 * H + 2 * D;   // bf16 norm weights per layer: input, post-attention, q, k
