@@ -474,10 +474,13 @@ __device__ __forceinline__ void tile_dot_step(const uint4 (&w)[T::CPL], const ui
   if (lane % T::SPAN == 0 && r < T::ROWS) s_up[r] = v;
 }
 // One phase: row sums of the tile into s_up[row]. pf holds the first PS steps; `after` runs once
-// they are consumed (before any streamed step).
-template <class T, typename RowPtr, typename After>
+// they are consumed (before any streamed step). With NST > 0 the next NST steps come from `stage`,
+// this lane's own LDS copy (word ((s - PS) * NMW + mw) * CPL + k of 64, lane-minor); the rest stream.
+template <class T, int NST = 0, typename RowPtr, typename After>
 __device__ __forceinline__ void tile_consume(const uint4 (&pf)[T::PS][T::CPL], int mw, int lane, const uint4* xh_lds,
-                                             const uint4* xl_lds, float* s_up, RowPtr rp, After after) {
+                                             const uint4* xl_lds, float* s_up, RowPtr rp, After after,
+                                             const uint4* stage = nullptr) {
+  static_assert(T::PS + NST <= T::STEPS, "staged steps");
   uint4 xh[T::CPL], xl[T::CPL];
 #pragma unroll
   for (int k = 0; k < T::CPL; ++k) {
@@ -522,7 +525,14 @@ __device__ __forceinline__ void tile_consume(const uint4 (&pf)[T::PS][T::CPL], i
   }
   after();
 #pragma unroll
-  for (int s = T::PS; s < T::STEPS; ++s) {
+  for (int s = T::PS; s < T::PS + NST; ++s) {
+    uint4 w[T::CPL];
+#pragma unroll
+    for (int k = 0; k < T::CPL; ++k) w[k] = stage[(((s - T::PS) * NMW + mw) * T::CPL + k) * 64 + lane];
+    tile_dot_step<T>(w, xh, xl, s, mw, lane, s_up);
+  }
+#pragma unroll
+  for (int s = T::PS + NST; s < T::STEPS; ++s) {
     uint4 w[1][T::CPL];
     tile_load<T, 1>(w, s, mw, lane, rp);
     tile_dot_step<T>(w[0], xh, xl, s, mw, lane, s_up);
@@ -585,6 +595,9 @@ struct Geo {
   typedef Tile<2 * DPW, H, 64, SMALL ? 8 : 1> TD;
   typedef Tile<HPW, IX, SMALL ? 16 : 32, SMALL ? 8 : 2> TE;
   static constexpr int XN = (H > IX ? H : IX);
+  // down steps after the register-held ones that go through LDS (see math_role, phase A)
+  static constexpr int EST = SMALL ? 0 : TE::STEPS - TE::PS;
+  static constexpr int EST_WORDS = EST > 0 ? EST * NMW * TE::CPL * 64 : 1;  // 16-byte words
   static constexpr int UMAX = 2 * DPW > HPW ? 2 * DPW : HPW;
   static constexpr int NSLOT = 2 * H + 2 * D;   // bf16 norm weights per layer: input, post-attention, q, k
   static constexpr int NSL16 = NSLOT / 8;       // ... in 16-byte chunks
@@ -613,6 +626,7 @@ struct Smem {
   uint32_t failed;                   // the launch drained (set before the LM head): logits are NaN
   mk_layer_weights layers[MAX_LAYERS];  // the layer table, copied once per launch
   int32_t bt[MAX_PAGES];             // block table of a paged launch (entries up to the position)
+  uint4 estage[Geo<H, I>::EST_WORDS];  // staged down steps, private to each math lane
 };
 
 // Element offset of the K/V row of `head` at position p in layer `layer`: contiguous
@@ -945,6 +959,8 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   auto slot_chunk = [&](int layer, int q) { return ad.slot_chunk(layer, q); };
 
   uint4 wA[TA::PS][TA::CPL], wC[TC::PS][TC::CPL], wD[TD::PS][TD::CPL], wE[TE::PS][TE::CPL];
+  constexpr int EST = G::EST;
+  uint4 wEs[EST > 0 ? EST : 1][TE::CPL];  // down steps PS .. STEPS - 1, on their way to LDS
   uint4 kK[NKV], kV[NKV];
   uint4 nsl[G::NSL_L];
 
@@ -1067,6 +1083,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     load_norms(layer);
     tile_consume<TA>(wA, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_A(lw), [&]() { mark(a, tl + T_M_A_DOT, 64); });
     mark(a, tl + T_M_A_END, 64);
+    if constexpr (EST > 0) tile_load<TE, EST>(wEs, TE::PS, opaque(mw), opaque(lane), rows_E(lw));
     lds_barrier();  // (A1)
     lds_barrier();  // (A2) comm: q, new K/V in LDS
     mark(a, tl + T_M_B_START, 64);
@@ -1131,6 +1148,12 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // C: o_proj partial over this group's 256 columns
     issue_ahead(I2(), layer);
     tile_consume<TC>(wC, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_C(lw), NoOp());
+    if constexpr (EST > 0) {
+#pragma unroll
+      for (int s2 = 0; s2 < EST; ++s2)
+#pragma unroll
+        for (int k = 0; k < TE::CPL; ++k) sm.estage[((s2 * NMW + mw) * TE::CPL + k) * 64 + lane] = wEs[s2][k];
+    }
     lds_barrier();  // (C1)
     lds_barrier();  // (C2) comm: x = RMSNorm(residual) * post-attention norm
 
@@ -1144,7 +1167,7 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     // E: down_proj partial over slice x's columns
     issue_ahead(I4(), layer);
     if constexpr (A_FIRST < TA::PS) load_phase(std::integral_constant<int, 6>(), layer + 1);
-    tile_consume<TE>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp());
+    tile_consume<TE, EST>(wE, opaque(mw), opaque(lane), sm.xh, sm.xl, sm.up, rows_E(lw), NoOp(), sm.estage);
     {
       // the next layer's norm weights (or the final norm) into the other LDS slot
       uint4* dst = reinterpret_cast<uint4*>(sm.nw[(layer + 1) & 1]);
@@ -1972,4 +1995,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.17 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.18 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }
