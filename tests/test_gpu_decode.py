@@ -35,6 +35,11 @@ def mini17():
 
 
 @pytest.fixture(scope="module")
+def mini_long():
+    return Session("mini", 4096)
+
+
+@pytest.fixture(scope="module")
 def q06():
     return Session("qwen3-0.6b", 512)
 
@@ -240,14 +245,16 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
     assert sess.kernel.status() == 0
 
 
-@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6)])
+@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6), ("mini_long", 3700, 4)])
 def test_paged_cache_matches_oracle(shape_fixture, P, n, request):
     """``decode_paged`` against the fp32 restatement on the gathered cache: every step, the cache the
     kernel has written through the block table is gathered back to ``[L, 8, max_seq, 128]`` and the
     restatement decodes the same token at the same position on it -- logits to 5e-3, the same
     greedy token, and the row the kernel wrote within one bf16 rounding step of the restatement's.
     Then ``decode_steps_paged`` (teacher mode) continues for n steps and its last logits and rows are
-    checked against the restatement run step by step on its own cache."""
+    checked against the restatement run step by step on its own cache. From prompt 3700 (cache 4096,
+    16 splits of ~231 positions) every split streams 5-6 K/V rows per group beyond its two register
+    rows through the block table, in one round of six."""
     from tests.paged_layout import from_pages
     sess = request.getfixturevalue(shape_fixture)
     ps = 32
