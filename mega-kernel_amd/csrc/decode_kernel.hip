@@ -79,9 +79,12 @@ constexpr int SPLIT_POS = MG;        // positions per split while the split coun
 template <int H> constexpr int merge_sb0() { return H <= 1024 ? 4 : 2; }
 constexpr int SB1 = 8;
 // Contexts above this many positions use two merge rounds' worth of splits, which spreads the
-// streamed K/V rows over twice as many CUs (measured on MI355X: at context 2000 (4000) 16 splits
-// take 525 (593) us per token at 0.6B against 556 (670) with 8).
-constexpr int S_LONG_CTX = 1024;
+// streamed K/V rows over twice as many CUs (measured on MI355X with four streamed rows per round:
+// at context 2000 (4000) 16 splits took 525 (593) us per token at 0.6B against 556 (670) with 8).
+// At the 1024 width, whose splits stream six rows per round, 8 splits cover up to 2048 positions
+// in one round and stay faster up to there (kernel 0.20, prompt 1100 / 1500 / 1900: -6 / -9.5 /
+// -1 us per token against switching at 1024).
+template <int H> constexpr int s_long_ctx() { return H <= 1024 ? 2048 : 1024; }
 constexpr int APW = 264;      // LL words per attention partial: acc[2][128], m0, l0, m1, l1, pad
 constexpr float EPS = 1e-6f;
 constexpr float ATT_SCALE = 0.08838834764831845f;  // 128 ** -0.5
@@ -661,7 +664,7 @@ struct Step {
 // split per SPLIT_POS positions, capped at what one merge round takes (two rounds' worth for long
 // contexts): a merge round costs more than a longer split. One register row while the splits are
 // at most SPLIT_POS long (a second would only re-read a row), two once they are longer, so that
-// contexts up to 512 (2048 at two merge rounds) stream no K/V inside the attention phase.
+// contexts up to 512 (1024 at two merge rounds) stream no K/V inside the attention phase.
 // (Measured on MI355X: packing two rows per group earlier, to keep S within one merge poll up to
 // context 256, costs 3-4 us per token at the 0.6B shape and ~4 at 1.7B for short contexts.)
 struct SplitPlan {
@@ -669,7 +672,7 @@ struct SplitPlan {
 };
 template <int H>
 __host__ __device__ constexpr SplitPlan split_plan(int ctx) {
-  const int cap = ctx > S_LONG_CTX ? 2 * SB1 : SB1;
+  const int cap = ctx > s_long_ctx<H>() ? 2 * SB1 : SB1;
   const int S = (ctx + SPLIT_POS - 1) / SPLIT_POS;
   return {S < cap ? S : cap, ctx > cap * SPLIT_POS ? 2 : 1};
 }
@@ -851,10 +854,9 @@ __device__ __forceinline__ void attention_split(const KArgs& a, Smem<H, I>& sm, 
 template <int H>
 struct LmTile {
   static constexpr int LCPL = H / 512;  // 16-byte chunks per lane of one row
-#ifndef MK_LP
-#define MK_LP 4
-#endif
-  static constexpr int LP = H <= 1024 ? MK_LP : MK_LP / 2;  // rows in flight per wave (register budget)
+  // rows in flight per wave: measured on MI355X (kernel 0.19, config 2), 3 at the 1024 width beats 4
+  // by ~1.8 us per token and 2 or 5 by ~1 us; at 2048 (register budget) 2, with 3 no faster
+  static constexpr int LP = H <= 1024 ? 3 : 2;
   // row groups of NMW rows interleaved over the workgroups (step s reads group blockIdx.x + NWG*s),
   // so the grid sweeps the table front to back instead of 256 separate streams
   __device__ static int nmine(const KArgs& a) {
@@ -1995,4 +1997,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.19 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.20 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }

@@ -245,16 +245,18 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
     assert sess.kernel.status() == 0
 
 
-@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6), ("mini_long", 3700, 4)])
+@pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6), ("mini_long", 1500, 4),
+                                                 ("mini_long", 2040, 4), ("mini_long", 3700, 4)])
 def test_paged_cache_matches_oracle(shape_fixture, P, n, request):
     """``decode_paged`` against the fp32 restatement on the gathered cache: every step, the cache the
     kernel has written through the block table is gathered back to ``[L, 8, max_seq, 128]`` and the
     restatement decodes the same token at the same position on it -- logits to 5e-3, the same
     greedy token, and the row the kernel wrote within one bf16 rounding step of the restatement's.
     Then ``decode_steps_paged`` (teacher mode) continues for n steps and its last logits and rows are
-    checked against the restatement run step by step on its own cache. From prompt 3700 (cache 4096,
-    16 splits of ~231 positions) every split streams 5-6 K/V rows per group beyond its two register
-    rows through the block table, in one round of six."""
+    checked against the restatement run step by step on its own cache. At the 1024 width, from
+    prompt 1500 and 2040 (8 splits up to context 2048: ~4 and 6 streamed rows per group, the last
+    steps at 2048) and 3700 (16 splits of ~231 positions: 5-6 per group), every split streams K/V
+    rows beyond its two register rows through the block table, in one round of six."""
     from tests.paged_layout import from_pages
     sess = request.getfixturevalue(shape_fixture)
     ps = 32
