@@ -88,7 +88,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus} is not supported: this build targets one MI355X; the decode step "
-              "runs on one GPU (see DESIGN.md for how it would shard)", file=sys.stderr)
+              "runs on one GPU (no multi-GPU sharding is built)", file=sys.stderr)
         return 2
     import torch
     import megakernel
