@@ -40,6 +40,11 @@ def mini_long():
 
 
 @pytest.fixture(scope="module")
+def mini17_long():
+    return Session("mini-1.7b", 2048)
+
+
+@pytest.fixture(scope="module")
 def q06():
     return Session("qwen3-0.6b", 512)
 
@@ -246,7 +251,8 @@ def test_paged_cache_matches_contiguous(shape_fixture, P, request):
 
 
 @pytest.mark.parametrize("shape_fixture, P, n", [("mini", 300, 10), ("mini17", 250, 6), ("mini_long", 1500, 4),
-                                                 ("mini_long", 2040, 4), ("mini_long", 3700, 4)])
+                                                 ("mini_long", 2040, 4), ("mini_long", 3700, 4),
+                                                 ("mini17_long", 1800, 4)])
 def test_paged_cache_matches_oracle(shape_fixture, P, n, request):
     """``decode_paged`` against the fp32 restatement on the gathered cache: every step, the cache the
     kernel has written through the block table is gathered back to ``[L, 8, max_seq, 128]`` and the
@@ -256,7 +262,8 @@ def test_paged_cache_matches_oracle(shape_fixture, P, n, request):
     checked against the restatement run step by step on its own cache. At the 1024 width, from
     prompt 1500 and 2040 (8 splits up to context 2048: ~4 and 6 streamed rows per group, the last
     steps at 2048) and 3700 (16 splits of ~231 positions: 5-6 per group), every split streams K/V
-    rows beyond its two register rows through the block table, in one round of six."""
+    rows beyond its two register rows through the block table, in one round of six; at the 2048
+    width from prompt 1800 (16 splits of ~113 positions) one round of up to four."""
     from tests.paged_layout import from_pages
     sess = request.getfixturevalue(shape_fixture)
     ps = 32
