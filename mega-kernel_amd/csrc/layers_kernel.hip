@@ -67,20 +67,33 @@ __device__ __forceinline__ size_t kv_row(const KvMap& m, int layer, int head, in
 
 
 // ------------------------------------------------------------------------------------------------
-// GEMM C[M][N] = A[M][K] . W[N][K]^T on the matrix cores, A given as a bf16 hi/lo pair, W bf16
-// row-major (nn.Linear layout, read in place). Tile 128 x 128 per workgroup of 4 waves (2 x 2, 64 x
-// 64 each), K in steps of 64 staged through LDS, the next step's global loads in flight during the
-// current step's MFMAs. The epilogue takes the tile's fp32 sums.
+// GEMM C[M][N] = A[M][K] . W[N][K]^T on the matrix cores, A given as a bf16 hi/lo pair in the
+// fragment-major layout below, W bf16 row-major (nn.Linear layout, read in place). Tile 128 x 128
+// per workgroup of 4 waves, wave w taking rows [32 w, 32 w + 32) and all 128 columns. K in steps of
+// 64: the weight tile is staged through LDS (every wave reads all of it), the activation fragments
+// go straight from memory into the registers of the one wave that uses them, so only a third of the
+// operand bytes are written to LDS. The next step's loads are in flight during the current step's
+// MFMAs. The epilogue takes the tile's fp32 sums.
 // ------------------------------------------------------------------------------------------------
 constexpr int MT = 128, NT = 128, KT = 64, KP = KT + 8;  // KP: padded LDS row (144 B)
 constexpr int CP = NT + 4;                              // padded fp32 row of the epilogue tile
 
+// Fragment-major layout of a bf16 activation matrix with K columns (K a multiple of 32), the A
+// operand of gemm_kernel: 16-row x 32-column blocks of 1 KB, block (m / 16, k / 32) at KB offset
+// (m / 16) * (K / 32) + k / 32; inside a block, MFMA lane l = (m % 16) + 16 * ((k % 32) / 8) holds
+// the 16 bytes of columns [8 ((k % 32) / 8), +8). A wave reads one operand fragment as 1 KB of
+// consecutive bytes. Buffers in this layout hold a multiple of MT rows; rows past M are never
+// written, and the sums they produce are never stored.
+__device__ __forceinline__ size_t frag_off(int m, int k, int K) {
+  return ((((size_t)(m >> 4) * (K >> 5) + (k >> 5)) * 64 + ((k >> 3) & 3) * 16 + (m & 15)) << 3) + (k & 7);
+}
+static size_t frag_rows(int M) { return (size_t)(M + MT - 1) / MT * MT; }
+
 enum Epi { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2 };
 
 struct GemmArgs {
-  const uint16_t* ah;
+  const uint16_t* ah;  // fragment-major, K columns
   const uint16_t* al;
-  int lda;
   int M, N, K;
   // weights: EPI_RESID: w0 [N][K]; EPI_QKV: w0 = Wq, w1 = Wk, w2 = Wv; EPI_SILU: w0 = Wg, w1 = Wu
   const uint16_t* w0;
@@ -91,10 +104,9 @@ struct GemmArgs {
   float* x;
   int ldx;
   float* part;
-  // EPI_SILU: m = silu(gate) * up into bh/bl [M][ldb]
+  // EPI_SILU: m = silu(gate) * up into bh/bl, fragment-major with I = N / 2 columns
   uint16_t* bh;
   uint16_t* bl;
-  int ldb;
   // EPI_QKV
   const uint16_t* q_norm;
   const uint16_t* k_norm;
@@ -125,10 +137,7 @@ __device__ __forceinline__ const uint16_t* weight_row(const GemmArgs& g, int t, 
 
 struct GemmSmem {
   union {
-    struct {
-      uint16_t a[2][MT][KP];  // hi, lo
-      uint16_t w[NT][KP];
-    } t;
+    uint16_t w[NT][KP];
     float c[MT][CP];
   };
 };
@@ -137,68 +146,92 @@ template <int EPI>
 __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) GemmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tn = blockIdx.x, m0 = blockIdx.y * MT;
+  int tn = blockIdx.x, tm = blockIdx.y;
+  if (gridDim.x <= 16 && gridDim.y >= 8 && (gridDim.x * gridDim.y) % 8 == 0) {
+    // Few column tiles and many row tiles (the residual products of long prompts): consecutive
+    // workgroups go to the 8 XCDs in turn, so with the plain order the column tiles of one row tile
+    // would sit on different XCDs and each XCD's L2 would fetch that row tile's activations again.
+    // XCD b % 8 takes the b % 8-th eighth of the tiles instead, row tile by row tile: the column
+    // tiles sharing activations share an L2. (With few row tiles the weights are the larger stream
+    // and the plain order, one column tile per XCD, measured faster.)
+    const int T = gridDim.x * gridDim.y, b = blockIdx.x + gridDim.x * blockIdx.y;
+    const int t = (b & 7) * (T >> 3) + (b >> 3);
+    tn = t % gridDim.x;
+    tm = t / gridDim.x;
+  }
+  const int m0 = tm * MT;
   const int li = lane & 15, lg = lane >> 4;
+  const int kch = g.K >> 5;  // 1 KB fragments per 16-row block
 
-  // global -> register staging: 4 chunks of 16 bytes per thread per matrix (row c / 8, chunk c % 8)
-  uint4 ra[2][4], rw[4];
-  auto load = [&](int k0) {
+  // this wave's two 16-row blocks of A: fragment (bm, 32-column chunk kc) at uint4 (bm * kch + kc) * 64
+  const size_t abase = (size_t)((m0 >> 4) + 2 * wave) * kch * 64 + lane;
+  const uint4* pah = reinterpret_cast<const uint4*>(g.ah) + abase;
+  const uint4* pal = reinterpret_cast<const uint4*>(g.al) + abase;
+  // one K step of A: [32-column half s][row block bm][hi, lo]
+  typedef uint4 AStep[2][2][2];
+  auto load_a = [&](int k0, AStep& d) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm) {
+        const int f = (bm * kch + (k0 >> 5) + s) * 64;
+        d[s][bm][0] = pah[f];
+        d[s][bm][1] = pal[f];
+      }
+  };
+  // weights: global -> registers -> LDS, 4 chunks of 16 bytes per thread (row c / 8, chunk c % 8)
+  uint4 rw[4];
+  auto load_w = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      const int m = m0 + row;
-      if (m < g.M) {
-        ra[0][i] = *reinterpret_cast<const uint4*>(g.ah + (size_t)m * g.lda + k0 + 8 * ch);
-        ra[1][i] = *reinterpret_cast<const uint4*>(g.al + (size_t)m * g.lda + k0 + 8 * ch);
-      } else {
-        ra[0][i] = make_uint4(0, 0, 0, 0);
-        ra[1][i] = make_uint4(0, 0, 0, 0);
-      }
       rw[i] = ld_stream(reinterpret_cast<const uint4*>(weight_row<EPI>(g, tn, row) + k0 + 8 * ch));
     }
   };
-  auto store = [&]() {
+  auto store_w = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<uint4*>(&sm.t.a[0][row][8 * ch]) = ra[0][i];
-      *reinterpret_cast<uint4*>(&sm.t.a[1][row][8 * ch]) = ra[1][i];
-      *reinterpret_cast<uint4*>(&sm.t.w[row][8 * ch]) = rw[i];
+      *reinterpret_cast<uint4*>(&sm.w[row][8 * ch]) = rw[i];
     }
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[2][8];
 #pragma unroll
-  for (int bm = 0; bm < 4; ++bm)
+  for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-    for (int bn = 0; bn < 4; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int bn = 0; bn < 8; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kspan = g.K / gridDim.z, kb = blockIdx.z * kspan, ke = kb + kspan;  // a multiple of KT
-  load(kb);
+  AStep an, ac;
+  load_w(kb);
+  load_a(kb, an);
   for (int k0 = kb; k0 < ke; k0 += KT) {
-    __syncthreads();  // every wave is done with the previous step's tile
-    store();
+    __syncthreads();  // every wave is done with the previous step's weight tile
+    store_w();
     __syncthreads();
-    if (k0 + KT < ke) load(k0 + KT);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm) {
+        ac[s][bm][0] = an[s][bm][0];
+        ac[s][bm][1] = an[s][bm][1];
+      }
+    if (k0 + KT < ke) {
+      load_w(k0 + KT);
+      load_a(k0 + KT, an);
+    }
 #pragma unroll
     for (int s = 0; s < KT / 32; ++s) {
-      uint4 fa[2][4], fw[4];
+      uint4 fw[8];
 #pragma unroll
-      for (int bm = 0; bm < 4; ++bm) {
-        const int r = wm * 64 + bm * 16 + li;
-        fa[0][bm] = *reinterpret_cast<const uint4*>(&sm.t.a[0][r][32 * s + 8 * lg]);
-        fa[1][bm] = *reinterpret_cast<const uint4*>(&sm.t.a[1][r][32 * s + 8 * lg]);
-      }
+      for (int bn = 0; bn < 8; ++bn) fw[bn] = *reinterpret_cast<const uint4*>(&sm.w[bn * 16 + li][32 * s + 8 * lg]);
 #pragma unroll
-      for (int bn = 0; bn < 4; ++bn)
-        fw[bn] = *reinterpret_cast<const uint4*>(&sm.t.w[wn * 64 + bn * 16 + li][32 * s + 8 * lg]);
+      for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-      for (int bm = 0; bm < 4; ++bm)
-#pragma unroll
-        for (int bn = 0; bn < 4; ++bn) {
-          acc[bm][bn] = mfma(fa[0][bm], fw[bn], acc[bm][bn]);
-          acc[bm][bn] = mfma(fa[1][bm], fw[bn], acc[bm][bn]);
+        for (int bn = 0; bn < 8; ++bn) {
+          acc[bm][bn] = mfma(ac[s][bm][0], fw[bn], acc[bm][bn]);
+          acc[bm][bn] = mfma(ac[s][bm][1], fw[bn], acc[bm][bn]);
         }
     }
   }
@@ -207,13 +240,13 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
     // x += C (or C into this K range's partial), each element owned by one lane
     auto each = [&](auto&& f) {
 #pragma unroll
-      for (int bm = 0; bm < 4; ++bm)
+      for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int m = m0 + wm * 64 + bm * 16 + 4 * lg + j;
+          const int m = m0 + wave * 32 + bm * 16 + 4 * lg + j;
           if (m < g.M) {
 #pragma unroll
-            for (int bn = 0; bn < 4; ++bn) f(m, tn * NT + wn * 64 + bn * 16 + li, acc[bm][bn][j]);
+            for (int bn = 0; bn < 8; ++bn) f(m, tn * NT + bn * 16 + li, acc[bm][bn][j]);
           }
         }
     };
@@ -229,11 +262,11 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   // QKV and SILU need whole rows of the tile: through LDS
   __syncthreads();
 #pragma unroll
-  for (int bm = 0; bm < 4; ++bm)
+  for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-    for (int bn = 0; bn < 4; ++bn)
+    for (int bn = 0; bn < 8; ++bn)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sm.c[wm * 64 + bm * 16 + 4 * lg + j][wn * 64 + bn * 16 + li] = acc[bm][bn][j];
+      for (int j = 0; j < 4; ++j) sm.c[wave * 32 + bm * 16 + 4 * lg + j][bn * 16 + li] = acc[bm][bn][j];
   __syncthreads();
   const int r = tid >> 1, half = tid & 1;  // two threads per row
   const int m = m0 + r;
@@ -252,7 +285,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
       }
       uint4 hi, lo;
       split8(mv, hi, lo);
-      const size_t o = (size_t)m * g.ldb + tn * (NT / 2) + c0 + c;
+      const size_t o = frag_off(m, tn * (NT / 2) + c0 + c, g.N / 2);
       *reinterpret_cast<uint4*>(g.bh + o) = hi;
       *reinterpret_cast<uint4*>(g.bl + o) = lo;
     }
@@ -347,9 +380,10 @@ struct AttnArgs {
   const uint16_t* ql;
   const uint16_t* k_cache;
   const uint16_t* v_cache;
-  uint16_t* oh;
+  uint16_t* oh;  // output rows [M][ldo], or with `frag` fragment-major with 16 * 128 columns
   uint16_t* ol;
   int ldo;
+  int frag;
   int M, layer, position;
   KvMap kv;
   int32_t* bad;
@@ -568,7 +602,8 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
       const int c = lane + 64 * r, part = c >> 8, row = (c >> 4) & 15, ch = c & 15;
       const int m = q0 + wq + row;
       const uint4 v = *reinterpret_cast<const uint4*>(&sm.o[w][part][row][8 * ch]);
-      if (m < a.M) *reinterpret_cast<uint4*>((part ? a.ol : a.oh) + (size_t)m * a.ldo + h * D + 8 * ch) = v;
+      const size_t o = a.frag ? frag_off(m, h * D + 8 * ch, HQ * D) : (size_t)m * a.ldo + h * D + 8 * ch;
+      if (m < a.M) *reinterpret_cast<uint4*>((part ? a.ol : a.oh) + o) = v;
     }
   }
 }
@@ -830,8 +865,9 @@ static int column_blocks(int rows) { return rows <= 8 ? 1 : rows <= 16 ? 2 : row
 
 // Rows b < B of the residual: with `tokens`, x[b] = embed[tokens[b]] (a token outside [0, vocab)
 // reads row 0 and sets *bad); with `part`, x[b] += sum over s < S of part[s][b] (in order); then,
-// with `w`, RMSNorm into the bf16 hi/lo pair [B][lda]. One wave per row.
-template <int H>
+// with `w`, RMSNorm into the bf16 hi/lo pair: [B][lda], or with FRAG the fragment-major layout of
+// H columns that gemm_kernel reads. One wave per row.
+template <int H, bool FRAG = false>
 __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tokens, const uint16_t* embed, int vocab,
                                                     int32_t* bad, const float* part, int S, const uint16_t* w,
                                                     uint16_t* ah, uint16_t* al, int lda, int B) {
@@ -887,8 +923,9 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
     for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
     uint4 hi, lo;
     split8(y, hi, lo);
-    *reinterpret_cast<uint4*>(ah + (size_t)b * lda + E * lane + k) = hi;
-    *reinterpret_cast<uint4*>(al + (size_t)b * lda + E * lane + k) = lo;
+    const size_t o = FRAG ? frag_off(b, E * lane + k, H) : (size_t)b * lda + E * lane + k;
+    *reinterpret_cast<uint4*>(ah + o) = hi;
+    *reinterpret_cast<uint4*>(al + o) = lo;
   }
 }
 
@@ -1138,15 +1175,17 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // to the residual by the next norm, in split order.
 static int resid_splits(int H, int M, int K) {
   const int tiles = (H / NT) * ((M + MT - 1) / MT);
-  if (M <= SMALL_M || tiles >= 192) return 1;
-  int sp = (512 + tiles - 1) / tiles;
+  if (M <= SMALL_M || tiles >= 512) return 1;
+  // two workgroups per CU: from 192 tiles on, as many splits as keep the grid within 512
+  int sp = tiles >= 192 ? 512 / tiles : (512 + tiles - 1) / tiles;
   sp = sp < 8 ? sp : 8;
   while ((K / KT) % sp != 0) --sp;
   return sp;
 }
 
-// Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16 [M][max(H, 2048)]; b (hi, lo) bf16
-// [M][I]; q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums; the split-K partials of
+// Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16, max(H, 2048) columns; b (hi, lo)
+// bf16, I columns (a and b: row-major for the skinny kernels, fragment-major for gemm_kernel, rows
+// rounded up to MT); q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums; the split-K partials of
 // the residual products; the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
   size_t x, ah, al, bh, bl, qh, ql, raw, part, keys, bad, bytes;
@@ -1156,11 +1195,12 @@ static Layout layout(int H, int I, int M) {
   Layout L;
   size_t o = 0;
   auto take = [&](size_t n) { const size_t r = o; o += align256(n); return r; };
+  const size_t MA = frag_rows(M);  // the GEMMs' activation operands hold whole row tiles
   L.x = take((size_t)M * H * 4);
-  L.ah = take((size_t)M * A * 2);
-  L.al = take((size_t)M * A * 2);
-  L.bh = take((size_t)M * I * 2);
-  L.bl = take((size_t)M * I * 2);
+  L.ah = take(MA * A * 2);
+  L.al = take(MA * A * 2);
+  L.bh = take(MA * I * 2);
+  L.bl = take(MA * I * 2);
   L.qh = take((size_t)M * HQ * D * 2);
   L.ql = take((size_t)M * HQ * D * 2);
   L.raw = take(M <= SMALL_M ? (size_t)M * (HQ + 2 * HKV) * D * 4 : 0);
@@ -1203,7 +1243,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad);
-  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M, 0, position, kv, wk.bad};
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M > SMALL_M ? 1 : 0, M, 0, position, kv, wk.bad};
   const dim3 attn_grid(((M + QB - 1) / QB + 1) / 2, HKV);
   if (M <= SMALL_M) {
     // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
@@ -1254,10 +1294,10 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   for (int l = 0; M > SMALL_M && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
     const dim3 rows((M + 3) / 4);
-    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab, wk.bad,
-               wk.part, l > 0 && sd > 1 ? sd : 0, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
+    MKP_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab,
+               wk.bad, wk.part, l > 0 && sd > 1 ? sd : 0, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
     GemmArgs g{};
-    g.ah = wk.ah; g.al = wk.al; g.lda = A; g.M = M; g.K = H;
+    g.ah = wk.ah; g.al = wk.al; g.M = M; g.K = H;
     g.w0 = (const uint16_t*)lw.q_weight; g.w1 = (const uint16_t*)lw.k_weight; g.w2 = (const uint16_t*)lw.v_weight;
     g.N = (HQ + 2 * HKV) * D;
     g.q_norm = (const uint16_t*)lw.q_norm_weight; g.k_norm = (const uint16_t*)lw.k_norm_weight;
@@ -1268,18 +1308,18 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     at.layer = l;
     MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
     GemmArgs go{};
-    go.ah = wk.ah; go.al = wk.al; go.lda = A; go.M = M; go.N = H; go.K = HQ * D;
+    go.ah = wk.ah; go.al = wk.al; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H; go.part = so > 1 ? wk.part : nullptr;
     MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, so), dim3(256), 0, st, go);
-    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
+    MKP_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
                so > 1 ? so : 0, (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
     GemmArgs gu{};
-    gu.ah = wk.ah; gu.al = wk.al; gu.lda = A; gu.M = M; gu.N = 2 * I; gu.K = H;
+    gu.ah = wk.ah; gu.al = wk.al; gu.M = M; gu.N = 2 * I; gu.K = H;
     gu.w0 = (const uint16_t*)lw.gate_proj_weight; gu.w1 = (const uint16_t*)lw.up_proj_weight;
-    gu.bh = wk.bh; gu.bl = wk.bl; gu.ldb = I;
+    gu.bh = wk.bh; gu.bl = wk.bl;
     MKP_LAUNCH(gemm_kernel<EPI_SILU>, dim3(I / (NT / 2), mtiles), dim3(256), 0, st, gu);
     GemmArgs gd{};
-    gd.ah = wk.bh; gd.al = wk.bl; gd.lda = I; gd.M = M; gd.N = H; gd.K = I;
+    gd.ah = wk.bh; gd.al = wk.bl; gd.M = M; gd.N = H; gd.K = I;
     gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H; gd.part = sd > 1 ? wk.part : nullptr;
     MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, sd), dim3(256), 0, st, gd);
   }
@@ -1378,8 +1418,8 @@ static BLayout blayout(int H, int I, int B, int max_seq) {
   size_t o = 0;
   auto take = [&](size_t n) { const size_t r = o; o += align256(n); return r; };
   L.x = take((size_t)B * H * 4);
-  L.ah = take((size_t)B * A * 2);
-  L.al = take((size_t)B * A * 2);
+  L.ah = take(frag_rows(B) * A * 2);  // whole row tiles for the LM head's gemm_kernel
+  L.al = take(frag_rows(B) * A * 2);
   L.bh = take((size_t)B * I * 2);
   L.bl = take((size_t)B * I * 2);
   L.raw = take((size_t)B * (HQ + 2 * HKV) * D * 4);
@@ -1454,9 +1494,14 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   // the last layer's down partials and the final norm, then the tied LM head as one more skinny
   // product (vocabulary rows x the B normalised rows: each table byte read once, on the matrix
   // cores) and the greedy keys
-  MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, final_norm,
-             ah, al, A, B);
-  if (B <= 8 || dims.vocab % NT != 0) {
+  const bool lm_tiles = B > 8 && dims.vocab % NT == 0;
+  if (lm_tiles)
+    MKB_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD,
+               final_norm, ah, al, A, B);
+  else
+    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, final_norm,
+               ah, al, A, B);
+  if (!lm_tiles) {
     SkArgs lmh{};
     lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
     lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
@@ -1465,7 +1510,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     // beyond one column block the skinny product re-reads every row's activations per 16 table
     // rows; a 128-row tile of the table reads them once per 128 (the B rows are one row tile)
     GemmArgs gl{};
-    gl.ah = ah; gl.al = al; gl.lda = A; gl.M = B; gl.N = dims.vocab; gl.K = H;
+    gl.ah = ah; gl.al = al; gl.M = B; gl.N = dims.vocab; gl.K = H;
     gl.w0 = lm_head; gl.part = logits;  // logits[b][v], no residual
     MKB_LAUNCH(gemm_kernel<EPI_RESID>, dim3(dims.vocab / NT, 1, 1), dim3(256), 0, st, gl);
   }
