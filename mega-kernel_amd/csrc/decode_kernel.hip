@@ -1997,4 +1997,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.20 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.21 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure; prefill GEMMs on fragment-major activations)"; }
