@@ -490,10 +490,7 @@ __device__ __forceinline__ void tile_consume(const uint4 (&pf)[T::PS][T::CPL], i
     xh[k] = xh_lds[k * T::SPAN + lane % T::SPAN];
     xl[k] = xl_lds[k * T::SPAN + lane % T::SPAN];
   }
-#ifndef MK_JOINT_RED
-#define MK_JOINT_RED 1
-#endif
-  if constexpr (MK_JOINT_RED && T::SPAN == 64 && (T::PS == 2 || T::PS == 4) && T::PS == T::STEPS) {
+  if constexpr (T::SPAN == 64 && (T::PS == 2 || T::PS == 4) && T::PS == T::STEPS) {
     // whole-wave rows, all prefetched: reduce the PS row sums together. Each lane-swap step halves
     // the values a lane carries (gfx950 v_permlane32/16_swap: lanes 0-31 keep the first operand's
     // pair sums, lanes 32-63 the second's; likewise per 16-lane row pair), so PS rows cost one
