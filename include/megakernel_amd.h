@@ -6,8 +6,9 @@
  *
  * Concurrency. A decode launch needs every CU of the device at once (one workgroup per CU,
  * waiting on each other). Each stream that launches gets its own exchange workspace (allocated on
- * the stream's first launch, up to 64 streams per device), so launches on different streams never
- * share exchange words; but launches that overlap in time on one device cannot all be resident:
+ * the stream's first launch; 64 sets per device, a 65th stream takes over the least recently used
+ * set after a device synchronization), so launches on different streams never share exchange
+ * words; but launches that overlap in time on one device cannot all be resident:
  * they wait with bounded spins and end as failed launches (see "Failure" below). Serialize decode
  * calls per device.
  *
@@ -252,19 +253,22 @@ hipError_t mk_decode_steps_paged(const mk_model_dims* dims, int32_t* tokens, int
  *   bit 3  a block-table entry was out of range: page 0 was read, and the new K/V rows were not
  *          written when the position's own entry was the bad one;
  *   bit 4  set by mk_request_drain: every later launch drains (NaN logits, token -1).
- * Bits are set with atomic ORs and only mk_reset clears them. Synchronizes with the device.
+ * Bits are set with atomic ORs and only mk_reset clears them; bits of a workspace set handed to
+ * another stream (more than 64 launching streams on the device) are kept. Synchronizes with the
+ * device.
  * No reference counterpart: the reference surfaces errors only through the launch status. */
 hipError_t mk_status(uint32_t* status);
 
 /* Engine of mk_decode_batch for the calling process: 0 automatic (the persistent kernel where it
- * applies: the Qwen3-0.6B shape, 1..8 sequences, at most 32 layers, a device with 256 CUs), 1 always
+ * applies: the Qwen3-0.6B shape, 1..16 sequences -- one MFMA column block up to 8, two from 9 on --, at
+ * most 32 layers, a device with 256 CUs), 1 always
  * the layer-by-layer engine, 2 the persistent kernel where it applies. Both give each sequence
  * mk_decode's numerics. hipErrorInvalidValue for another value. No reference counterpart. */
 hipError_t mk_set_batch_engine(int engine);
 
 /* Phase trace of the persistent batched kernel: with a device buffer of at least
  * mk_batch_trace_bytes() bytes, later launches store s_memrealtime stamps (100 MHz) per workgroup
- * (index j * 8 + xcd), layer (33 rows of 16 stamps; row 32: kernel start, LM head start and end) at
+ * (index j * 8 + xcd), layer (33 rows of 24 stamps; row 32: kernel start, LM head start and end) at
  * fixed points of each layer; NULL turns it off. For profiling (megakernel.batch_trace). No
  * reference counterpart. */
 hipError_t mk_set_batch_trace(uint64_t* device_buffer, size_t bytes);
@@ -274,11 +278,14 @@ size_t mk_batch_trace_bytes(void);
  * restarts their launch sequences. Synchronizes with the device. No reference counterpart. */
 hipError_t mk_reset(void);
 
-/* Sets status bit 4 on every workspace of the current device, so that every later launch drains at
- * once (all its waits give up, NaN logits, token -1) until mk_reset: lets a caller abandon work it
- * has queued (a long mk_decode_steps), and lets tests exercise the failure path with every kernel
- * still exiting normally. The persistent batched kernel of mk_decode_batch drains too (NaN logits,
- * token -1 for every sequence). Synchronizes with the device. No reference counterpart. */
+/* Waits for all work queued on the current device to finish (a device synchronization), then sets
+ * status bit 4 on every workspace of the device, so that every launch enqueued after the call drains
+ * at once (all its waits give up, NaN logits, token -1) until mk_reset. Launches queued before the
+ * call run to completion first: it does not abandon queued work. Workspace sets created later (a new
+ * stream's, or mk_decode_noalloc's first use) start drained too, and batched decodes enqueued after
+ * the call on the persistent kernel of mk_decode_batch drain as well (NaN logits, token -1 for every
+ * sequence). Its use is to exercise the failure path with every kernel still exiting normally. No
+ * reference counterpart. */
 hipError_t mk_request_drain(void);
 
 /* Bytes of one exchange workspace set (the static array of mk_decode_noalloc has this size; each

@@ -81,37 +81,19 @@ static_assert(QR == 16 && OR == 32 && GI == 12, "work split of the 0.6B shape");
 // gate/up after C1 and C3 with down after E2 708. Later, at 8 and 16 sequences: down after E1 613
 // and 840 us, after E2 618 and 856; the next layer's first K/V round after F1 641 and 875, after F2
 // 627 and 857.
-// The split merge on all waves (1) or on the comm waves only (0), the math waves issuing loads meanwhile.
-#ifndef MKB_MERGE_ALL
-#define MKB_MERGE_ALL 1
-#endif
+// The split merge on all waves (true) or on the comm waves only, the math waves issuing loads meanwhile.
+constexpr bool MERGE_ALL = true;
 // K steps per load chunk of the LM head (two chunks in flight per wave).
-#ifndef MKB_LM_CH
-#define MKB_LM_CH 8
-#endif
-// Polls of up to MKB_TWO_MAX chunks per lane keep two rounds of loads in flight.
-#ifndef MKB_TWO_MAX
-#define MKB_TWO_MAX 4
-#endif
-#ifndef MKB_GU_AT
-#define MKB_GU_AT 4
-#endif
-#ifndef MKB_GU2_AT
-#define MKB_GU2_AT 6  // >= 0: the second half of the gate/up rows at this point (-1: all at GU_AT)
-#endif
-#ifndef MKB_DN_AT
-#define MKB_DN_AT 7
-#endif
-#ifndef MKB_QKV_AT
-#define MKB_QKV_AT 6
-#endif
-#ifndef MKB_O_AT
-#define MKB_O_AT 10
-#endif
-#ifndef MKB_KV_AT
-#define MKB_KV_AT 8
-#endif
-static_assert(MKB_GU_AT <= 6 && MKB_DN_AT <= 8 && MKB_QKV_AT >= 1 && MKB_O_AT >= 6 && MKB_KV_AT >= 3,
+constexpr int LM_CH = 8;
+// Polls of up to POLL_TWO_MAX chunks per lane keep two rounds of loads in flight.
+constexpr int POLL_TWO_MAX = 4;
+constexpr int GU_AT = 4;
+constexpr int GU2_AT = 6;  // >= 0: the second half of the gate/up rows at this point (-1: all at GU_AT)
+constexpr int DN_AT = 7;
+constexpr int QKV_AT = 6;
+constexpr int O_AT = 10;
+constexpr int KV_AT = 8;
+static_assert(GU_AT <= 6 && DN_AT <= 8 && QKV_AT >= 1 && O_AT >= 6 && KV_AT >= 3,
               "load schedule");
 
 // Exchange area (32-bit words) of a launch with up to BM sequences, zeroed before every launch
@@ -181,6 +163,7 @@ struct Smem {
   u64 wk[NWAVE][BM];             // LM head keys per wave
   int pos[BM], tok[BM], f[BM], ns[BM], sb[WPX];
   int x, j, nsplit, ks, bad;
+  uint32_t badseq;  // bit b: sequence b's position or token is out of range
 };
 
 // threadIdx.x with its origin hidden from the optimizer: lane offsets derived from it are recomputed
@@ -252,7 +235,7 @@ __device__ __forceinline__ void poll(Ctl& c, const uint32_t* base, const int (&o
     }
     return false;
   };
-  if constexpr (NK <= MKB_TWO_MAX) {
+  if constexpr (NK <= POLL_TWO_MAX) {
     u4v r0[NK], r1[NK];
     issue(r0);
     for (uint32_t it = 0;; it += 2) {
@@ -549,6 +532,7 @@ __device__ __forceinline__ void mma_to_red(S& sm, const uint4 (&w)[NS], int ks0,
 
 struct Split {
   bool on;
+  bool wr;  // the sequence's position and token are valid: its new K/V rows are written
   int b, s, k0, k1, pos;
 };
 
@@ -704,7 +688,7 @@ __device__ __forceinline__ void comm_role(S& sm, Ctl& c, const BArgs& a, const S
     mark(a, x, j, l, 6);
     lds_barrier();  // C1
     mark(a, x, j, l, 20);
-    for (int o = tid; o < a.B * 64; o += MKB_MERGE_ALL ? NT : CL) merge_splits(sm, a, o);
+    for (int o = tid; o < a.B * 64; o += MERGE_ALL ? NT : CL) merge_splits(sm, a, o);
     lds_barrier();  // C2
     mark(a, x, j, l, 7);
     lds_barrier();  // C3
@@ -769,13 +753,13 @@ __device__ __forceinline__ void math_role(S& sm, const BArgs& a, const Split& sp
     const uint32_t ep = (uint32_t)l + 1;
     const bool next = l + 1 < a.L;
     auto issue = [&](int p) {
-      if (MKB_GU2_AT < 0 && p == MKB_GU_AT) load_gu(wg, lw, ml, x, j);
-      if (MKB_GU2_AT >= 0 && p == MKB_GU_AT) load_gu<0, 4>(wg, lw, ml, x, j);
-      if (MKB_GU2_AT >= 0 && p == MKB_GU2_AT) load_gu<4, 8>(wg, lw, ml, x, j);
-      if (p == MKB_DN_AT) load_down(wd, lw, ml, x, j);
-      if (p == MKB_QKV_AT && next) load_qkv(wq, a.lw[l + 1], ml, x, j);
-      if (p == MKB_O_AT && next) load_o(wo, a.lw[l + 1], ml, x, j);
-      if (p == MKB_KV_AT && next && sp.on) load_kv(kw, vw, a, sp, l + 1, x, gi, t, 0);
+      if (GU2_AT < 0 && p == GU_AT) load_gu(wg, lw, ml, x, j);
+      if (GU2_AT >= 0 && p == GU_AT) load_gu<0, 4>(wg, lw, ml, x, j);
+      if (GU2_AT >= 0 && p == GU2_AT) load_gu<4, 8>(wg, lw, ml, x, j);
+      if (p == DN_AT) load_down(wd, lw, ml, x, j);
+      if (p == QKV_AT && next) load_qkv(wq, a.lw[l + 1], ml, x, j);
+      if (p == O_AT && next) load_o(wo, a.lw[l + 1], ml, x, j);
+      if (p == KV_AT && next && sp.on) load_kv(kw, vw, a, sp, l + 1, x, gi, t, 0);
     };
     lds_barrier();  // A1
     issue(0);
@@ -798,7 +782,9 @@ __device__ __forceinline__ void math_role(S& sm, const BArgs& a, const Split& sp
       }
       const uint4 knew = *reinterpret_cast<const uint4*>(&sm.kvn[0][8 * t]);
       const uint4 vnew = *reinterpret_cast<const uint4*>(&sm.kvn[1][8 * t]);
-      if (gi == 0 && sp.pos < sp.k1) {  // the split holding the new position writes its K/V rows
+      // the split holding the new position writes its K/V rows, unless the sequence's position or
+      // token was out of range: its step reports NaN and -1, and its cache stays as it was
+      if (gi == 0 && sp.pos < sp.k1 && sp.wr) {
         const size_t row = ((((size_t)sp.b * a.L + l) * HKV + x) * a.max_seq + sp.pos) * D + 8 * t;
         *reinterpret_cast<uint4*>(a.k_cache + row) = knew;
         *reinterpret_cast<uint4*>(a.v_cache + row) = vnew;
@@ -868,7 +854,7 @@ __device__ __forceinline__ void math_role(S& sm, const BArgs& a, const Split& sp
     lds_barrier();  // C1
     issue(4);
     mark(a, x, j, l, 22, 64 * NCW);
-    if (MKB_MERGE_ALL) merge_splits(sm, a, tid);
+    if (MERGE_ALL) merge_splits(sm, a, tid);
     mark(a, x, j, l, 23, 64 * NCW);
     lds_barrier();  // C2
     issue(5);
@@ -911,6 +897,7 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     sm.x = x;
     sm.j = (int)__hip_atomic_fetch_add(a.ws + W::TICK + 64 * x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sm.bad = 0;
+    sm.badseq = 0;
   }
   if (tid >= 64 && tid < 64 + BM) {
     const int b = tid - 64;
@@ -924,7 +911,10 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     if (t < 0 || t >= a.vocab) { bad = true; t = 0; }
     sm.pos[b] = p;
     sm.tok[b] = t;
-    if (bad && b < a.B) atomicOr(&sm.bad, 1);
+    if (bad && b < a.B) {
+      atomicOr(&sm.bad, 1);
+      atomicOr(&sm.badseq, 1u << b);
+    }
   }
   for (int i = tid; i < 16 * CB * KST / 8; i += NT) reinterpret_cast<uint4*>(&sm.act[0][0])[i] = make_uint4(0, 0, 0, 0);
   __syncthreads();
@@ -971,6 +961,7 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
   sp.b = __builtin_amdgcn_readfirstlane(sp.on ? sm.sb[j] : 0);
   sp.s = __builtin_amdgcn_readfirstlane(sp.on ? j - sm.f[sp.b] : 0);
   sp.pos = __builtin_amdgcn_readfirstlane(sm.pos[sp.b]);
+  sp.wr = __builtin_amdgcn_readfirstlane((sm.badseq >> sp.b) & 1u) == 0;
   sp.k0 = sp.s * __builtin_amdgcn_readfirstlane(sm.ks);
   sp.k1 = min(sp.k0 + __builtin_amdgcn_readfirstlane(sm.ks), sp.pos + 1);
   if (tid < 32) {
@@ -1000,7 +991,7 @@ __global__ void __launch_bounds__(NT, 1) batch_kernel(const BArgs a) {
     for (int cb = 0; cb < CB; ++cb) best[cb] = 0;
     const __amdgpu_buffer_rsrc_t rlm = make_rsrc(a.lm_head);
     // a tile (16 rows x H) in NC chunks of CH K steps, two chunk buffers in flight
-    constexpr int CH = MKB_LM_CH, NC = H / 32 / CH;
+    constexpr int CH = LM_CH, NC = H / 32 / CH;
     static_assert(NC >= 2 && NC % 2 == 0, "LM head chunks");
     auto load_chunk = [&](uint4 (&w)[CH], int tile, int ch) {
       const int off = ((16 * tile + li) * H + 32 * CH * ch + 8 * g) * 2;

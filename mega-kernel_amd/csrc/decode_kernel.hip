@@ -98,10 +98,7 @@ constexpr uint32_t ERR_PAGE = 8u;       // a block-table entry was out of range 
 constexpr uint32_t ERR_HOST = 16u;      // set by the host (mk_request_drain)
 constexpr uint32_t ERR_DRAIN = ERR_TIMEOUT | ERR_HOST;  // bits that make every launch drain at once
 constexpr int MAX_PAGES = 2048;     // block-table entries a paged launch may use (LDS copy)
-#ifndef MK_PF_DIST
-#define MK_PF_DIST 2
-#endif
-constexpr int PF_DIST = MK_PF_DIST;  // phases of weights each math lane keeps in flight (0..4)
+constexpr int PF_DIST = 2;  // phases of weights each math lane keeps in flight (0..4)
 static_assert(PF_DIST >= 0 && PF_DIST <= 4, "prefetch distance");
 constexpr int MAX_LAYERS = 62;  // epoch = seq << 6 | layer; 63 marks the final exchange
 
@@ -978,22 +975,16 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
   // Past the last layer the loads still issue (same count, so the wait counts stay exact) but every
   // row reads the final norm's 2-4 KB, which stays in L2: no weight traffic for a layer that never
   // runs.
-#ifndef MK_KV_PRED
-#define MK_KV_PRED (H <= 1024)
-#endif
   // K/V rows: a slot this workgroup's split does not attend to (or a workgroup without a split)
   // skips its load. The compiler then counts these two loads as possibly absent, which makes a few
   // later waits one or two loads stricter; worth it at the 0.6B shape (387 vs 395 us per token at
   // config 2), not at 1.7B (862 vs 848 at config 5, 932 vs 915 from prompt 1800).
-  constexpr bool KV_PRED = MK_KV_PRED;
-#ifndef MK_A_FIRST
-#define MK_A_FIRST 1
-#endif
+  constexpr bool KV_PRED = H <= 1024;
   // QKV register steps issued at phase D (the rest at phase E). A burst of weight loads delays every
   // exchange poll the CU issues after it until the burst has drained (~1.3 us for all QKV rows
   // chip-wide), so the QKV burst is split between the D and E hops, each of which it fits. Measured
   // on MI355X at config 2: 381 -> 365 us per token.
-  constexpr int A_FIRST = MK_A_FIRST < TA::PS ? (MK_A_FIRST < 1 ? 1 : MK_A_FIRST) : TA::PS;
+  constexpr int A_FIRST = TA::PS > 1 ? 1 : TA::PS;
 
   auto load_phase = [&](auto qc, int layer) {
     constexpr int Q = decltype(qc)::value;
@@ -1566,18 +1557,25 @@ __global__ void placement_probe(uint32_t* out) {
 }
 
 constexpr int MAX_DEVICES = 64;
-constexpr int MAX_STREAMS = 64;  // workspace sets per device (one per stream that launches)
+// Workspace sets per device, one per stream that launches. A stream beyond this many takes over the
+// set used least recently, after a device synchronization (so no launch can still be using it); the
+// set's status bits are kept in the device's retired status.
+constexpr int MAX_STREAMS = 64;
 
 struct Workspace {
   hipStream_t stream;
   void* ws;
+  uint64_t last_use;  // launch counter value at the set's last launch
 };
 struct DeviceState {
   bool init = false;
   hipError_t err = hipSuccess;  // why the device cannot run the kernel, if it cannot
   bool cooperative = false;     // launch mode, see launch()
   bool force_wt = false;        // placement b % 8 not confirmed: exchanges write through
+  bool drain_pending = false;   // mk_request_drain was called and mk_reset has not been since
+  uint32_t retired_status = 0;  // status bits of workspace sets handed to another stream
   int nws = 0;
+  uint64_t launches = 0;
   Workspace ws[MAX_STREAMS];
   uint64_t* trace = nullptr;    // set by mk_set_trace; null in normal operation
 };
@@ -1663,20 +1661,49 @@ static hipError_t device_state(DeviceState** out) {
   return hipSuccess;
 }
 
+// A newly initialised workspace set starts drained while a drain is pending (mk_request_drain).
+static hipError_t mark_if_draining(bool drain_pending, void* ws, hipStream_t stream) {
+  if (!drain_pending) return hipSuccess;
+  hipLaunchKernelGGL(ws_raise_kernel, dim3(1), dim3(64), 0, stream, static_cast<u64*>(ws), ERR_HOST);
+  return hipGetLastError();
+}
+
 // The workspace set of `stream` on the current device, allocated and initialised on the stream's
-// first launch. Launches on different streams never share exchange words or epochs.
+// first launch. Launches on different streams never share exchange words or epochs. With every slot
+// taken, the least recently used set is handed over: the device is synchronized first (no launch on
+// any stream can still use it), its status bits are kept, and it is initialised again on `stream`.
 static hipError_t stream_workspace(DeviceState* st, hipStream_t stream, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
+  const uint64_t now = ++st->launches;
   for (int i = 0; i < st->nws; ++i)
-    if (st->ws[i].stream == stream) { *out = st->ws[i].ws; return hipSuccess; }
-  if (st->nws == MAX_STREAMS) return hipErrorNotSupported;
-  void* ws = nullptr;
-  hipError_t e = hipMalloc(&ws, WS_SET_BYTES);
-  if (e != hipSuccess) return e;
+    if (st->ws[i].stream == stream) { st->ws[i].last_use = now; *out = st->ws[i].ws; return hipSuccess; }
+  hipError_t e;
   bool placement_ok = false;
+  if (st->nws == MAX_STREAMS) {
+    int v = 0;
+    for (int i = 1; i < st->nws; ++i)
+      if (st->ws[i].last_use < st->ws[v].last_use) v = i;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    for (int i = 0; i < NSHAPE; ++i) {
+      uint32_t w = 0;
+      if ((e = hipMemcpy(&w, (char*)st->ws[v].ws + i * WS_BYTES + X_STATUS * 8, 4, hipMemcpyDeviceToHost)) != hipSuccess)
+        return e;
+      st->retired_status |= w;
+    }
+    if ((e = init_workspace(st->ws[v].ws, stream, &placement_ok)) != hipSuccess) return e;
+    if ((e = mark_if_draining(st->drain_pending, st->ws[v].ws, stream)) != hipSuccess) return e;
+    if (!placement_ok) st->force_wt = true;
+    st->ws[v].stream = stream;
+    st->ws[v].last_use = now;
+    *out = st->ws[v].ws;
+    return hipSuccess;
+  }
+  void* ws = nullptr;
+  if ((e = hipMalloc(&ws, WS_SET_BYTES)) != hipSuccess) return e;
   if ((e = init_workspace(ws, stream, &placement_ok)) != hipSuccess) { (void)hipFree(ws); return e; }
+  if ((e = mark_if_draining(st->drain_pending, ws, stream)) != hipSuccess) { (void)hipFree(ws); return e; }
   if (!placement_ok) st->force_wt = true;
-  st->ws[st->nws++] = {stream, ws};
+  st->ws[st->nws++] = {stream, ws, now};
   *out = ws;
   return hipSuccess;
 }
@@ -1696,6 +1723,7 @@ static hipError_t static_workspace(hipStream_t stream, void** out, bool* force_w
     if (s.err == hipSuccess && s.ptr == nullptr) s.err = hipErrorInvalidSymbol;
     bool placement_ok = false;
     if (s.err == hipSuccess) s.err = init_workspace(s.ptr, stream, &placement_ok);
+    if (s.err == hipSuccess) s.err = mark_if_draining(g_dev[dev].drain_pending, s.ptr, stream);
     s.force_wt = !placement_ok;
   }
   if (s.err != hipSuccess) return s.err;
@@ -1939,6 +1967,12 @@ extern "C" hipError_t mk_status(uint32_t* status) {
     return hipSuccess;
   });
   if (e != hipSuccess) return e;
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    acc |= st->retired_status;
+  }
   *status = acc;
   return hipSuccess;
 }
@@ -1947,6 +1981,13 @@ extern "C" hipError_t mk_reset(void) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
   mkb_set_drain(false);
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    st->drain_pending = false;
+    st->retired_status = 0;
+  }
   e = for_each_workspace([](void* ws) {
     hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, 0, static_cast<u64*>(ws));
     return hipGetLastError();
@@ -1959,6 +2000,12 @@ extern "C" hipError_t mk_request_drain(void) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return e;
   mkb_set_drain(true);
+  DeviceState* st = nullptr;
+  if ((e = device_state(&st)) != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    st->drain_pending = true;  // workspace sets created from now on start drained too
+  }
   e = for_each_workspace([](void* ws) {
     hipLaunchKernelGGL(ws_raise_kernel, dim3(1), dim3(64), 0, 0, static_cast<u64*>(ws), ERR_HOST);
     return hipGetLastError();

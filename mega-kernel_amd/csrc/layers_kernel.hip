@@ -1072,6 +1072,7 @@ __device__ __forceinline__ void battn_split(const float (&qa)[8], const float (&
 // position from registers. Workgroup x takes splits x, x + gridDim.x, ... of [0, position] (the grid
 // does not depend on the device-side positions); the merge reads splits below ceil(ctx / KS) only.
 __global__ void __launch_bounds__(256) battn_partial_kernel(const float* raw, const int32_t* positions,
+                                                            const int32_t* tokens, int vocab,
                                                             const uint16_t* q_norm, const uint16_t* k_norm,
                                                             const uint16_t* cos_tab, const uint16_t* sin_tab,
                                                             uint16_t* k_cache, uint16_t* v_cache, int L, int layer,
@@ -1081,6 +1082,9 @@ __global__ void __launch_bounds__(256) battn_partial_kernel(const float* raw, co
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, t = lane & 15;
   const int pos = seq_pos(positions, b, max_seq, threadIdx.x == 0 && blockIdx.x == 0 && kvh == 0 ? bad : nullptr);
+  // a sequence whose position or token is out of range reports NaN and -1 and keeps its cache as it
+  // was: its new K/V rows are not written (the clamped position would overwrite a valid row)
+  const bool write_ok = positions[b] == pos && tokens[b] >= 0 && tokens[b] < vocab;
   const int ctx = pos + 1;
   if ((int)blockIdx.x * KS >= ctx) return;  // no split for this workgroup (the grid fits the longest cache)
   // the first split's K/V rows are in flight while the new row's projections are finished
@@ -1107,7 +1111,7 @@ __global__ void __launch_bounds__(256) battn_partial_kernel(const float* raw, co
                                 pack_bf16x2(kn[6], kn[7]));
   const uint4 vnew = make_uint4(pack_bf16x2(vv[0], vv[1]), pack_bf16x2(vv[2], vv[3]), pack_bf16x2(vv[4], vv[5]),
                                 pack_bf16x2(vv[6], vv[7]));
-  if (threadIdx.x < 16 && (pos / KS) % gridDim.x == blockIdx.x) {
+  if (write_ok && threadIdx.x < 16 && (pos / KS) % gridDim.x == blockIdx.x) {
     const size_t row = ((((size_t)b * L + layer) * HKV + kvh) * max_seq + pos) * D + 8 * t;
     *reinterpret_cast<uint4*>(k_cache + row) = knew;
     *reinterpret_cast<uint4*>(v_cache + row) = vnew;
@@ -1473,8 +1477,8 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
     if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st)) != hipSuccess) return e;
-    MKB_LAUNCH(battn_partial_kernel, dim3(S < gx ? S : gx, HKV, B), dim3(256), 0, st, raw, positions,
-               (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
+    MKB_LAUNCH(battn_partial_kernel, dim3(S < gx ? S : gx, HKV, B), dim3(256), 0, st, raw, positions, tokens,
+               dims.vocab, (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
                v_cache, L, l, max_seq, apart, S, bad);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
     SkArgs o{};

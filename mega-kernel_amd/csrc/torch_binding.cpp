@@ -34,15 +34,22 @@ constexpr int kHeadDim = 128, kQHeads = 16, kKVHeads = 8;
     TORCH_CHECK(e_ == hipSuccess, "megakernel: ", #expr, " failed: ", hipGetErrorString(e_)); \
   } while (0)
 
-// Device-resident LayerWeights table, rebuilt only when the weight tensors change. Holds
-// references to the tensors so the cached pointers cannot dangle.
+// Device-resident LayerWeights tables, one per weight set (the 11 * L tensors' data pointers), so
+// that sessions alternating between weight sets (e.g. two models) reuse their tables instead of
+// rebuilding one on every switch. Each entry holds references to its tensors so the cached pointers
+// cannot dangle. Up to kTablesPerDevice sets per device; beyond that the least recently used entry
+// is dropped (and its tensors released).
 struct TableCache {
   std::vector<torch::Tensor> held;
   std::vector<const void*> ptrs;
   torch::Tensor table;  // uint8 on device, num_layers * sizeof(mk_layer_weights)
+  uint64_t last_use = 0;
 };
+constexpr size_t kTablesPerDevice = 8;
 std::mutex g_mu;
-std::vector<TableCache> g_tables(64);
+std::vector<std::vector<TableCache>> g_tables(64);
+uint64_t g_table_clock = 0;
+int64_t g_tables_built = 0;
 
 void check_bf16(const torch::Tensor& t, const char* name, at::IntArrayRef shape, const torch::Device& dev) {
   TORCH_CHECK(t.defined(), "megakernel: ", name, " is undefined");
@@ -115,10 +122,14 @@ const void* device_table(const std::vector<torch::Tensor>& lw, const torch::Devi
   std::lock_guard<std::mutex> lk(g_mu);
   const int idx = dev.index() < 0 ? 0 : dev.index();
   TORCH_CHECK(idx < (int)g_tables.size(), "megakernel: device index too large");
-  TableCache& tc = g_tables[idx];
+  std::vector<TableCache>& cache = g_tables[idx];
   std::vector<const void*> ptrs(lw.size());
   for (size_t i = 0; i < lw.size(); ++i) ptrs[i] = lw[i].data_ptr();
-  if (tc.table.defined() && ptrs == tc.ptrs) return tc.table.data_ptr();
+  for (TableCache& tc : cache)
+    if (tc.ptrs == ptrs) {
+      tc.last_use = ++g_table_clock;
+      return tc.table.data_ptr();
+    }
   const int64_t L = lw.size() / kPerLayer;
   auto host = torch::empty({L * (int64_t)sizeof(mk_layer_weights)}, torch::dtype(torch::kUInt8).pinned_memory(true));
   auto* h = reinterpret_cast<mk_layer_weights*>(host.data_ptr());
@@ -129,10 +140,31 @@ const void* device_table(const std::vector<torch::Tensor>& lw, const torch::Devi
   auto table = torch::empty({host.numel()}, torch::dtype(torch::kUInt8).device(dev));
   MK_HIP_CHECK(hipMemcpyAsync(table.data_ptr(), host.data_ptr(), host.numel(), hipMemcpyHostToDevice, stream));
   MK_HIP_CHECK(hipStreamSynchronize(stream));  // once per new weight set; keeps `host` alive until copied
-  tc.held = lw;
-  tc.ptrs = std::move(ptrs);
-  tc.table = table;
-  return tc.table.data_ptr();
+  TableCache* slot = nullptr;
+  if (cache.size() < kTablesPerDevice) {
+    cache.emplace_back();
+    slot = &cache.back();
+  } else {
+    // the least recently used set; after a device synchronization no launch on any stream still
+    // reads its device table, which can then be released
+    MK_HIP_CHECK(hipDeviceSynchronize());
+    slot = &cache[0];
+    for (TableCache& tc : cache)
+      if (tc.last_use < slot->last_use) slot = &tc;
+  }
+  slot->held = lw;
+  slot->ptrs = std::move(ptrs);
+  slot->table = table;
+  slot->last_use = ++g_table_clock;
+  ++g_tables_built;
+  return slot->table.data_ptr();
+}
+
+// Weight tables built so far by this process (all devices): a test hook showing that alternating
+// weight sets reuses their tables.
+int64_t weight_tables_built() {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_tables_built;
 }
 
 std::tuple<torch::Tensor, torch::Tensor> run(int64_t token_id, torch::Tensor embed, torch::Tensor lm_head,
@@ -419,7 +451,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "batched decode of B <= 64 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
         "returns (fp32 logits [B, V], int32 greedy tokens [B] on device)");
   m.def("set_batch_engine", &set_batch_engine,
-        "engine of decode_batch: 0 automatic (the persistent kernel for <= 8 sequences of the 0.6B shape), "
+        "engine of decode_batch: 0 automatic (the persistent kernel for <= 16 sequences of the 0.6B shape), "
         "1 layer by layer, 2 persistent where it applies");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
@@ -429,4 +461,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("set_launch_mode", &set_launch_mode, "0 = plain launch (default), 1 = cooperative launch, on the current device");
   m.def("check_args", &check_args, "validate decode's arguments without launching; returns (hidden, intermediate, layers, vocab)");
   m.def("version", []() { return std::string(mk_version()); });
+  m.def("weight_tables_built", &weight_tables_built,
+        "LayerWeights tables the operator has built so far (one per distinct weight set while it stays cached)");
 }

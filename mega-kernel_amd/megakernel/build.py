@@ -78,20 +78,11 @@ def build_bench(verbose=True):
     return out
 
 
-def build_probe(verbose=True):
-    """``exchange_probe``: exchange-latency floors of the MI355X (standalone, no library)."""
-    out = os.path.join(PKG_ROOT, "exchange_probe")
-    _run([_hipcc(), *HIP_FLAGS, os.path.join(CSRC, "exchange_probe.hip"), "-o", out + ".tmp"], verbose)
-    os.replace(out + ".tmp", out)
-    return out
-
-
 def build(verbose=True):
     """Compile every artefact (always; this is the build check)."""
     build_library(verbose)
     build_extension(verbose)
     build_bench(verbose)
-    build_probe(verbose)
 
 
 if __name__ == "__main__":

@@ -49,7 +49,11 @@ def build_model(shape, max_positions, seed=0):
     return Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
 
 
-def main(argv=None):
+def run(argv=None, keep_prefill_cache=False):
+    """Runs the driver and returns what it did: the generated tokens (the prefill's greedy token
+    first), the prompt length, the device status after the loop, ms per token, and, with
+    ``keep_prefill_cache``, a copy of the K/V cache as the prefill left it together with the decode
+    operator's other inputs (so a caller can replay the decode from the same state)."""
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shape", default="qwen3-0.6b", choices=sorted(SHAPES))
     ap.add_argument("--prompt", type=int, default=32, help="random prompt length (token ids, seed 1)")
@@ -57,7 +61,8 @@ def main(argv=None):
     ap.add_argument("--new", type=int, default=64, help="tokens to generate")
     ap.add_argument("--device-loop", action="store_true", help="generate with one decode_steps call")
     ap.add_argument("--native-prefill", action="store_true",
-                    help="fill the cache with decode_steps over the prompt instead of the Transformers prefill")
+                    help="fill the cache with the batched prefill kernel (prefill) instead of the Transformers "
+                         "prefill and cache copy")
     a = ap.parse_args(argv)
     import torch
     import megakernel
@@ -86,6 +91,11 @@ def main(argv=None):
             out = model(ids, use_cache=True)
         position = megakernel.copy_prefill_cache(out.past_key_values, k_cache, v_cache)
         token = int(out.logits[0, -1].float().argmax())
+    result = {"prompt": position, "first_token": token}
+    if keep_prefill_cache:
+        result["prefill_cache"] = (k_cache.clone(), v_cache.clone())
+        result["inputs"] = {"embed": embed, "final_norm": final_norm, "layer_weights": layer_weights, "cos": cos,
+                            "sin": sin, "max_seq": a.max_seq}
 
     generated = [token]
     steps = min(a.new, a.max_seq - position)
@@ -110,9 +120,17 @@ def main(argv=None):
     if a.device_loop and steps > 1:
         generated = tokens.tolist()
     n = max(steps - 1, 1)
+    result.update(generated=generated, status=kernel.status(), ms_per_token=start.elapsed_time(end) / n)
     print(f"generated {len(generated)} tokens: {generated[:16]}{' ...' if len(generated) > 16 else ''}")
-    print(f"decode: {start.elapsed_time(end) / n:.3f} ms/token (device events), {n / wall:.1f} tokens/s wall, "
-          f"device status {kernel.status()}")
+    print(f"decode: {result['ms_per_token']:.3f} ms/token (device events), {n / wall:.1f} tokens/s wall, "
+          f"device status {result['status']}")
+    return result
+
+
+def main(argv=None):
+    """The command line: 0 when the device status is clean and every generated token is valid."""
+    r = run(argv)
+    return 0 if r["status"] == 0 and all(t >= 0 for t in r["generated"]) else 1
 
 
 if __name__ == "__main__":

@@ -99,3 +99,28 @@ def stats(ours, ref):
     ours, ref = ours.double(), ref.double()
     cos = torch.nn.functional.cosine_similarity(ours, ref, dim=0).item()
     return (ours - ref).abs().max().item(), cos
+
+
+def parity_dir():
+    """Where the parity tests leave their per-config records: ``$MK_PARITY_DIR``, else
+    ``gpurun_out/parity`` under the repository root."""
+    import os
+    d = os.environ.get("MK_PARITY_DIR") or os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                                       "gpurun_out", "parity")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def write_record(name, rec):
+    """One parity record as JSON (``<name>.json`` in ``parity_dir()``), with the kernel version and
+    the GPU it ran on, so that a summary can be rebuilt from the files alone."""
+    import json
+    import os
+    import megakernel
+    out = dict(rec)
+    out["kernel_version"] = megakernel.load().version()
+    out["device"] = torch.cuda.get_device_name(0) if torch.cuda.is_available() else None
+    path = os.path.join(parity_dir(), f"{name}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    return path

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import hf, restate
-from tests.gpu_common import DEV, Session, c_library, stats, stream_handle, Dims
+from tests.gpu_common import DEV, Session, c_library, stats, stream_handle, Dims, write_record
 
 pytestmark = pytest.mark.gpu
 
@@ -573,6 +573,32 @@ def _merge(recs):
     return out
 
 
+def _record(rec, name, workload):
+    """Writes the per-config parity record (tokens, max-abs, cosine, tight check, north-star values)
+    next to the other parity records, before the gates are asserted, so a failing run leaves it too."""
+    n = rec["steps"]
+    summary = {
+        "workload": workload, "steps": n,
+        "tokens_equal_transformers": {"kernel": rec["k_agree"], "oracle": rec["o_agree"]},
+        "tokens_kernel_equal_oracle": rec["k_o_same"],
+        "max_abs_vs_transformers": {"kernel": max(rec["k_abs"]), "oracle": max(rec["o_abs"])},
+        "min_cos_vs_transformers": {"kernel": min(rec["k_cos"]), "oracle": min(rec["o_cos"])},
+        "mean_cos_vs_transformers": {"kernel": sum(rec["k_cos"]) / n, "oracle": sum(rec["o_cos"]) / n},
+        "max_rel_kernel_vs_oracle": max(rec["k_o_rel"]),
+        "tight": {"steps": rec["tight_steps"], "tokens_same": rec["tight_same"], "max_abs": rec["tight_abs"]},
+        "north_star": {"tokens": NS_TOKENS, "max_abs": NS_MAXABS, "cos": NS_COS},
+        "north_star_met": {
+            who: {"tokens": rec[f"{k}_agree"] >= math.ceil(NS_TOKENS * n),
+                  "max_abs": max(rec[f"{k}_abs"]) <= NS_MAXABS,
+                  "cos": min(rec[f"{k}_cos"]) >= NS_COS}
+            for who, k in (("kernel", "k"), ("oracle", "o"))},
+        "per_step": {k: rec[k] for k in ("k_cos", "o_cos", "k_abs", "o_abs", "k_o_rel")},
+    }
+    path = write_record(name, summary)
+    print(f"[{name}] parity record: {path}", flush=True)
+    return rec
+
+
 def _assert_parity(rec):
     """The gates every BASELINE config passes.
 
@@ -607,20 +633,24 @@ def _assert_parity(rec):
 def test_qwen06_config1_one_step(q06):
     """prompt 64, cache 512, one greedy step -- logits and argmax against
     Transformers, with the same-run fp32-oracle floor."""
-    _assert_parity(_parity_run(q06, 64, 1, 1, "config1"))
+    _assert_parity(_record(_parity_run(q06, 64, 1, 1, "config1"), "decode_config1",
+                           "qwen3-0.6b, prompt 64, cache 512, 1 greedy step"))
 
 
 def test_qwen06_config2_teacher_forced(q06):
     """prompt 32, cache 512, 256 teacher-forced steps (ctx 33-288; past 256 the
     launches hold two K/V rows per group in registers). Tight check on every 4th step."""
-    _assert_parity(_parity_run(q06, 32, 256, 4, "config2"))
+    _assert_parity(_record(_parity_run(q06, 32, 256, 4, "config2"), "decode_config2",
+                           "qwen3-0.6b, prompt 32, cache 512, 256 teacher-forced steps"))
 
 
 def test_qwen06_config3_prompt_sweep(q06):
     """Config 3: prompts of 16, 128, 256 and 480 tokens, cache 512, 32 teacher-forced steps each --
     the attention split count S = min(ceil(ctx / 32), 8) runs from 1 to 8 and the last step writes the
     cache's final slot (position 511). Gates pooled over the 128 steps."""
-    _assert_parity(_merge([_parity_run(q06, P, 32, 8, "config3") for P in (16, 128, 256, 480)]))
+    _assert_parity(_record(_merge([_parity_run(q06, P, 32, 8, "config3") for P in (16, 128, 256, 480)]),
+                           "decode_config3", "qwen3-0.6b, prompts 16/128/256/480, cache 512, 32 teacher-forced "
+                           "steps each (pooled)"))
 
 
 @pytest.fixture(scope="module")
@@ -632,13 +662,15 @@ def test_qwen06_config4_long_context(q06_4k):
     """Config 4: prompt 3584, cache 4096, 256 teacher-forced steps (ctx 3585-3840): 16 attention
     splits of ~230 keys merged in two poll rounds, most keys streamed inside the attention phase
     rather than held in registers. Tight check on every 32nd step."""
-    _assert_parity(_parity_run(q06_4k, 3584, 256, 32, "config4"))
+    _assert_parity(_record(_parity_run(q06_4k, 3584, 256, 32, "config4"), "decode_config4",
+                           "qwen3-0.6b, prompt 3584, cache 4096, 256 teacher-forced steps"))
 
 
 def test_qwen17_config5():
     """Config 5: the Qwen3-1.7B shape (H 2048, I 6144, 28 layers, full vocabulary), prompt 512,
     cache 2048, 256 teacher-forced steps; tight check on every 8th step."""
-    _assert_parity(_parity_run(Session("qwen3-1.7b", 2048), 512, 256, 8, "config5"))
+    _assert_parity(_record(_parity_run(Session("qwen3-1.7b", 2048), 512, 256, 8, "config5"), "decode_config5",
+                           "qwen3-1.7b, prompt 512, cache 2048, 256 teacher-forced steps"))
 
 
 def test_launch_modes_agree(mini):
@@ -676,4 +708,52 @@ def test_two_streams_have_separate_workspaces(mini):
             got = mini.decode(tok, kb, vb, P)
         s.synchronize()
         assert torch.equal(got, want)
+    assert mini.kernel.status() == 0
+
+
+def test_more_streams_than_workspace_sets(mini):
+    """A device keeps 64 exchange-workspace sets; the 65th and later launching streams take over the
+    least recently used set (after a device synchronization). 70 streams in turn, and the default
+    stream again, all give the default stream's result bit for bit, with a clean status."""
+    P = 40
+    _, last, _, kc, vc = mini.prefill(P)
+    tok = int(last.float().argmax())
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    want = mini.decode(tok, kd, vd, P)
+    torch.cuda.synchronize()
+    streams = []
+    for i in range(70):
+        s = torch.cuda.Stream()
+        streams.append(s)  # kept alive, so every stream is a distinct handle
+        with torch.cuda.stream(s):
+            kb, vb = kc.to(DEV), vc.to(DEV)
+            got = mini.decode(tok, kb, vb, P)
+        s.synchronize()
+        assert torch.equal(got, want), f"stream {i}"
+    kb, vb = kc.to(DEV), vc.to(DEV)
+    assert torch.equal(mini.decode(tok, kb, vb, P), want)
+    assert mini.kernel.status() == 0
+
+
+def test_alternating_weight_sets_reuse_their_tables(mini):
+    """The operator caches one device LayerWeights table per weight set: decoding alternately with two
+    weight sets (two copies of the model on the device) builds each table once, and each set's result
+    is unchanged by the other's calls."""
+    other = [t.clone() for t in mini.layers]
+    P = 30
+    _, last, _, kc, vc = mini.prefill(P)
+    tok = int(last.float().argmax())
+    args = lambda lw, kd, vd: (tok, mini.embed, mini.lm_head, mini.final_norm, lw, mini.cos, mini.sin, kd, vd, P,
+                               mini.max_seq)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    want = mini.kernel.decode(*args(mini.layers, kd, vd))
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    mini.kernel.decode(*args(other, kd, vd))  # the second set's table
+    built = mini.kernel.weight_tables_built()
+    for _ in range(3):
+        for lw in (mini.layers, other):
+            kd, vd = kc.to(DEV), vc.to(DEV)
+            got = mini.kernel.decode(*args(lw, kd, vd))
+            assert torch.equal(got, want)  # identical values in both sets
+    assert mini.kernel.weight_tables_built() == built, "a cached weight table was rebuilt"
     assert mini.kernel.status() == 0

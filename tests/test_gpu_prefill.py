@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import hf, restate
-from tests.gpu_common import DEV, Session, stats
+from tests.gpu_common import DEV, Session, stats, write_record
 
 pytestmark = pytest.mark.gpu
 
@@ -183,6 +183,16 @@ def test_prefill_baseline_prompts_against_transformers(shape_name, P, max_seq):
           f"{om:.3e} cos {oc:.8f}; tokens kernel {int(tok.item())} oracle {restate.argmax_bf16(want)} "
           f"Transformers {int(r.argmax())}", flush=True)
     rel = ((got.double() - want.double()).norm() / want.double().norm()).item()
+    write_record(f"prefill_{shape_name}_p{P}", {
+        "workload": f"{shape_name}, prompt {P}, cache {max_seq}: native prefill", "prefill_ms": ms,
+        "tight": {"max_abs": maxabs, "token_kernel": int(tok.item()), "token_oracle": restate.argmax_bf16(want)},
+        "last_logits_vs_transformers": {"kernel": {"max_abs": km, "cos": kc}, "oracle": {"max_abs": om, "cos": oc}},
+        "tokens": {"kernel": int(tok.item()), "oracle": restate.argmax_bf16(want), "transformers": int(r.argmax())},
+        "rel_kernel_vs_oracle": rel,
+        "mean_abs_cache_vs_transformers_per_layer": {
+            "k": {"kernel": _layer_dist(kcpu, kh, P).tolist(), "oracle": _layer_dist(kw, kh, P).tolist()},
+            "v": {"kernel": _layer_dist(vcpu, vh, P).tolist(), "oracle": _layer_dist(vw, vh, P).tolist()}},
+    })
     assert km <= om + 1e-3
     assert kc >= oc - (rel * (1.0 - oc * oc) ** 0.5 + rel * rel)  # the per-step bound of the decode tests
     if restate.argmax_bf16(want) == int(r.argmax()):
