@@ -1078,62 +1078,88 @@ __device__ __forceinline__ void math_role(const KArgs& a, Smem<H, I>& sm, const 
     lds_barrier();  // (A2) comm: q, new K/V in LDS
     mark(a, tl + T_M_B_START, 64);
 
-    // B: split-K attention; this phase's loads are issued after it, off the attention's path
-    if (att) attention_split<H, I, NKV>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
-    // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
-    // issued only after this workgroup's attention partial is published: neither the attention nor
-    // the publish queues behind them.
-    mark(a, tl + T_M_B_END, 64);
-    lds_barrier();  // (B1) every group's partial in sm.gq
-    {
-      // Merge the 32 group partials and publish this split's: wave mw takes head mw / 4, dims
-      // 32 (mw % 4) .. +32. Lane = (subset sub of 4 groups, dim quad q4): each lane merges its 4
-      // groups for 4 dims, then the 8 subsets combine across lanes (xor 8, 16, 32) with a common
-      // max. Lanes 0-7 publish the head's 32 dims; lane 0 of waves 0 and 4 its (m, l).
-      // A workgroup without a split publishes zeros into its slot: every exchange word is written
-      // at every layer, which is what keeps a stale word's epoch from ever matching (the epochs
-      // of consecutive writes of a word are then 1 to 64 apart, never equal mod 255).
-      const int h = mw >> 2, sub = lane >> 3, d0 = 32 * (mw & 3) + 4 * (lane & 7);
-      float M = 0.f, Ls = 0.f;
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      if (att) {
-        float m[4], l[4];
-        float4 p[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float2 ml = *reinterpret_cast<const float2*>(&sm.gq[4 * sub + k][h][D]);
-          m[k] = ml.x; l[k] = ml.y;
-          p[k] = *reinterpret_cast<const float4*>(&sm.gq[4 * sub + k][h][d0]);
-        }
-        M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
-        M = fmaxf(M, dpp<0x128>(M));  // row_ror:8 == lane ^ 8 inside a 16-lane row
-        M = xmax32(xmax16(M));        // every split has a key, so M is finite
-        mark(a, tl + T_B_MAX, 64);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float f = __expf(m[k] - M);  // 0 for a group without keys
-          Ls = fmaf(l[k], f, Ls);
-          acc[0] = fmaf(p[k].x, f, acc[0]); acc[1] = fmaf(p[k].y, f, acc[1]);
-          acc[2] = fmaf(p[k].z, f, acc[2]); acc[3] = fmaf(p[k].w, f, acc[3]);
-        }
-        auto sub_sum = [](float v) { v += dpp<0x128>(v); return xsum32(xsum16(v)); };
-        Ls = sub_sum(Ls);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = sub_sum(acc[i]);
+    if (G::SMALL && !att) {
+      // B on a workgroup without an attention split (0.6B width): its gate/up rows (phase B + DIST)
+      // are issued right away, once its QKV rows are out (A1), so that the burst (48 KB per CU) has
+      // mostly drained by the time the split partials it polls for next are published. It publishes
+      // zeros into its split slot (every exchange word is written at every layer, see below).
+      // Measured on MI355X (mk_bench, against issuing them after B3 as below): config 2 -3 us per
+      // token, prompt 3584 -8 us; at the 2048 width +2.4 us, so there every workgroup takes the
+      // single path below.
+      issue_ahead(I1(), layer);
+      mark(a, tl + T_M_B_END, 64);
+      lds_barrier();  // (B1)
+      {
+        Comm c;
+        c.wt = sm.wt != 0;
+        const uint32_t ep = ll_epoch(sm.seq, layer);
+        uint32_t* att_x = reinterpret_cast<uint32_t*>(a.xw) + W_ATT + (size_t)xcd * WPX * APW + (size_t)j * APW;
+        const int h = mw >> 2, d0 = 32 * (mw & 3) + 4 * (lane & 7);
+        const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+        if (lane < 8) ll_store<4>(c, att_x, h * D + d0, zero, ep, false);
+        if (lane == 0 && (mw & 3) == 0) ll_store<2>(c, att_x, 2 * D + 2 * h, zero, ep, false);
       }
-      Comm c;
-      c.wt = sm.wt != 0;
-      const uint32_t ep = ll_epoch(sm.seq, layer);
-      uint32_t* att_x = reinterpret_cast<uint32_t*>(a.xw) + W_ATT + (size_t)xcd * WPX * APW + (size_t)j * APW;
-      const float ml[2] = {M, Ls};
-      if (lane < 8) ll_store<4>(c, att_x, h * D + d0, acc, ep, false);
-      if (lane == 0 && (mw & 3) == 0) ll_store<2>(c, att_x, 2 * D + 2 * h, ml, ep, false);
-      if (att) mark(a, tl + T_B_PUB, 64);
+      lds_barrier();  // (B3)
+      mark(a, tl + T_M_B_ISSUED, 64);
+      lds_barrier();  // (B2) comm: attention output in x[0, 256)
+    } else {
+      // B: split-K attention; this phase's loads are issued after it, off the attention's path
+      if (att) attention_split<H, I, NKV>(a, sm, st, ad, layer, mw, lane, kK, kV, tl);
+      // This phase's loads (phase B + DIST) occupy the CU's memory pipeline for a while, so they are
+      // issued only after this workgroup's attention partial is published: neither the attention nor
+      // the publish queues behind them.
+      mark(a, tl + T_M_B_END, 64);
+      lds_barrier();  // (B1) every group's partial in sm.gq
+      {
+        // Merge the 32 group partials and publish this split's: wave mw takes head mw / 4, dims
+        // 32 (mw % 4) .. +32. Lane = (subset sub of 4 groups, dim quad q4): each lane merges its 4
+        // groups for 4 dims, then the 8 subsets combine across lanes (xor 8, 16, 32) with a common
+        // max. Lanes 0-7 publish the head's 32 dims; lane 0 of waves 0 and 4 its (m, l).
+        // A workgroup without a split publishes zeros into its slot: every exchange word is written
+        // at every layer, which is what keeps a stale word's epoch from ever matching (the epochs
+        // of consecutive writes of a word are then 1 to 64 apart, never equal mod 255).
+        const int h = mw >> 2, sub = lane >> 3, d0 = 32 * (mw & 3) + 4 * (lane & 7);
+        float M = 0.f, Ls = 0.f;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (att) {
+          float m[4], l[4];
+          float4 p[4];
+  #pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float2 ml = *reinterpret_cast<const float2*>(&sm.gq[4 * sub + k][h][D]);
+            m[k] = ml.x; l[k] = ml.y;
+            p[k] = *reinterpret_cast<const float4*>(&sm.gq[4 * sub + k][h][d0]);
+          }
+          M = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+          M = fmaxf(M, dpp<0x128>(M));  // row_ror:8 == lane ^ 8 inside a 16-lane row
+          M = xmax32(xmax16(M));        // every split has a key, so M is finite
+          mark(a, tl + T_B_MAX, 64);
+  #pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float f = __expf(m[k] - M);  // 0 for a group without keys
+            Ls = fmaf(l[k], f, Ls);
+            acc[0] = fmaf(p[k].x, f, acc[0]); acc[1] = fmaf(p[k].y, f, acc[1]);
+            acc[2] = fmaf(p[k].z, f, acc[2]); acc[3] = fmaf(p[k].w, f, acc[3]);
+          }
+          auto sub_sum = [](float v) { v += dpp<0x128>(v); return xsum32(xsum16(v)); };
+          Ls = sub_sum(Ls);
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = sub_sum(acc[i]);
+        }
+        Comm c;
+        c.wt = sm.wt != 0;
+        const uint32_t ep = ll_epoch(sm.seq, layer);
+        uint32_t* att_x = reinterpret_cast<uint32_t*>(a.xw) + W_ATT + (size_t)xcd * WPX * APW + (size_t)j * APW;
+        const float ml[2] = {M, Ls};
+        if (lane < 8) ll_store<4>(c, att_x, h * D + d0, acc, ep, false);
+        if (lane == 0 && (mw & 3) == 0) ll_store<2>(c, att_x, 2 * D + 2 * h, ml, ep, false);
+        if (att) mark(a, tl + T_B_PUB, 64);
+      }
+      lds_barrier();  // (B3) every wave's share of the partial is out before the loads below
+      issue_ahead(I1(), layer);
+      mark(a, tl + T_M_B_ISSUED, 64);
+      lds_barrier();  // (B2) comm: attention output in x[0, 256)
     }
-    lds_barrier();  // (B3) every wave's share of the partial is out before the loads below
-    issue_ahead(I1(), layer);
-    mark(a, tl + T_M_B_ISSUED, 64);
-    lds_barrier();  // (B2) comm: attention output in x[0, 256)
 
     // C: o_proj partial over this group's 256 columns
     issue_ahead(I2(), layer);
@@ -2041,4 +2067,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.21 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure; prefill GEMMs on fragment-major activations)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.22 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, gate/up rows early on split-free workgroups, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure; prefill GEMMs on fragment-major activations)"; }
