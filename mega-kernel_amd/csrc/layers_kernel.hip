@@ -761,6 +761,32 @@ struct SkArgs {
   int ldm;
 };
 
+// Activation operand of the skinny products in fragment order ("skinny fragments", used by the
+// batched decode): for column block cb (sequences 8 cb .. 8 cb + 7) and K block kb (32 inputs), one
+// 1 KB fragment holding, at lane l, MFMA column li = l % 16 (sequence 8 cb + li / 2, bf16 hi part for
+// even li, lo for odd) and inputs 32 kb + 8 (l / 16) .. + 8. A wave then loads a whole B operand as
+// 1 KB of consecutive bytes. In row order (B rows of ldx elements, hi and lo in two arrays) each lane
+// of such a load reads 16 bytes of a different row, and the vector cache takes one access per lane:
+// at 64 sequences that was the skinny products' bound (rocprof at 64 sequences: ~64 L1 accesses per
+// load instruction, TA address stalls). Rows past the batch are never written; their columns of the
+// products are never read.
+// Fragment order: with 2 or 4 column blocks (CB, skf_blocks) K-block major (the CB fragments of one
+// K block adjacent), with 8 column-block major (the K blocks of one column block adjacent). Every
+// workgroup of a product reads the same fragments at about the same time; measured on MI355X at
+// context 256 (layer by layer, per step), 16 / 32 / 64 sequences: column-block major 1744 / 2412 /
+// 2411 us, K-block major 1513 / 1994 / 2596, row order 1544 / 1979 / 2863.
+__host__ __device__ inline int skf_blocks(int B) { return B <= 8 ? 1 : B <= 16 ? 2 : B <= 32 ? 4 : 8; }
+__host__ __device__ inline size_t skf_frag(int cb, int kb, int CB, int K) {
+  return CB == 8 ? (size_t)cb * (K >> 5) + kb : (size_t)kb * CB + cb;
+}
+__host__ __device__ inline size_t skf_off(int b, int k, int part, int B, int K) {
+  const int cb = b >> 3, li = 2 * (b & 7) + part, kb = k >> 5, lg = (k & 31) >> 3;
+  return ((skf_frag(cb, kb, skf_blocks(B), K) * 64 + lg * 16 + li) << 3) + (k & 7);
+}
+// Elements of the skinny fragments of B rows: whole column blocks of the kernel that reads them (1,
+// 2, 4 or 8 blocks of 8 rows), hi and lo.
+__host__ __device__ inline size_t skf_elems(int B, int K) { return (size_t)skf_blocks(B) * 8 * K * 2; }
+
 // A workgroup takes 16 weight rows (rows 16 bx ..). SK_RAW / SK_PART: its K range [by K / gy, ...)
 // split over the 4 waves; SK_SILU: 16 intermediates, gate rows on waves 0-1 and up rows on waves
 // 2-3, each pair splitting K in two. Each wave's K range is a multiple of 256 (checked on the host).
@@ -768,7 +794,8 @@ struct SkArgs {
 // tokens): column li of block cb is row 8 cb + li / 2, hi (even li) or lo (odd li). The weight
 // fragments of a K chunk stay in registers across the column blocks; the next block's activation
 // fragments are loaded while the current block is multiplied.
-template <int EPI, int CB>
+// With FRAG the activations are skinny fragments (skf_off) in xh, of the batch's CB column blocks.
+template <int EPI, int CB, bool FRAG = false>
 __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   constexpr int NC = 8 * CB;
   __shared__ float red[4][16][NC + 1];
@@ -804,20 +831,24 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   f32x4 c[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) c[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint4* xf = reinterpret_cast<const uint4*>(g.xh) + lane;  // FRAG: this lane's 16 bytes of fragment 0
+  auto ld_act = [&](int cb, int k) {
+    if constexpr (FRAG) return xf[skf_frag(cb, k >> 5, CB, g.K) * 64];
+    else return live[cb] ? *reinterpret_cast<const uint4*>(xs[cb] + k) : make_uint4(0, 0, 0, 0);
+  };
   for (int k0 = kb; k0 < ke; k0 += 256) {
     uint4 wa[8], xb[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       wa[u] = ld_stream(reinterpret_cast<const uint4*>(wrow + k0 + 32 * u + 8 * lg));
-      xb[u] = live[0] ? *reinterpret_cast<const uint4*>(xs[0] + k0 + 32 * u) : make_uint4(0, 0, 0, 0);
+      xb[u] = ld_act(0, k0 + 32 * u);
     }
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
       uint4 xn[8];
       if (cb + 1 < CB) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          xn[u] = live[cb + 1] ? *reinterpret_cast<const uint4*>(xs[cb + 1] + k0 + 32 * u) : make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < 8; ++u) xn[u] = ld_act(cb + 1, k0 + 32 * u);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) c[cb] = mfma(wa[u], xb[u], c[cb]);
@@ -841,9 +872,14 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
     if constexpr (EPI == SK_SILU) {
       const float gt = red[0][r][b] + red[1][r][b], up = red[2][r][b] + red[3][r][b];
       const float m = gt / (1.f + expf(-gt)) * up;
-      const uint16_t hi = f32_to_bf16(m);
-      g.mh[(size_t)b * g.ldm + n0 + r] = hi;
-      g.ml[(size_t)b * g.ldm + n0 + r] = f32_to_bf16(m - bf16_to_f32(hi));
+      const uint16_t hi = f32_to_bf16(m), lo = f32_to_bf16(m - bf16_to_f32(hi));
+      if constexpr (FRAG) {  // the down product's skinny fragments (g.ldm inputs)
+        g.mh[skf_off(b, n0 + r, 0, g.B, g.ldm)] = hi;
+        g.mh[skf_off(b, n0 + r, 1, g.B, g.ldm)] = lo;
+      } else {
+        g.mh[(size_t)b * g.ldm + n0 + r] = hi;
+        g.ml[(size_t)b * g.ldm + n0 + r] = lo;
+      }
     } else {
       const float v = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
       g.out[((size_t)blockIdx.y * g.B + b) * g.N + n0 + r] = v;
@@ -851,12 +887,16 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   }
 }
 
+
 // The skinny product for up to 8 * cb activation rows (cb: 1, 2, 4 or 8 column blocks).
-static hipError_t launch_skinny(int epi, int cb, dim3 grid, const SkArgs& a, hipStream_t st) {
-#define MK_SK(E, C) hipLaunchKernelGGL((skinny_kernel<E, C>), grid, dim3(256), 0, st, a)
-#define MK_SK_CB(E) \
-  if (cb == 1) MK_SK(E, 1); else if (cb == 2) MK_SK(E, 2); else if (cb == 4) MK_SK(E, 4); else MK_SK(E, 8)
-  if (epi == SK_RAW) { MK_SK_CB(SK_RAW); } else if (epi == SK_PART) { MK_SK_CB(SK_PART); } else { MK_SK_CB(SK_SILU); }
+static hipError_t launch_skinny(int epi, int cb, dim3 grid, const SkArgs& a, hipStream_t st, bool frag = false) {
+#define MK_SK(E, C, F) hipLaunchKernelGGL((skinny_kernel<E, C, F>), grid, dim3(256), 0, st, a)
+#define MK_SK_CB(E, F) \
+  if (cb == 1) MK_SK(E, 1, F); else if (cb == 2) MK_SK(E, 2, F); else if (cb == 4) MK_SK(E, 4, F); else MK_SK(E, 8, F)
+#define MK_SK_E(F) \
+  if (epi == SK_RAW) { MK_SK_CB(SK_RAW, F); } else if (epi == SK_PART) { MK_SK_CB(SK_PART, F); } else { MK_SK_CB(SK_SILU, F); }
+  if (frag) { MK_SK_E(true); } else { MK_SK_E(false); }
+#undef MK_SK_E
 #undef MK_SK_CB
 #undef MK_SK
   return hipGetLastError();
@@ -867,7 +907,9 @@ static int column_blocks(int rows) { return rows <= 8 ? 1 : rows <= 16 ? 2 : row
 // reads row 0 and sets *bad); with `part`, x[b] += sum over s < S of part[s][b] (in order); then,
 // with `w`, RMSNorm into the bf16 hi/lo pair: [B][lda], or with FRAG the fragment-major layout of
 // H columns that gemm_kernel reads. One wave per row.
-template <int H, bool FRAG = false>
+// LAYOUT 0: row order ah/al [B][lda]; 1: the GEMM's fragment order (frag_off, H columns); 2: skinny
+// fragments (skf_off, H inputs, hi and lo both in ah).
+template <int H, int LAYOUT = 0>
 __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tokens, const uint16_t* embed, int vocab,
                                                     int32_t* bad, const float* part, int S, const uint16_t* w,
                                                     uint16_t* ah, uint16_t* al, int lda, int B) {
@@ -897,12 +939,24 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
       const float4 t = *reinterpret_cast<const float4*>(xr + k);
       v[k] = t.x; v[k + 1] = t.y; v[k + 2] = t.z; v[k + 3] = t.w;
     }
-    for (int s = 0; s < S; ++s) {
-      const float* pr = part + ((size_t)s * B + b) * H + E * lane;
+    // the partials in order, four at a time: their loads go out together (one round trip per four
+    // partials instead of one per partial; up to 16 partials come from the batched decode's products)
+    for (int s0 = 0; s0 < S; s0 += 4) {
+      float4 t[4][E / 4];
 #pragma unroll
-      for (int k = 0; k < E; k += 4) {
-        const float4 t = *reinterpret_cast<const float4*>(pr + k);
-        v[k] += t.x; v[k + 1] += t.y; v[k + 2] += t.z; v[k + 3] += t.w;
+      for (int i = 0; i < 4; ++i) {
+        const float* pr = part + ((size_t)(s0 + i < S ? s0 + i : s0) * B + b) * H + E * lane;
+#pragma unroll
+        for (int k = 0; k < E; k += 4) t[i][k / 4] = *reinterpret_cast<const float4*>(pr + k);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (s0 + i < S) {
+#pragma unroll
+          for (int k = 0; k < E; k += 4) {
+            v[k] += t[i][k / 4].x; v[k + 1] += t[i][k / 4].y; v[k + 2] += t[i][k / 4].z; v[k + 3] += t[i][k / 4].w;
+          }
+        }
       }
     }
   }
@@ -923,9 +977,14 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
     for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
     uint4 hi, lo;
     split8(y, hi, lo);
-    const size_t o = FRAG ? frag_off(b, E * lane + k, H) : (size_t)b * lda + E * lane + k;
-    *reinterpret_cast<uint4*>(ah + o) = hi;
-    *reinterpret_cast<uint4*>(al + o) = lo;
+    if constexpr (LAYOUT == 2) {
+      *reinterpret_cast<uint4*>(ah + skf_off(b, E * lane + k, 0, B, H)) = hi;
+      *reinterpret_cast<uint4*>(ah + skf_off(b, E * lane + k, 1, B, H)) = lo;
+    } else {
+      const size_t o = LAYOUT == 1 ? frag_off(b, E * lane + k, H) : (size_t)b * lda + E * lane + k;
+      *reinterpret_cast<uint4*>(ah + o) = hi;
+      *reinterpret_cast<uint4*>(al + o) = lo;
+    }
   }
 }
 
@@ -1125,6 +1184,7 @@ __global__ void __launch_bounds__(256) battn_partial_kernel(const float* raw, co
 
 // Merge of the splits of each sequence and query head into the O-projection's input row (bf16 hi/lo
 // [B][2048]); 128 threads, one per dim.
+// ldo == 0: skinny fragments of the 2048 attention outputs in oh (hi and lo).
 __global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int S, const int32_t* positions,
                                                           int max_seq, uint16_t* oh, uint16_t* ol, int ldo) {
   const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
@@ -1141,9 +1201,14 @@ __global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int
     Ls = fmaf(q[D + 1], f, Ls);
   }
   const float o = A / Ls;
-  const uint16_t hi = f32_to_bf16(o);
-  oh[(size_t)b * ldo + h * D + d] = hi;
-  ol[(size_t)b * ldo + h * D + d] = f32_to_bf16(o - bf16_to_f32(hi));
+  const uint16_t hi = f32_to_bf16(o), lo = f32_to_bf16(o - bf16_to_f32(hi));
+  if (ldo == 0) {
+    oh[skf_off(b, h * D + d, 0, gridDim.x, HQ * D)] = hi;
+    oh[skf_off(b, h * D + d, 1, gridDim.x, HQ * D)] = lo;
+  } else {
+    oh[(size_t)b * ldo + h * D + d] = hi;
+    ol[(size_t)b * ldo + h * D + d] = lo;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1298,7 +1363,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   for (int l = 0; M > SMALL_M && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
     const dim3 rows((M + 3) / 4);
-    MKP_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab,
+    MKP_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab,
                wk.bad, wk.part, l > 0 && sd > 1 ? sd : 0, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
     GemmArgs g{};
     g.ah = wk.ah; g.al = wk.al; g.M = M; g.K = H;
@@ -1315,7 +1380,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     go.ah = wk.ah; go.al = wk.al; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H; go.part = so > 1 ? wk.part : nullptr;
     MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, so), dim3(256), 0, st, go);
-    MKP_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
+    MKP_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
                so > 1 ? so : 0, (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
     GemmArgs gu{};
     gu.ah = wk.ah; gu.al = wk.al; gu.M = M; gu.N = 2 * I; gu.K = H;
@@ -1413,7 +1478,7 @@ namespace mkp {
 // Split-K factors of the O and down products (each wave's K range a multiple of 256)
 
 struct BLayout {
-  size_t x, ah, al, bh, bl, raw, part, apart, keys, bad, bytes;
+  size_t x, ah, al, af, bf, raw, part, apart, keys, bad, bytes;
 };
 static BLayout blayout(int H, int I, int B, int max_seq) {
   const size_t A = H > HQ * D ? H : HQ * D;
@@ -1424,8 +1489,8 @@ static BLayout blayout(int H, int I, int B, int max_seq) {
   L.x = take((size_t)B * H * 4);
   L.ah = take(frag_rows(B) * A * 2);  // whole row tiles for the LM head's gemm_kernel
   L.al = take(frag_rows(B) * A * 2);
-  L.bh = take((size_t)B * I * 2);
-  L.bl = take((size_t)B * I * 2);
+  L.af = take(skf_elems(B, (int)A) * 2);  // skinny fragments: the QKV, O and gate/up inputs
+  L.bf = take(skf_elems(B, I) * 2);       // ... and the down input
   L.raw = take((size_t)B * (HQ + 2 * HKV) * D * 4);
   L.part = take((size_t)3 * B * H * 4);
   L.apart = take((size_t)B * HKV * S * 2 * APW * 4);
@@ -1447,8 +1512,8 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   float* x = reinterpret_cast<float*>(ws + Lo.x);
   uint16_t* ah = reinterpret_cast<uint16_t*>(ws + Lo.ah);
   uint16_t* al = reinterpret_cast<uint16_t*>(ws + Lo.al);
-  uint16_t* bh = reinterpret_cast<uint16_t*>(ws + Lo.bh);
-  uint16_t* bl = reinterpret_cast<uint16_t*>(ws + Lo.bl);
+  uint16_t* af = reinterpret_cast<uint16_t*>(ws + Lo.af);
+  uint16_t* bf = reinterpret_cast<uint16_t*>(ws + Lo.bf);
   float* raw = reinterpret_cast<float*>(ws + Lo.raw);
   float* part = reinterpret_cast<float*>(ws + Lo.part);
   float* apart = reinterpret_cast<float*>(ws + Lo.apart);
@@ -1467,49 +1532,50 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   // 16 at most (the grid cannot follow the device-side positions, so it must not be mostly idle)
   const int gx = B <= 8 ? 16 : B <= 16 ? 8 : B <= 32 ? 4 : 2;
   const dim3 rows((B + 3) / 4);
+  const int so = BP::SO, sd = BP::SD;
   for (int l = 0; l < L; ++l) {
     const mk_layer_weights& lw = layers[l];
-    // x (embedding, or + the previous layer's down partials) -> input norm
-    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, l == 0 ? tokens : nullptr, embed, dims.vocab, bad,
-               part, l == 0 ? 0 : BP::SD, (const uint16_t*)lw.norm_weight, ah, al, A, B);
+    // x (embedding, or + the previous layer's down partials) -> input norm, as skinny fragments
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, l == 0 ? tokens : nullptr, embed, dims.vocab, bad,
+               part, l == 0 ? 0 : sd, (const uint16_t*)lw.norm_weight, af, nullptr, 0, B);
     SkArgs q{};
-    q.xh = ah; q.xl = al; q.ldx = A; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
+    q.xh = af; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
-    if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st, true)) != hipSuccess) return e;
     MKB_LAUNCH(battn_partial_kernel, dim3(S < gx ? S : gx, HKV, B), dim3(256), 0, st, raw, positions, tokens,
                dims.vocab, (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
                v_cache, L, l, max_seq, apart, S, bad);
-    MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, ah, al, A);
+    MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, af, nullptr, 0);
     SkArgs o{};
-    o.xh = ah; o.xl = al; o.ldx = A; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
-    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, BP::SO), o, st)) != hipSuccess) return e;
-    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SO,
-               (const uint16_t*)lw.post_attn_norm_weight, ah, al, A, B);
+    o.xh = af; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, so), o, st, true)) != hipSuccess) return e;
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, so,
+               (const uint16_t*)lw.post_attn_norm_weight, af, nullptr, 0, B);
     SkArgs u{};
-    u.xh = ah; u.xl = al; u.ldx = A; u.B = B; u.N = I; u.K = H;
-    u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bh; u.ml = bl; u.ldm = I;
-    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 16, 1), u, st)) != hipSuccess) return e;
+    u.xh = af; u.B = B; u.N = I; u.K = H;
+    u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bf; u.ldm = I;
+    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 16, 1), u, st, true)) != hipSuccess) return e;
     SkArgs dn{};
-    dn.xh = bh; dn.xl = bl; dn.ldx = I; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
+    dn.xh = bf; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
     dn.out = part;
-    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, BP::SD), dn, st)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, sd), dn, st, true)) != hipSuccess) return e;
   }
   // the last layer's down partials and the final norm, then the tied LM head as one more skinny
   // product (vocabulary rows x the B normalised rows: each table byte read once, on the matrix
   // cores) and the greedy keys
   const bool lm_tiles = B > 8 && dims.vocab % NT == 0;
   if (lm_tiles)
-    MKB_LAUNCH((bnorm_kernel<H, true>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD,
+    MKB_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
                final_norm, ah, al, A, B);
   else
-    MKB_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, BP::SD, final_norm,
-               ah, al, A, B);
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
+               final_norm, af, nullptr, 0, B);
   if (!lm_tiles) {
     SkArgs lmh{};
-    lmh.xh = ah; lmh.xl = al; lmh.ldx = A; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
+    lmh.xh = af; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
     lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
-    if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st, true)) != hipSuccess) return e;
   } else {
     // beyond one column block the skinny product re-reads every row's activations per 16 table
     // rows; a 128-row tile of the table reads them once per 128 (the B rows are one row tile)

@@ -75,6 +75,7 @@ def engine(request):
     ("mini", tuple(2 + 31 * i for i in range(16)), 3, 2),  # 16 sequences: two full column blocks
     ("mini2k", (1900, 50, 1000, 1500, 300, 2000, 17, 800, 1200, 640, 1, 1750), 2, 2),  # 12 long: 32 ranges of 448
     ("mini17", (33, 200, 90), 4, 1),
+    ("mini17", tuple(5 + 37 * i for i in range(12)), 2, 1),  # 1.7B width, 12 sequences: register-blocked products
     ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
     ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
 ], indirect=["engine"])
