@@ -805,10 +805,10 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   const uint16_t* wrow;
   int kb, ke;
   if constexpr (EPI == SK_SILU) {
-    wrow = (w < 2 ? g.w0 : g.w1) + (size_t)n * g.K;
-    const int kc = g.K / 2;
-    kb = (w & 1) * kc;
-    ke = kb + kc;
+    wrow = (li < 8 ? g.w0 : g.w1) + (size_t)(8 * blockIdx.x + (li & 7)) * g.K;
+    const int kw = g.K / 4;
+    kb = w * kw;
+    ke = kb + kw;
   } else {
     if constexpr (EPI == SK_RAW)
       wrow = n < g.n1 ? g.w0 + (size_t)n * g.K
@@ -867,18 +867,20 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
       if (!(li & 1)) red[w][4 * lg + j][8 * cb + sb] = v;
     }
   __syncthreads();
-  for (int idx = tid; idx < 16 * g.B; idx += 256) {
+  for (int idx = tid; idx < (EPI == SK_SILU ? 8 : 16) * g.B; idx += 256) {
     const int r = idx / g.B, b = idx % g.B;
     if constexpr (EPI == SK_SILU) {
-      const float gt = red[0][r][b] + red[1][r][b], up = red[2][r][b] + red[3][r][b];
+      const float gt = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
+      const float up = ((red[0][r + 8][b] + red[1][r + 8][b]) + red[2][r + 8][b]) + red[3][r + 8][b];
       const float m = gt / (1.f + expf(-gt)) * up;
       const uint16_t hi = f32_to_bf16(m), lo = f32_to_bf16(m - bf16_to_f32(hi));
+      const int it = 8 * blockIdx.x + r;
       if constexpr (FRAG) {  // the down product's skinny fragments (g.ldm inputs)
-        g.mh[skf_off(b, n0 + r, 0, g.B, g.ldm)] = hi;
-        g.mh[skf_off(b, n0 + r, 1, g.B, g.ldm)] = lo;
+        g.mh[skf_off(b, it, 0, g.B, g.ldm)] = hi;
+        g.mh[skf_off(b, it, 1, g.B, g.ldm)] = lo;
       } else {
-        g.mh[(size_t)b * g.ldm + n0 + r] = hi;
-        g.ml[(size_t)b * g.ldm + n0 + r] = lo;
+        g.mh[(size_t)b * g.ldm + it] = hi;
+        g.ml[(size_t)b * g.ldm + it] = lo;
       }
     } else {
       const float v = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
@@ -1347,7 +1349,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       u.xh = wk.ah; u.xl = wk.al; u.ldx = A; u.B = M; u.N = I; u.K = H;
       u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight;
       u.mh = wk.bh; u.ml = wk.bl; u.ldm = I;
-      if ((e = skinny(SK_SILU, dim3(I / 16, 1), u)) != hipSuccess) return e;
+      if ((e = skinny(SK_SILU, dim3(I / 8, 1), u)) != hipSuccess) return e;
       SkArgs dn{};
       dn.xh = wk.bh; dn.xl = wk.bl; dn.ldx = I; dn.B = M; dn.N = H; dn.K = I;
       dn.w0 = (const uint16_t*)lw.down_proj_weight; dn.out = wk.part;
@@ -1555,7 +1557,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     SkArgs u{};
     u.xh = af; u.B = B; u.N = I; u.K = H;
     u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bf; u.ldm = I;
-    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 16, 1), u, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 8, 1), u, st, true)) != hipSuccess) return e;
     SkArgs dn{};
     dn.xh = bf; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
     dn.out = part;

@@ -44,6 +44,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--engine", type=int, default=0, choices=(0, 1, 2),
                     help="decode_batch engine: 0 automatic, 1 layer by layer, 2 persistent kernel (where it applies)")
+    ap.add_argument("--graph", action="store_true",
+                    help="decode_batch: capture one call in a HIP graph (torch.cuda.graph) and time its replays")
     ap.add_argument("--transformers", action="store_true",
                     help="also time the reference path: Transformers' GPU prefill plus the cache copy")
     a = ap.parse_args(argv)
@@ -92,9 +94,20 @@ def main(argv=None):
         vc = torch.randn(B, L, 8, a.max_seq, 128, generator=dgen, device=dev).to(torch.bfloat16)
         toks = torch.randint(0, vocab, (B,), generator=gen).to(dev, torch.int32)
         pos = torch.full((B,), a.context, dtype=torch.int32, device=dev)
-        med, runs = _time(lambda: kernel.decode_batch(toks, pos, embed, embed, fn, lw, cos, sin, kc, vc, a.max_seq),
-                          a.warmup, a.runs)
-        print(f"[decode_batch {a.shape} B={B} context={a.context} engine {a.engine}] {med * 1e3:.1f} us per step median of "
+        step = lambda: kernel.decode_batch(toks, pos, embed, embed, fn, lw, cos, sin, kc, vc, a.max_seq)
+        if a.graph:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step()
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            step = g.replay
+        med, runs = _time(step, a.warmup, a.runs)
+        print(f"[decode_batch {a.shape} B={B} context={a.context} engine {a.engine}{' graph' if a.graph else ''}] "
+              f"{med * 1e3:.1f} us per step median of "
               f"{len(runs)} ({B / med * 1e3:,.0f} tokens/s)", flush=True)
         del kc, vc
     if kernel.status() != 0:
