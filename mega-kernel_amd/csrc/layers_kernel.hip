@@ -75,7 +75,11 @@ __device__ __forceinline__ size_t kv_row(const KvMap& m, int layer, int head, in
 // operand bytes are written to LDS. The next step's loads are in flight during the current step's
 // MFMAs. The epilogue takes the tile's fp32 sums.
 // ------------------------------------------------------------------------------------------------
-constexpr int MT = 128, NT = 128, KT = 64, KP = KT + 8;  // KP: padded LDS row (144 B)
+// KP: padded LDS row of the weight tile, 160 B. A row stride of 32 modulo 128 bytes is what makes the
+// fragment reads (16 lanes on 16 rows, 4 lanes on consecutive 16-byte chunks of each) conflict-free
+// on MI355X; 144 B (16 mod 128) costs a second LDS cycle per read (SQ_LDS_BANK_CONFLICT, measured
+// with an LDS probe: 4 extra cycles per ds_read_b128).
+constexpr int MT = 128, NT = 128, KT = 64, KP = KT + 16;
 constexpr int CP = NT + 4;                              // padded fp32 row of the epilogue tile
 
 // Fragment-major layout of a bf16 activation matrix with K columns (K a multiple of 32), the A
@@ -371,9 +375,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 // staged through LDS so that every global store is 16 bytes.
 // ------------------------------------------------------------------------------------------------
 constexpr int QB = 64, KB = 64;
-constexpr int KSP = D + 8;   // padded K row in LDS (272 B)
-constexpr int VSP = KB + 8;  // padded V^T row (144 B = 36 banks: rows 8 apart sit 32 banks apart)
-constexpr int OSP = D + 8;   // padded output staging row
+constexpr int KSP = D + 16;  // padded K row in LDS (288 B: 32 modulo 128, conflict-free fragment reads)
+constexpr int VSP = KB + 8;  // padded V^T row (144 B: its 8-byte fragment reads measured conflict-free)
+constexpr int OSP = D + 16;  // padded output staging row (288 B)
 
 struct AttnArgs {
   const uint16_t* qh;
@@ -486,18 +490,22 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     auto consume = [&](int kb, int buf) __attribute__((always_inline)) {
       const int kp0 = kb * KB;
       if (kp0 > wlast) return;  // a block entirely after this wave's queries adds nothing
-      // scores S^T: 4 blocks of 16 keys x this wave's 16 queries
+      // scores S^T: 4 blocks of 16 keys x this wave's 16 queries. The four key blocks' products are
+      // interleaved (a dependent MFMA waits ~45 cycles for its accumulator, an independent one
+      // issues every ~17); each block's sum keeps the order dims 0..127, hi before lo.
       f32x4 st[4];
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      for (int mb = 0; mb < 4; ++mb) st[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const uint4 fk = *reinterpret_cast<const uint4*>(&sm.kv.ks[buf][16 * mb + li][32 * s + 8 * lg]);
-          c = mfma(fk, fq[0][s], c);
-          c = mfma(fk, fq[1][s], c);
-        }
-        st[mb] = c;
+      for (int s = 0; s < 4; ++s) {
+        uint4 fk[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          fk[mb] = *reinterpret_cast<const uint4*>(&sm.kv.ks[buf][16 * mb + li][32 * s + 8 * lg]);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) st[mb] = mfma(fk[mb], fq[0][s], st[mb]);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) st[mb] = mfma(fk[mb], fq[1][s], st[mb]);
       }
       // causal mask (only on blocks that reach past the wave's first query) and scale; block
       // maximum of this lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip)
@@ -553,15 +561,19 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
         for (int j = 0; j < 4; ++j) { pw[j] = st[2 * t][j]; pw[4 + j] = st[2 * t + 1][j]; }
         uint4 ph, pl;
         split8(pw, ph, pl);
+        uint4 fv[8];
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) {
           const uint16_t* vr = &sm.kv.vt[buf][16 * nb + li][32 * t + 4 * lg];
           const uint2 v0 = *reinterpret_cast<const uint2*>(vr);       // keys 32t + 4g .. +3
           const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);  // keys 32t + 16 + 4g .. +3
-          const uint4 fv = make_uint4(v0.x, v0.y, v1.x, v1.y);
-          acc[nb] = mfma(ph, fv, acc[nb]);
-          acc[nb] = mfma(pl, fv, acc[nb]);
+          fv[nb] = make_uint4(v0.x, v0.y, v1.x, v1.y);
         }
+        // hi for every dim block, then lo: eight independent accumulators between dependent MFMAs
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[nb] = mfma(ph, fv[nb], acc[nb]);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[nb] = mfma(pl, fv[nb], acc[nb]);
       }
     };
 
