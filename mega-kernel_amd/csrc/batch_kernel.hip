@@ -61,7 +61,7 @@ constexpr int QR = QX / WPX;            // 16 rows per workgroup
 constexpr int OR = H / WPX;             // 32 o_proj rows (and down_proj rows) per workgroup
 constexpr int GI = IX / WPX;            // 12 intermediates per workgroup
 constexpr int APW = 2 * D + 4;          // attention partial: acc[2][128], m0, l0, m1, l1
-constexpr int KST = H + 16;             // LDS row stride of the MFMA B operand (bf16): 32 mod 128 bytes, conflict-free reads
+constexpr int KST = H + 8;              // LDS row stride of the MFMA B operand (bf16): conflict-free reads
 template <int CB> constexpr int rst() { return 16 * CB + 4; }  // reduction tile row stride (floats): conflict-free
 constexpr int MAXL = 32;
 constexpr int NG = 4 * NMW;             // 16-lane attention groups per workgroup
