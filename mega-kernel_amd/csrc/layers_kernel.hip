@@ -272,80 +272,80 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) sm.c[wave * 32 + bm * 16 + 4 * lg + j][bn * 16 + li] = acc[bm][bn][j];
   __syncthreads();
-  const int r = tid >> 1, half = tid & 1;  // two threads per row
-  const int m = m0 + r;
-  if (m >= g.M) return;
+  // The stores are laid out so that a wave's store instruction writes whole 256-byte rows or whole
+  // 1 KB fragments: per-thread row segments (two threads per row, each lane of a store on another
+  // row) made the stores a third of the QKV GEMM's time at 3,584 tokens.
+  auto ld8 = [&](int row, int c, float (&v)[8]) {
+    const float4 x0 = *reinterpret_cast<const float4*>(&sm.c[row][c]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&sm.c[row][c + 4]);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  };
 
   if constexpr (EPI == EPI_SILU) {
-    // columns 0..63 gate, 64..127 up of intermediates [64 tn, 64 tn + 64); this thread: 32 of them
-    const int c0 = 32 * half;
+    // columns 0..63 gate, 64..127 up of intermediates [64 tn, 64 tn + 64): 8 row blocks x 2 K blocks
+    // of 32 = 16 fragments of the down product's A operand; wave w writes fragments 4 w .. 4 w + 3,
+    // lane l its row l % 16 and intermediates 8 (l / 16) .. +7 (frag_off's order)
 #pragma unroll
-    for (int c = 0; c < 32; c += 8) {
-      float mv[8];
+    for (int f = 0; f < 4; ++f) {
+      const int fr = 4 * wave + f, rb = fr >> 1, kb = fr & 1;
+      const int r = 16 * rb + li, m = m0 + r, c = 32 * kb + 8 * lg;
+      if (m < g.M) {
+        float gt[8], up[8], mv[8];
+        ld8(r, c, gt);
+        ld8(r, NT / 2 + c, up);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float gt = sm.c[r][c0 + c + q], up = sm.c[r][NT / 2 + c0 + c + q];
-        mv[q] = gt / (1.f + expf(-gt)) * up;  // silu(gate) * up (/root/reference/megakernel.cu:659-665)
+        for (int q = 0; q < 8; ++q) mv[q] = gt[q] / (1.f + expf(-gt[q])) * up[q];  // silu(gate) * up (/root/reference/megakernel.cu:659-665)
+        uint4 hi, lo;
+        split8(mv, hi, lo);
+        const size_t o = frag_off(m, tn * (NT / 2) + c, g.N / 2);
+        *reinterpret_cast<uint4*>(g.bh + o) = hi;
+        *reinterpret_cast<uint4*>(g.bl + o) = lo;
       }
-      uint4 hi, lo;
-      split8(mv, hi, lo);
-      const size_t o = frag_off(m, tn * (NT / 2) + c0 + c, g.N / 2);
-      *reinterpret_cast<uint4*>(g.bh + o) = hi;
-      *reinterpret_cast<uint4*>(g.bl + o) = lo;
     }
     return;
   }
 
   if constexpr (EPI == EPI_QKV) {
-    // tile tn is one head: q head tn (< 16), k head tn - 16 (< 24) or v head tn - 24
-    const int pos = g.position + m;
-    const int d0 = 64 * half;  // this thread's dims [d0, d0 + 64); the RoPE partner of d is d ^ 64
-    const int page = tn >= HQ && g.kv.bt ? kv_page(g.kv, pos, g.bad) : 0;
-    if (tn >= HQ + HKV) {      // v: rounded to bf16 into the cache as is
-      if (page < 0) return;
-      uint16_t* dst = g.v_cache + kv_row(g.kv, g.layer, tn - HQ - HKV, pos, page) + d0;
+    // tile tn is one head: q head tn (< 16), k head tn - 16 (< 24) or v head tn - 24. 16 lanes per
+    // row (lane t: dims 8t .. 8t + 7), 4 rows per wave and pass, 8 passes
+    const int tt = lane & 15, rq = lane >> 4;  // tt: the lane's 8 dims; rq: its row of the pass
+    float wn[8];
+    if (tn < HQ + HKV) unpack8(*reinterpret_cast<const uint4*>((tn < HQ ? g.q_norm : g.k_norm) + 8 * tt), wn);
+#pragma unroll 2
+    for (int pass = 0; pass < 8; ++pass) {
+      const int r = 32 * wave + 4 * pass + rq, m = m0 + r;
+      if (m >= g.M) continue;
+      const int pos = g.position + m;
+      const int page = tn >= HQ && g.kv.bt ? kv_page(g.kv, pos, g.bad) : 0;
+      float v[8];
+      ld8(r, 8 * tt, v);
+      if (tn >= HQ + HKV) {  // v: rounded to bf16 into the cache as is
+        if (page >= 0) {
+          uint32_t p[4];
 #pragma unroll
-      for (int c = 0; c < 64; c += 8) {
-        uint32_t p[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(sm.c[r][d0 + c + 2 * q], sm.c[r][d0 + c + 2 * q + 1]);
-        *reinterpret_cast<uint4*>(dst + c) = make_uint4(p[0], p[1], p[2], p[3]);
+          for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+          *reinterpret_cast<uint4*>(g.v_cache + kv_row(g.kv, g.layer, tn - HQ - HKV, pos, page) + 8 * tt) =
+              make_uint4(p[0], p[1], p[2], p[3]);
+        }
+        continue;
       }
-      return;
-    }
-    // per-head RMSNorm over the 128 dims (/root/reference/megakernel.cu:490-630), then rotate-half
-    // RoPE with the table entry of dim d mod 64 (/root/reference/megakernel.cu:548-555)
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < 64; ++c) ss = fmaf(sm.c[r][d0 + c], sm.c[r][d0 + c], ss);
-    ss += __shfl_xor(ss, 1);
-    const float rs = rsqrtf(ss / (float)D + EPS);
-    const uint16_t* nw = tn < HQ ? g.q_norm : g.k_norm;
-    const uint16_t* cr = g.cos_tab + (size_t)pos * D;
-    const uint16_t* sr = g.sin_tab + (size_t)pos * D;
-    const int dp = 64 - d0;  // partner half
-#pragma unroll
-    for (int c = 0; c < 64; c += 8) {
-      float o[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = c + q;
-        const float u = sm.c[r][d0 + i] * rs * bf16_to_f32(nw[d0 + i]);
-        const float up = sm.c[r][dp + i] * rs * bf16_to_f32(nw[dp + i]);
-        const float cs = bf16_to_f32(cr[i]), sn = bf16_to_f32(sr[i]);
-        o[q] = half == 0 ? u * cs - up * sn : u * cs + up * sn;
-      }
+      // per-head RMSNorm over the 128 dims (/root/reference/megakernel.cu:490-630), then rotate-half
+      // RoPE with the table entry of dim d mod 64 (/root/reference/megakernel.cu:548-555)
+      float cs[8], sn[8];
+      unpack8(*reinterpret_cast<const uint4*>(g.cos_tab + (size_t)pos * D + 8 * (tt & 7)), cs);
+      unpack8(*reinterpret_cast<const uint4*>(g.sin_tab + (size_t)pos * D + 8 * (tt & 7)), sn);
+      head_norm_rope(v, wn, cs, sn, tt);
       if (tn < HQ) {
         uint4 hi, lo;
-        split8(o, hi, lo);
-        const size_t off = (size_t)m * (HQ * D) + tn * D + d0 + c;
+        split8(v, hi, lo);
+        const size_t off = (size_t)m * (HQ * D) + tn * D + 8 * tt;
         *reinterpret_cast<uint4*>(g.qh + off) = hi;
         *reinterpret_cast<uint4*>(g.ql + off) = lo;
       } else if (page >= 0) {
         uint32_t p[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(o[2 * q], o[2 * q + 1]);
-        *reinterpret_cast<uint4*>(g.k_cache + kv_row(g.kv, g.layer, tn - HQ, pos, page) + d0 + c) =
+        for (int q = 0; q < 4; ++q) p[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+        *reinterpret_cast<uint4*>(g.k_cache + kv_row(g.kv, g.layer, tn - HQ, pos, page) + 8 * tt) =
             make_uint4(p[0], p[1], p[2], p[3]);
       }
     }
