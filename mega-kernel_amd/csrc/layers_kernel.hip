@@ -376,8 +376,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 // ------------------------------------------------------------------------------------------------
 constexpr int QB = 64, KB = 64;
 constexpr int KSP = D + 16;  // padded K row in LDS (288 B: 32 modulo 128, conflict-free fragment reads)
-constexpr int VSP = KB + 8;  // padded V^T row (144 B: its 8-byte fragment reads measured conflict-free)
-constexpr int OSP = D + 16;  // padded output staging row (288 B)
+constexpr int VSP = KB + 4;  // padded V^T row (136 B: the paired 8-byte fragment reads, one ds_read2_b64, conflict-free; 144 B costs 8 cycles each)
+constexpr int OSP = D + 8;   // padded output staging row (272 B: its 2-byte writes four rows apart on different banks)
 
 struct AttnArgs {
   const uint16_t* qh;
