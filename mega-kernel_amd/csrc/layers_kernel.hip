@@ -357,10 +357,12 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 // flash-style over blocks of 64 keys). Query row m sits at position `position + m` and attends keys
 // [0, position + m] of the cache, which already holds this layer's new rows (written by the QKV
 // epilogue).
-//   Work split: a workgroup (8 waves) takes one K/V head and a pair of 64-query blocks, i and
-//   nqb - 1 - i, one after the other, so that every workgroup does the same causal work. Waves 0-3
-//   take query head 2 kvh, waves 4-7 head 2 kvh + 1, 16 queries each: the two heads of a GQA pair
-//   share each K/V block staged in LDS.
+//   Work split: a workgroup (8 waves) takes one K/V head and one 64-query block, the blocks with
+//   the most keys dispatched first (workgroups 0-7 take the last block of each head), so the CUs
+//   that finish short blocks pick up the rest. (Pairs of blocks i and nqb - 1 - i per workgroup balanced the
+//   work too, but left 32 of the 256 CUs idle at 3,584 tokens: 224 workgroups.) Waves 0-3 take
+//   query head 2 kvh, waves 4-7 head 2 kvh + 1, 16 queries each: the two heads of a GQA pair share
+//   each K/V block staged in LDS.
 //   Pipeline: the next K/V block is loaded into registers while the current one is multiplied,
 //   then written into the other half of a double-buffered LDS tile; one barrier per block.
 //   S^T = K . Q^T on the matrix cores (keys as rows): lane l holds the scores of query i = l % 16
@@ -409,7 +411,8 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   __shared__ int32_t pages[ATT_MAX_PAGES];  // a paged cache's table entries (-1: out of range)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  const int kvh = blockIdx.y, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
+  // workgroup b: K/V head b % 8, query block nqb - 1 - b / 8 (the longest blocks of all heads first)
+  const int kvh = blockIdx.x % HKV, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
   const int nqb = (a.M + QB - 1) / QB;
   if (a.kv.bt) {
     const int n = ((a.position + a.M - 1) >> a.kv.shift) + 1;  // entries of keys [0, position + M)
@@ -428,9 +431,8 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   // dims 8 vc .. +7 (lanes of a wave span 32 key pairs and two chunks: conflict-free 32-bit writes)
   const int vp = lane & 31, vc = 2 * w + (lane >> 5);
 
-  for (int pass = 0; pass < 2; ++pass) {
-    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
-    if (pass == 1 && qb <= (int)blockIdx.x) break;  // odd nqb: the middle block runs once
+  {
+    const int qb = nqb - 1 - (int)blockIdx.x / HKV;
     const int q0 = qb * QB;
     const int qrow = q0 + wq + li;                       // this lane's query (score layout)
     const int qpos = a.position + qrow;
@@ -577,8 +579,7 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
       }
     };
 
-    if (pass == 1) __syncthreads();  // the first pass's output staging (which aliases the tiles) is read
-    // Earlier stores (the first pass's output rows, a paged table's error flag) complete first: with
+    // Earlier stores (a paged table's error flag) complete first: with
     // loads alone in flight the compiler's waits below cover single loads (a store in flight with them
     // makes every wait a full one, loads and stores completing out of order relative to each other).
     wait_vmem();
@@ -1327,7 +1328,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   } while (0)
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad);
   const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M > SMALL_M ? 1 : 0, M, 0, position, kv, wk.bad};
-  const dim3 attn_grid(((M + QB - 1) / QB + 1) / 2, HKV);
+  const dim3 attn_grid((M + QB - 1) / QB * HKV);
   if (M <= SMALL_M) {
     // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
     // weight rows per workgroup, 256 to 384 workgroups), the O and down products split over K into
