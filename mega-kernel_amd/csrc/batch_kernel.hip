@@ -54,7 +54,7 @@ using namespace mkp;
 constexpr int NXCD = 8, WPX = 32, NWG = NXCD * WPX;
 constexpr int NCW = 4, NMW = 8, NWAVE = NCW + NMW, NT = 64 * NWAVE;  // 768 threads
 constexpr int CL = 64 * NCW;            // comm lanes
-constexpr int BMAX = 16;                // sequences per launch: CB column blocks of 8 (hi and lo of 8 fill 16 columns)
+constexpr int BMAX = MKB_MAX;           // sequences per launch: CB column blocks of 8 (hi and lo of 8 fill 16 columns)
 constexpr int H = 1024, I = 3072, IX = I / NXCD;
 constexpr int QX = 4 * D;               // q (2 heads), k, v rows of one K/V head: 512
 constexpr int QR = QX / WPX;            // 16 rows per workgroup

@@ -8,9 +8,11 @@
 
 #include "../../include/megakernel_amd.h"
 
-// Whether mk_decode_batch runs this batch on the persistent kernel: the Qwen3-0.6B shape, at most 16
-// sequences, at most 32 layers, a device with 256 CUs, and the engine not forced to the
-// layer-by-layer one (mk_set_batch_engine).
+// Sequences per launch of the persistent kernel.
+constexpr int MKB_MAX = 16;
+// Whether mk_decode_batch runs this batch on the persistent kernel: the Qwen3-0.6B shape, at most
+// MKB_MAX sequences, at most 32 layers, a device with 256 CUs, and the engine not forced to the
+// layer-by-layer one (mk_set_batch_engine). (17-32 sequences run as two such launches.)
 bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len);
 // Workspace bytes the persistent kernel needs (exchange words, tickets, greedy keys).
 size_t mkb_workspace_bytes();

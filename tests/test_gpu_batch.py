@@ -77,6 +77,8 @@ def engine(request):
     ("mini17", (33, 200, 90), 4, 1),
     ("mini17", tuple(5 + 37 * i for i in range(12)), 2, 1),  # 1.7B width, 12 sequences: register-blocked products
     ("mini", tuple(3 + 11 * i for i in range(20)), 2, 1),  # 20 sequences: 3 column blocks of 8 (of 4)
+    ("mini", tuple(3 + 11 * i for i in range(20)), 2, 2),  # 20 sequences: two persistent launches, 16 + 4
+    ("mini", tuple(1 + 15 * i for i in range(32)), 1, 2),  # 32 sequences: two persistent launches of 16
     ("mini", tuple(1 + 5 * i for i in range(64)), 1, 1),   # the largest batch: 8 column blocks
 ], indirect=["engine"])
 def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, engine, request):
@@ -85,7 +87,8 @@ def test_batch_matches_oracle_per_sequence(shape_fixture, lengths, steps, engine
     greedy token against the restatement on the kernel's cache for that sequence, and its new K/V
     rows. Layer by layer, up to 8 sequences share one 16-column MFMA block; 20 and 64 sequences use 3
     and 8. The persistent kernel (engine 2) runs up to 8 sequences in one column block and up to 16
-    in two, and cuts the batch's keys into at most 32 ranges, one per workgroup of an XCD."""
+    in two, and cuts the batch's keys into at most 32 ranges, one per workgroup of an XCD; 17-32
+    sequences run as two of its launches (the first 16, then the rest)."""
     sess = request.getfixturevalue(shape_fixture)
     prompts = [hf.prompt_ids(n, sess.shape.vocab, seed=10 + i)[0].tolist() for i, n in enumerate(lengths)]
     kc, vc, toks = _batched_cache(sess, prompts)
@@ -232,7 +235,8 @@ def test_persistent_engine_is_the_one_that_runs(mini, engine):
     the other engine-2 cases would pass on the wrong engine if the device check failed. With its phase
     trace on, the persistent kernel stamps every workgroup's kernel start, LM-head start and end (a
     100 MHz counter, in order); the layer-by-layer engine writes nothing there. Checked at 8
-    sequences (one MFMA column block) and 16 (two), and not at 17 (layer by layer)."""
+    sequences (one MFMA column block), 16 (two) and 17 and 32 (two launches: the trace holds the
+    second one's stamps), and not at 33 (layer by layer)."""
     import ctypes
 
     from megakernel import build as mkbuild
@@ -241,7 +245,7 @@ def test_persistent_engine_is_the_one_that_runs(mini, engine):
     lib.mk_set_batch_trace.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     nbytes = lib.mk_batch_trace_bytes()
     maxl, slots, grid = 32, 24, 256
-    for B, persistent in ((8, True), (16, True), (17, False)):
+    for B, persistent in ((8, True), (16, True), (17, True), (32, True), (33, False)):
         kd = torch.zeros(B, mini.shape.layers, 8, mini.max_seq, 128, dtype=torch.bfloat16, device=DEV)
         vd = torch.zeros_like(kd)
         buf = torch.zeros(nbytes // 8, dtype=torch.int64, device=DEV)

@@ -70,8 +70,8 @@ def test_prefill_graph_replays_match_eager(mini, P):
 
 
 @pytest.mark.parametrize("engine, lengths", [(1, (5, 40, 100, 300)), (1, tuple(3 + 11 * i for i in range(20))),
-                                             (2, (5, 40, 100, 300))],
-                         ids=["layers-b4", "layers-b20", "persistent-b4"])
+                                             (2, (5, 40, 100, 300)), (2, tuple(3 + 11 * i for i in range(20)))],
+                         ids=["layers-b4", "layers-b20", "persistent-b4", "persistent-two-launches-b20"])
 def test_decode_batch_graph_replays_match_eager(mini, engine, lengths):
     s = mini.shape
     B = len(lengths)
