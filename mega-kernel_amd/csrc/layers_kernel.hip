@@ -393,7 +393,27 @@ struct AttnArgs {
   int M, layer, position;
   KvMap kv;
   int32_t* bad;
+  // Key-range chunks (attn_plan): chunk > 0 cuts every query block into chunks of `chunk` key blocks,
+  // one workgroup each; a block with more than one chunk has its chunks' unnormalised partials
+  // written to `part` (slot = workgroup index: [slot][2 heads][qr rows][APS]) and merged by
+  // attn_merge_kernel. chunk == 0: one workgroup per query block, no partials.
+  float* part;
+  int chunk, qr;
 };
+constexpr int APS = D + 4;  // floats per partial row: acc[128], m, l, pad (16-byte aligned rows)
+
+// Key blocks that query block qb attends to: keys [0, position + min(M, (qb + 1) QB)).
+__host__ __device__ inline int attn_nkb(int qb, int M, int position) {
+  return (position + (M < (qb + 1) * QB ? M : (qb + 1) * QB) - 1) / KB + 1;
+}
+// Query blocks with more than c * T key blocks, i.e. those with a chunk c: the blocks qb >= the
+// first such one (attn_nkb grows with qb). Round c of the grid lists them from qb = nqb - 1 down.
+__host__ __device__ inline int attn_round(int c, int T, int M, int position, int nqb) {
+  const int need = c * T * KB - position + 1;  // qb qualifies iff min(M, (qb + 1) QB) >= need
+  if (need <= 0) return nqb;
+  if (need > M) return 0;
+  return nqb - ((need + QB - 1) / QB - 1);
+}
 constexpr int ATT_MAX_PAGES = 2048;  // block-table entries staged in LDS (as mk_decode_paged)
 
 struct AttnSmem {
@@ -405,15 +425,27 @@ struct AttnSmem {
     uint16_t o[8][2][16][OSP];  // per wave: hi, lo of its 16 output rows
   };
 };
+static_assert(sizeof(AttnSmem) >= 8 * 16 * (D + 4) * 4, "a chunk's partial rows staged per wave");
 
 __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) AttnSmem sm;
   __shared__ int32_t pages[ATT_MAX_PAGES];  // a paged cache's table entries (-1: out of range)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  // workgroup b: K/V head b % 8, query block nqb - 1 - b / 8 (the longest blocks of all heads first)
+  // workgroup b: K/V head b % 8, query block nqb - 1 - b / 8 (the longest blocks of all heads first);
+  // with chunks, round c of the grid (the rounds in order) lists chunk c of every query block that
+  // has one, longest blocks first, so the rounds hold full chunks before the shorter last ones
   const int kvh = blockIdx.x % HKV, h = 2 * kvh + (w >> 2), wq = 16 * (w & 3);
   const int nqb = (a.M + QB - 1) / QB;
+  int r = (int)blockIdx.x / HKV, c = 0;
+  if (a.chunk > 0) {
+    for (;; ++c) {  // bounded: the round sizes fall to 0, and the grid is their sum
+      const int n = attn_round(c, a.chunk, a.M, a.position, nqb);
+      if (n == 0) return;
+      if (r < n) break;
+      r -= n;
+    }
+  }
   if (a.kv.bt) {
     const int n = ((a.position + a.M - 1) >> a.kv.shift) + 1;  // entries of keys [0, position + M)
     for (int i = tid; i < n; i += 512) {
@@ -432,13 +464,17 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
   const int vp = lane & 31, vc = 2 * w + (lane >> 5);
 
   {
-    const int qb = nqb - 1 - (int)blockIdx.x / HKV;
+    const int qb = nqb - 1 - r;
     const int q0 = qb * QB;
     const int qrow = q0 + wq + li;                       // this lane's query (score layout)
     const int qpos = a.position + qrow;
     const int wlast = a.position + q0 + wq + 15;         // last position any query of this wave has
     const int last = a.position + min(a.M, q0 + QB) - 1;  // last key any query of the block sees
     const int nkb = last / KB + 1;
+    // this workgroup's key blocks [kb0, kb1): all of them, or chunk c
+    const int kb0 = a.chunk > 0 ? c * a.chunk : 0;
+    const int kb1 = a.chunk > 0 ? min(kb0 + a.chunk, nkb) : nkb;
+    const bool partial = a.chunk > 0 && nkb > a.chunk;
 
     // this lane's query fragments (B operand of S^T = K . Q^T): dims 32 s + 8 g .. +7, hi and lo
     uint4 fq[2][4];
@@ -532,14 +568,18 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
           }
       }
       bmax = xmax32(xmax16(bmax));
-      const float mnew = fmaxf(mrun, bmax);  // finite: key 0 <= every query's position
-      const float alpha = __expf(mrun - mnew);
+      // mnew is finite once the query has seen a key: from the first block on (key 0) without
+      // chunks; a chunk that starts past some of its block's queries leaves those at -inf, and
+      // then msafe keeps their weights exp(-inf) = 0 instead of NaN
+      const float mnew = fmaxf(mrun, bmax);
+      const float msafe = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __expf(mrun - msafe);
       float psum = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p = __expf(st[mb][j] - mnew);
+          const float p = __expf(st[mb][j] - msafe);
           st[mb][j] = p;
           psum += p;
         }
@@ -584,17 +624,33 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     // makes every wait a full one, loads and stores completing out of order relative to each other).
     wait_vmem();
     Blk A;
-    load_block(A, 0);
+    load_block(A, kb0);
     store_block(A, 0);
     __syncthreads();
     // the next block in flight while the current one is consumed (a second block in flight, or no
     // streaming at all, times the same: the loop is bound by its MFMA, VALU and LDS work)
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int buf = kb & 1;
-      if (kb + 1 < nkb) load_block(A, kb + 1);
+    for (int kb = kb0; kb < kb1; ++kb) {
+      const int buf = (kb - kb0) & 1;
+      if (kb + 1 < kb1) load_block(A, kb + 1);
       consume(kb, buf);
-      if (kb + 1 < nkb) store_block(A, buf ^ 1);
+      if (kb + 1 < kb1) store_block(A, buf ^ 1);
       __syncthreads();  // block kb consumed by every wave; block kb + 1 staged
+    }
+    if (partial) {
+      // this chunk's unnormalised rows and their (m, l) into the workgroup's slot, staged per wave in
+      // LDS as the slot's rows (APS floats; the tiles are free after the loop's last barrier) and
+      // stored as 16-byte chunks; rows past qr (queries past a short prompt) are not kept
+      float* stg = reinterpret_cast<float*>(&sm) + w * 16 * APS;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) stg[(4 * lg + j) * APS + 16 * nb + li] = acc[nb][j];
+      if (lg == 0) *reinterpret_cast<float2*>(stg + li * APS + D) = make_float2(mrun, lrun);
+      float* P = a.part + (((size_t)blockIdx.x * 2 + (w >> 2)) * a.qr + wq) * APS;
+      const int nch = (min(16, a.qr - wq) * APS) / 4;  // 16-byte chunks of this wave's kept rows
+      for (int k = lane; k < nch; k += 64)
+        reinterpret_cast<float4*>(P)[k] = reinterpret_cast<const float4*>(stg)[k];
+      return;
     }
     // normalise by each row's sum (query 4g + j's, from lane 4g + j), stage this wave's 16 rows as
     // hi/lo in LDS (the tiles are free after the loop's last barrier), then store 16-byte chunks
@@ -620,6 +676,97 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     }
   }
 }
+
+// The chunks of the query blocks that attn_kernel split (more than `chunk` key blocks): eight
+// workgroups per query block nqb - 1 - r and K/V head kvh, 16 of its 128 rows each, merge them max
+// first and in chunk order (so the result does not depend on which chunk finished first), and
+// write the normalised rows as the attention's own epilogue does. Chunk c of the block is attention
+// workgroup (rounds before c + r) * 8 + kvh.
+__global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
+  constexpr int MAXC = 32;  // chunks per query block (attn_plan: at most 32)
+  __shared__ int slot[MAXC];
+  __shared__ float wgt[16][MAXC + 1];  // exp(m_c - max) per row of this workgroup and chunk
+  // workgroup b: rows 16 (b % 8) .. +15 of the 128 (2 heads x 64 queries) of query block nqb - 1 - r
+  // of K/V head kvh, b / 8 = r * 8 + kvh; thread t: row t / 16, dims 8 (t % 16) .. +7
+  const int rg = blockIdx.x & 7, kvh = (blockIdx.x >> 3) % HKV, r = (blockIdx.x >> 3) / HKV;
+  const int nqb = (a.M + QB - 1) / QB, qb = nqb - 1 - r, q0 = qb * QB;
+  const int nc = min((attn_nkb(qb, a.M, a.position) + a.chunk - 1) / a.chunk, MAXC);
+  const int t = threadIdx.x, tr = t >> 4, ch = t & 15;
+  const int row = 16 * rg + tr, hh = row >> 6, rq = row & 63, m = q0 + rq;
+  if (t == 0) {
+    int off = 0;
+    for (int c = 0; c < nc; ++c) {
+      slot[c] = (off + r) * HKV + kvh;
+      off += attn_round(c, a.chunk, a.M, a.position, nqb);
+    }
+  }
+  __syncthreads();
+  auto prow = [&](int c, int rr) {  // row rr (of the 128) of chunk c's partial
+    return a.part + (((size_t)slot[c] * 2 + (rr >> 6)) * a.qr + (rr & 63)) * APS;
+  };
+  // every (row, chunk) m of the workgroup's 16 rows, loaded together; then each row's weights
+  for (int k = t; k < 16 * nc; k += 256) {
+    const int rr = 16 * rg + k / nc, c = k % nc;
+    wgt[k / nc][c] = (q0 + (rr & 63) < a.M) ? prow(c, rr)[D] : 0.f;
+  }
+  __syncthreads();
+  if (t < 16) {
+    float mx = -INFINITY;
+    for (int c = 0; c < nc; ++c) mx = fmaxf(mx, wgt[t][c]);  // finite: chunk 0 holds key 0
+    for (int c = 0; c < nc; ++c) wgt[t][c] = __expf(wgt[t][c] - mx);  // 0 for a chunk without keys (m = -inf)
+  }
+  __syncthreads();
+  if (m >= a.M) return;
+  float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int c = 0; c < nc; ++c) {
+    const float* p = prow(c, row);
+    const float f = wgt[tr][c];
+    const float4 u = *reinterpret_cast<const float4*>(p + 8 * ch), v = *reinterpret_cast<const float4*>(p + 8 * ch + 4);
+    L = fmaf(p[D + 1], f, L);
+    o[0] = fmaf(u.x, f, o[0]); o[1] = fmaf(u.y, f, o[1]); o[2] = fmaf(u.z, f, o[2]); o[3] = fmaf(u.w, f, o[3]);
+    o[4] = fmaf(v.x, f, o[4]); o[5] = fmaf(v.y, f, o[5]); o[6] = fmaf(v.z, f, o[6]); o[7] = fmaf(v.w, f, o[7]);
+  }
+  const float inv = 1.f / L;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] *= inv;
+  uint4 hi, lo;
+  split8(o, hi, lo);
+  const int h = 2 * kvh + hh;
+  const size_t off = a.frag ? frag_off(m, h * D + 8 * ch, HQ * D) : (size_t)m * a.ldo + h * D + 8 * ch;
+  *reinterpret_cast<uint4*>(a.oh + off) = hi;
+  *reinterpret_cast<uint4*>(a.ol + off) = lo;
+}
+
+// Chunk plan of the attention over a prompt of M tokens at `position`: chunk = ceil(U / 32) key
+// blocks, U the key blocks of one head's query blocks summed, i.e. about 256 chunk workgroups over
+// the 8 heads (one per CU; a workgroup of attn_kernel fills a CU), when the longest query block has
+// at least 1.25 chunks and 2 key blocks more than one chunk; otherwise no chunks (one workgroup per
+// query block: the grid then holds the work evenly enough, or the merge's extra launch would cost
+// more than the shorter chain saves). Every query block has at most U / chunk + 1 chunks, so the
+// grid holds at most 8 (32 + nqb) workgroups, the size of the partials' area. Measured on MI355X
+// (0.6B prefill from position 0, same box, against one workgroup per query block): prompt 300 3.11
+// -> 3.05 ms, 512 3.47 -> 3.30, 1024 4.76 -> 4.33, 2048 7.05 -> 6.63; 1.7B 512 6.14 -> 5.92, 1500
+// 12.96 -> 12.60; prompt 100 (2 key blocks) 2.84 -> 2.93 with chunks, hence the 2-block margin.
+struct AttnPlan {
+  int chunk, wgs, merge;  // key blocks per chunk (0: none), attn_kernel and attn_merge_kernel workgroups
+};
+static AttnPlan attn_plan(int M, int position) {
+  const int nqb = (M + QB - 1) / QB;
+  long long U = 0;
+  for (int qb = 0; qb < nqb; ++qb) U += attn_nkb(qb, M, position);
+  const int T = (int)((U + 31) / 32), maxn = attn_nkb(nqb - 1, M, position);
+  if (4 * maxn < 5 * T || maxn < T + 2) return {0, nqb * HKV, 0};
+  int wgs = 0;
+  for (int c = 0;; ++c) {
+    const int n = attn_round(c, T, M, position, nqb);
+    if (n == 0) break;
+    wgs += n;
+  }
+  return {T, wgs * HKV, attn_round(1, T, M, position, nqb) * HKV * 8};
+}
+static size_t attn_part_slots(int M) { return (size_t)HKV * (32 + (M + QB - 1) / QB); }
+static int attn_part_rows(int M) { return M < QB ? M : QB; }
 
 // ------------------------------------------------------------------------------------------------
 // Final RMSNorm of row `row` of x (the prompt's last token) and the tied LM head with fused greedy
@@ -1243,6 +1390,7 @@ struct Work {
   uint16_t *ah, *al, *bh, *bl, *qh, *ql;
   float* raw;   // short prompts: Q/K/V row sums [M][4096]
   float* part;  // split-K partials of the O and down products [splits][M][H]
+  float* apart; // the attention's key-range chunk partials (attn_plan)
   u64* keys;
   int32_t* bad;
 };
@@ -1272,7 +1420,7 @@ static int resid_splits(int H, int M, int K) {
 // rounded up to MT); q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums; the split-K partials of
 // the residual products; the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
-  size_t x, ah, al, bh, bl, qh, ql, raw, part, keys, bad, bytes;
+  size_t x, ah, al, bh, bl, qh, ql, raw, part, apart, keys, bad, bytes;
 };
 static Layout layout(int H, int I, int M) {
   const size_t A = H > HQ * D ? H : HQ * D;
@@ -1291,6 +1439,7 @@ static Layout layout(int H, int I, int M) {
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
   const int sp = M <= SMALL_M ? 3 : (so > sd ? so : sd);
   L.part = take(sp > 1 ? (size_t)sp * M * H * 4 : 0);
+  L.apart = take(attn_part_slots(M) * 2 * attn_part_rows(M) * APS * 4);
   L.keys = take(8);
   L.bad = take(4);
   L.bytes = o;
@@ -1308,6 +1457,7 @@ static Work carve(void* base, const Layout& L) {
   w.ql = reinterpret_cast<uint16_t*>(p + L.ql);
   w.raw = reinterpret_cast<float*>(p + L.raw);
   w.part = reinterpret_cast<float*>(p + L.part);
+  w.apart = reinterpret_cast<float*>(p + L.apart);
   w.keys = reinterpret_cast<u64*>(p + L.keys);
   w.bad = reinterpret_cast<int32_t*>(p + L.bad);
   return w;
@@ -1327,8 +1477,11 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     if ((e = hipGetLastError()) != hipSuccess) return e;  \
   } while (0)
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad);
-  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M > SMALL_M ? 1 : 0, M, 0, position, kv, wk.bad};
-  const dim3 attn_grid((M + QB - 1) / QB * HKV);
+  const AttnPlan ap = attn_plan(M, position);
+  if ((size_t)ap.wgs > attn_part_slots(M)) return hipErrorInvalidValue;  // cannot happen (see attn_plan)
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M > SMALL_M ? 1 : 0, M, 0, position, kv, wk.bad,
+                     wk.apart, ap.chunk, attn_part_rows(M)};
+  const dim3 attn_grid(ap.wgs);
   if (M <= SMALL_M) {
     // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
     // weight rows per workgroup, 256 to 384 workgroups), the O and down products split over K into
@@ -1352,6 +1505,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       AttnArgs at = at0;
       at.layer = l;
       MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
+      if (ap.merge) MKP_LAUNCH(attn_merge_kernel, dim3(ap.merge), dim3(256), 0, st, at);
       SkArgs o{};
       o.xh = wk.ah; o.xl = wk.al; o.ldx = A; o.B = M; o.N = H; o.K = HQ * D;
       o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = wk.part;
@@ -1391,6 +1545,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     AttnArgs at = at0;
     at.layer = l;
     MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
+    if (ap.merge) MKP_LAUNCH(attn_merge_kernel, dim3(ap.merge), dim3(256), 0, st, at);
     GemmArgs go{};
     go.ah = wk.ah; go.al = wk.al; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H; go.part = so > 1 ? wk.part : nullptr;

@@ -40,6 +40,9 @@ def main(argv=None):
     ap.add_argument("--batch", default="", help="comma-separated batch sizes (1..64)")
     ap.add_argument("--context", type=int, default=256, help="position of every sequence of a decode batch")
     ap.add_argument("--max-seq", type=int, default=4096)
+    ap.add_argument("--offset", type=int, default=0,
+                    help="prefill at this position: the prompt continues a cache of that many positions (a later "
+                         "chunk of a longer prompt)")
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--engine", type=int, default=0, choices=(0, 1, 2),
@@ -65,15 +68,16 @@ def main(argv=None):
     vocab = embed.shape[0]
     gen = torch.Generator().manual_seed(1)
     for P in [int(x) for x in a.prefill.split(",") if x]:
-        if P > a.max_seq:
-            sys.exit(f"prompt {P} exceeds --max-seq {a.max_seq}")
+        if a.offset + P > a.max_seq:
+            sys.exit(f"offset {a.offset} + prompt {P} exceeds --max-seq {a.max_seq}")
         kc, vc = megakernel.empty_cache(L, a.max_seq, dev)
         ids = torch.randint(0, vocab, (P,), generator=gen).to(dev, torch.int32)
-        med, runs = _time(lambda: kernel.prefill(ids, embed, embed, fn, lw, cos, sin, kc, vc, 0, a.max_seq),
+        med, runs = _time(lambda: kernel.prefill(ids, embed, embed, fn, lw, cos, sin, kc, vc, a.offset, a.max_seq),
                           a.warmup, a.runs)
-        print(f"[prefill {a.shape} P={P}] {med:.3f} ms median of {len(runs)} ({P / med * 1e3:,.0f} tokens/s); "
+        at = f" at {a.offset}" if a.offset else ""
+        print(f"[prefill {a.shape} P={P}{at}] {med:.3f} ms median of {len(runs)} ({P / med * 1e3:,.0f} tokens/s); "
               f"runs {[round(t, 3) for t in runs]}", flush=True)
-        if a.transformers:
+        if a.transformers and not a.offset:
             gpu_model = model.to(dev)
             ids2 = ids.long().unsqueeze(0)
 

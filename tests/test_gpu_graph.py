@@ -1,5 +1,5 @@
 """HIP-graph capture of the multi-kernel entry points: the batched prefill (``prefill``, both of its
-regimes) and the batched decode (``decode_batch``, the layer-by-layer engine and the persistent
+regimes, and at 300 tokens with the attention cut into key-range chunks and merged) and the batched decode (``decode_batch``, the layer-by-layer engine and the persistent
 kernel), captured with ``torch.cuda.graph`` after an eager call and replayed several times. Between
 replays the test restores the inputs the call mutates (the caches) with eager kernels and runs
 unrelated eager work, then checks every replay bit for bit against the eager result: the graph must
@@ -40,7 +40,7 @@ def _unrelated_eager_work():
     return float((x * 2).sum().item())
 
 
-@pytest.mark.parametrize("P", [24, 100], ids=["skinny-path", "tile-path"])
+@pytest.mark.parametrize("P", [24, 100, 300], ids=["skinny-path", "tile-path", "tile-path-key-chunks"])
 def test_prefill_graph_replays_match_eager(mini, P):
     s = mini.shape
     ids = torch.randint(0, s.vocab, (P,), generator=torch.Generator().manual_seed(7), dtype=torch.int64)

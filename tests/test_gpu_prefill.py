@@ -93,16 +93,22 @@ def test_prefill_matches_oracle(shape_fixture, P, request):
     assert sess.kernel.status() == 0
 
 
-def test_prefill_in_chunks_and_decode_after_it(mini):
-    """A prompt fed in three chunks (positions 0, 40, 75) gives the cache and last logits of the
-    one-shot oracle prefill; a decode step after it (the decode kernel, reading the prefilled
-    cache) matches the oracle's decode step on the oracle's cache."""
-    P = 100
+@pytest.mark.parametrize("shape_fixture, cuts", [("mini", (0, 40, 75, 100)), ("mini_4k", (0, 900, 964, 1000))],
+                         ids=["chunks-40-75", "chunks-900-964"])
+def test_prefill_in_chunks_and_decode_after_it(shape_fixture, cuts, request):
+    """A prompt fed in three chunks gives the cache and last logits of the one-shot oracle prefill;
+    a decode step after it (the decode kernel, reading the prefilled cache) matches the oracle's
+    decode step on the oracle's cache. The chunks at 900 and 964 are short prompts (64 and 36
+    tokens) over 16 key blocks each: their attention runs as key-range chunks of one block on 128
+    workgroups, merged by attn_merge_kernel; the first chunk (900 tokens) as chunks of 4 key
+    blocks."""
+    mini = request.getfixturevalue(shape_fixture)
+    P = cuts[-1]
     ids = hf.prompt_ids(P, mini.shape.vocab, seed=4)[0].tolist()
     s = mini.shape
     kd = torch.zeros(s.layers, s.kv_heads, mini.max_seq, s.head_dim, dtype=torch.bfloat16, device=DEV)
     vd = torch.zeros_like(kd)
-    for a, b in ((0, 40), (40, 75), (75, P)):
+    for a, b in zip(cuts[:-1], cuts[1:]):
         logits, tok = _prefill(mini, ids[a:b], kd, vd, a)
     want, kw, vw = restate.prefill(mini.W, ids, mini.cos_cpu, mini.sin_cpu, mini.max_seq)
     maxabs, _ = stats(logits.cpu(), want)
@@ -227,6 +233,7 @@ def _pool(sess, ps, extra, seed):
     ("mini", ((0, 300),), 16),                     # 128-row tiles, residual products split over K
     ("mini17", ((0, 200),), 64),
     ("mini", ((0, 40), (40, 75), (75, 100)), 32),  # chunks reading earlier chunks through the table
+    ("mini_4k", ((0, 900), (900, 964), (964, 1000)), 64),  # attention as key-range chunks, merged
 ])
 def test_paged_prefill_matches_contiguous(shape_fixture, chunks, ps, request):
     """``prefill_paged`` (C ABI ``mk_prefill_paged``) into a pool of pages in shuffled order, the pool
