@@ -146,7 +146,12 @@ struct GemmSmem {
   };
 };
 
-template <int EPI>
+// PF: K steps of operands in flight. 1: the next step's loads are issued as a step's MFMAs start
+// (two workgroups per CU hide each other's load latency). PF > 1 for grids of at most one workgroup
+// per CU (short prompts), where a lone workgroup otherwise waits out most of each load round trip:
+// PF steps are loaded ahead in registers (a clamped re-load of the last step past the end, so that
+// every step issues the same loads and each wait covers exactly its own step).
+template <int EPI, int PF = 1>
 __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) GemmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -184,15 +189,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
       }
   };
   // weights: global -> registers -> LDS, 4 chunks of 16 bytes per thread (row c / 8, chunk c % 8)
-  uint4 rw[4];
-  auto load_w = [&](int k0) {
+  typedef uint4 WStep[4];
+  auto load_w = [&](int k0, WStep& rw) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
       rw[i] = ld_stream(reinterpret_cast<const uint4*>(weight_row<EPI>(g, tn, row) + k0 + 8 * ch));
     }
   };
-  auto store_w = [&]() {
+  auto store_w = [&](const WStep& rw) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
@@ -207,24 +212,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
     for (int bn = 0; bn < 8; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kspan = g.K / gridDim.z, kb = blockIdx.z * kspan, ke = kb + kspan;  // a multiple of KT
-  AStep an, ac;
-  load_w(kb);
-  load_a(kb, an);
-  for (int k0 = kb; k0 < ke; k0 += KT) {
-    __syncthreads();  // every wave is done with the previous step's weight tile
-    store_w();
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm) {
-        ac[s][bm][0] = an[s][bm][0];
-        ac[s][bm][1] = an[s][bm][1];
-      }
-    if (k0 + KT < ke) {
-      load_w(k0 + KT);
-      load_a(k0 + KT, an);
-    }
+  auto step = [&](const AStep& ac) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < KT / 32; ++s) {
       uint4 fw[8];
@@ -237,6 +225,60 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
           acc[bm][bn] = mfma(ac[s][bm][0], fw[bn], acc[bm][bn]);
           acc[bm][bn] = mfma(ac[s][bm][1], fw[bn], acc[bm][bn]);
         }
+    }
+  };
+  if constexpr (PF == 1) {
+    AStep an, ac;
+    WStep rw;
+    load_w(kb, rw);
+    load_a(kb, an);
+    for (int k0 = kb; k0 < ke; k0 += KT) {
+      __syncthreads();  // every wave is done with the previous step's weight tile
+      store_w(rw);
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int bm = 0; bm < 2; ++bm) {
+          ac[s][bm][0] = an[s][bm][0];
+          ac[s][bm][1] = an[s][bm][1];
+        }
+      if (k0 + KT < ke) {
+        load_w(k0 + KT, rw);
+        load_a(k0 + KT, an);
+      }
+      step(ac);
+    }
+  } else {
+    // the K range is a multiple of PF steps (host); step i + PF's loads go out as step i starts
+    AStep aq[PF];
+    WStep wq[PF];
+    const int klast = ke - KT;
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int k = min(kb + p * KT, klast);
+      load_w(k, wq[p]);
+      load_a(k, aq[p]);
+    }
+    for (int k0 = kb; k0 < ke; k0 += PF * KT) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        __syncthreads();  // every wave is done with the previous step's weight tile
+        store_w(wq[p]);
+        __syncthreads();
+        AStep ac;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int bm = 0; bm < 2; ++bm) {
+            ac[s][bm][0] = aq[p][s][bm][0];
+            ac[s][bm][1] = aq[p][s][bm][1];
+          }
+        const int kn = min(k0 + (p + PF) * KT, klast);
+        load_w(kn, wq[p]);
+        load_a(kn, aq[p]);
+        step(ac);
+      }
     }
   }
 
@@ -1463,6 +1505,32 @@ static Work carve(void* base, const Layout& L) {
   return w;
 }
 
+// K steps in flight (gemm_kernel's PF) of a launch: up to GEMM_PF_MAX when the grid holds at most
+// GEMM_PF_WGS workgroups (one per CU), the largest power of two that divides the steps.
+#ifndef MKP_GEMM_PF_MAX
+#define MKP_GEMM_PF_MAX 4
+#endif
+#ifndef MKP_GEMM_PF_WGS
+#define MKP_GEMM_PF_WGS 256
+#endif
+constexpr int GEMM_PF_MAX = MKP_GEMM_PF_MAX, GEMM_PF_WGS = MKP_GEMM_PF_WGS;
+static int gemm_pf(dim3 grid, int K) {
+  const int steps = K / (int)grid.z / KT;
+  if ((int)(grid.x * grid.y * grid.z) > GEMM_PF_WGS) return 1;
+  for (int pf = GEMM_PF_MAX; pf > 1; pf /= 2)
+    if (steps % pf == 0) return pf;
+  return 1;
+}
+template <int EPI>
+static hipError_t launch_gemm(dim3 grid, const GemmArgs& g, hipStream_t st) {
+  switch (gemm_pf(grid, g.K)) {
+    case 4: hipLaunchKernelGGL((gemm_kernel<EPI, 4>), grid, dim3(256), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<EPI, 2>), grid, dim3(256), 0, st, g); break;
+    default: hipLaunchKernelGGL((gemm_kernel<EPI, 1>), grid, dim3(256), 0, st, g); break;
+  }
+  return hipGetLastError();
+}
+
 template <int H, int I>
 static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, int position, const uint16_t* embed,
                       const uint16_t* lm_head, const uint16_t* final_norm, const mk_layer_weights* layers,
@@ -1541,7 +1609,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     g.q_norm = (const uint16_t*)lw.q_norm_weight; g.k_norm = (const uint16_t*)lw.k_norm_weight;
     g.cos_tab = cos_tab; g.sin_tab = sin_tab; g.qh = wk.qh; g.ql = wk.ql; g.k_cache = k_cache; g.v_cache = v_cache;
     g.layer = l; g.position = position; g.kv = kv; g.bad = wk.bad;
-    MKP_LAUNCH(gemm_kernel<EPI_QKV>, dim3(g.N / NT, mtiles), dim3(256), 0, st, g);
+    if ((e = launch_gemm<EPI_QKV>(dim3(g.N / NT, mtiles), g, st)) != hipSuccess) return e;
     AttnArgs at = at0;
     at.layer = l;
     MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
@@ -1549,18 +1617,18 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     GemmArgs go{};
     go.ah = wk.ah; go.al = wk.al; go.M = M; go.N = H; go.K = HQ * D;
     go.w0 = (const uint16_t*)lw.o_proj_weight; go.x = wk.x; go.ldx = H; go.part = so > 1 ? wk.part : nullptr;
-    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, so), dim3(256), 0, st, go);
+    if ((e = launch_gemm<EPI_RESID>(dim3(H / NT, mtiles, so), go, st)) != hipSuccess) return e;
     MKP_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
                so > 1 ? so : 0, (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
     GemmArgs gu{};
     gu.ah = wk.ah; gu.al = wk.al; gu.M = M; gu.N = 2 * I; gu.K = H;
     gu.w0 = (const uint16_t*)lw.gate_proj_weight; gu.w1 = (const uint16_t*)lw.up_proj_weight;
     gu.bh = wk.bh; gu.bl = wk.bl;
-    MKP_LAUNCH(gemm_kernel<EPI_SILU>, dim3(I / (NT / 2), mtiles), dim3(256), 0, st, gu);
+    if ((e = launch_gemm<EPI_SILU>(dim3(I / (NT / 2), mtiles), gu, st)) != hipSuccess) return e;
     GemmArgs gd{};
     gd.ah = wk.bh; gd.al = wk.bl; gd.M = M; gd.N = H; gd.K = I;
     gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H; gd.part = sd > 1 ? wk.part : nullptr;
-    MKP_LAUNCH(gemm_kernel<EPI_RESID>, dim3(H / NT, mtiles, sd), dim3(256), 0, st, gd);
+    if ((e = launch_gemm<EPI_RESID>(dim3(H / NT, mtiles, sd), gd, st)) != hipSuccess) return e;
   }
   if (M > SMALL_M && sd > 1)  // the last layer's down partials into the residual
     MKP_LAUNCH(bnorm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
