@@ -1121,6 +1121,13 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
+  // the norm weights first: their loads then overlap the residual's instead of following the
+  // reduction (one round trip fewer per call)
+  uint4 wr[E / 8];
+  if (w) {
+#pragma unroll
+    for (int k = 0; k < E; k += 8) wr[k / 8] = *reinterpret_cast<const uint4*>(w + E * lane + k);
+  }
   float v[E];
   float* xr = x + (size_t)b * H + E * lane;
   if (tokens) {
@@ -1176,7 +1183,7 @@ __global__ void __launch_bounds__(256) bnorm_kernel(float* x, const int32_t* tok
 #pragma unroll
   for (int k = 0; k < E; k += 8) {
     float wv[8], y[8];
-    unpack8(*reinterpret_cast<const uint4*>(w + E * lane + k), wv);
+    unpack8(wr[k / 8], wv);
 #pragma unroll
     for (int q = 0; q < 8; ++q) y[q] = v[k + q] * wv[q] * rs;
     uint4 hi, lo;
@@ -1393,14 +1400,51 @@ __global__ void __launch_bounds__(128) battn_merge_kernel(const float* part, int
                                                           int max_seq, uint16_t* oh, uint16_t* ol, int ldo) {
   const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
   const int kvh = h >> 1, hh = h & 1;
-  const int ns = (seq_pos(positions, b, max_seq, nullptr) + KS) / KS;  // ceil((pos + 1) / KS)
+  const int pos = seq_pos(positions, b, max_seq, nullptr);
   const float* p = part + (((size_t)b * HKV + kvh) * S * 2 + hh) * APW;
+  // The first NB splits' words are loaded together with the position (one round trip instead of one
+  // per split and pass); those past the sequence's split count are read (inside the S allocated
+  // slots) but never used.
+  constexpr int NB = 16;
+  float mv[NB], lv[NB], av[NB];
+  {
+    // lane l of each wave loads split l % NB's (m, l) pair (vector loads, issued with the rest), then
+    // every lane reads them off lanes 0..NB-1
+    const int sl = d & (NB - 1);
+    const float2 ml = *reinterpret_cast<const float2*>(p + (size_t)(sl < S ? sl : 0) * 2 * APW + D);
+#pragma unroll
+    for (int s = 0; s < NB; ++s) av[s] = p[(size_t)(s < S ? s : 0) * 2 * APW + d];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      mv[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml.x), s));
+      lv[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml.y), s));
+    }
+  }
+  const int ns = (pos + KS) / KS;  // ceil((pos + 1) / KS)
+  // max first over the first NB splits, then their weighted sums in split order (selects, not
+  // branches, so that no loop separates the loads above from their use)
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, p[(size_t)s * 2 * APW + D]);
+#pragma unroll
+  for (int s = 0; s < NB; ++s) M = fmaxf(M, s < ns ? mv[s] : -INFINITY);
   float A = 0.f, Ls = 0.f;
-  for (int s = 0; s < ns; ++s) {
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
+    const bool in = s < ns;
+    const float f = in ? __expf(mv[s] - M) : 0.f;
+    A = in ? fmaf(av[s], f, A) : A;
+    Ls = in ? fmaf(lv[s], f, Ls) : Ls;
+  }
+  // splits past NB (caches longer than NB * KS keys): online, rescaling the sums to a new maximum
+  for (int s = NB; s < ns; ++s) {
     const float* q = p + (size_t)s * 2 * APW;
-    const float f = __expf(q[D] - M);
+    const float m = q[D];
+    if (m > M) {
+      const float c = __expf(M - m);
+      A *= c;
+      Ls *= c;
+      M = m;
+    }
+    const float f = __expf(m - M);
     A = fmaf(q[d], f, A);
     Ls = fmaf(q[D + 1], f, Ls);
   }
