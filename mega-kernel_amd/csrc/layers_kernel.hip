@@ -402,7 +402,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 //   Work split: a workgroup (8 waves) takes one K/V head and one 64-query block, the blocks with
 //   the most keys dispatched first (workgroups 0-7 take the last block of each head), so the CUs
 //   that finish short blocks pick up the rest. (Pairs of blocks i and nqb - 1 - i per workgroup balanced the
-//   work too, but left 32 of the 256 CUs idle at 3,584 tokens: 224 workgroups.) Waves 0-3 take
+//   work too, but left 32 of the 256 CUs idle at 3,584 tokens: 224 workgroups.) Where the blocks'
+//   key chains are uneven against the grid (attn_plan), a workgroup takes one key-range chunk of a
+//   block instead and attn_merge_kernel combines the chunks. Waves 0-3 take
 //   query head 2 kvh, waves 4-7 head 2 kvh + 1, 16 queries each: the two heads of a GQA pair share
 //   each K/V block staged in LDS.
 //   Pipeline: the next K/V block is loaded into registers while the current one is multiplied,
