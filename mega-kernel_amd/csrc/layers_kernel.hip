@@ -18,8 +18,8 @@
 //               m = silu(a . Wg^T) * (a . Wu^T)        (gemm, EPI_SILU: gate and up rows in one tile)
 //               x += m . Wd^T                          (gemm, EPI_RESID)
 //   logits of the last row = RMSNorm(x) . E^T, greedy token (lm_head_kernel, fused argmax)
-// When the residual products' tile grid is small (prompts up to ~1000 tokens) they are split over K
-// into partials that the next norm adds in a fixed order. Prompts of at most SMALL_M tokens run the
+// When the residual products' tile grid is small (below 192 tiles) they are split over K into
+// partials that the next norm adds in a fixed order. Prompts of at most small_m(H) tokens run the
 // products on the skinny kernels of the batched decode instead (weights as the MFMA A operand).
 //
 // Numerics are the decode kernel's (the reference kernel's fp32 design, /root/reference/
@@ -1483,13 +1483,15 @@ struct Work {
   int32_t* bad;
 };
 
-// Prompts of at most SMALL_M tokens run their products on the skinny kernels (weights as the MFMA A
-// operand, the tokens as up to 8 column blocks); longer ones on 128 x 128 tiles.
-constexpr int SMALL_M = 64;
+// Prompts of at most small_m(H) tokens run their products on the skinny kernels (weights as the
+// MFMA A operand, the tokens as up to 8 column blocks); longer ones on 128 x 128 tiles. Measured on
+// MI355X (same box, ms per prefill, skinny / tiles): 0.6B 40 tokens 1.93 / 2.45, 48 2.08 / 2.44, 64
+// 2.38 / 2.46; 1.7B 48 tokens 3.73 / 4.01, 64 4.36 / 3.97.
+static int small_m(int H) { return H <= 1024 ? 64 : 48; }
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// K splits of a residual product (O or down, N = H columns) on 128 x 128 tiles for M > SMALL_M:
+// K splits of a residual product (O or down, N = H columns) on 128 x 128 tiles for M > small_m(H):
 // as many as keep the grid within one workgroup per CU (the grid then takes gemm_kernel's deeper
 // pipeline), none from 192 tiles on, at most 8, each K range a whole number of 64-wide steps. The
 // partials are added to the residual by the next norm, in split order; without a split the
@@ -1498,7 +1500,7 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // 12.36 ms, 1.7B prompt 512 / 1,500 5.95 / 13.04 -> 5.47 / 12.77 ms, 2,048 unchanged.
 static int resid_splits(int H, int M, int K) {
   const int tiles = (H / NT) * ((M + MT - 1) / MT);
-  if (M <= SMALL_M || tiles >= 192) return 1;
+  if (M <= small_m(H) || tiles >= 192) return 1;
   int sp = 256 / tiles;
   sp = sp < 8 ? sp : 8;
   while ((K / KT) % sp != 0) --sp;
@@ -1507,7 +1509,7 @@ static int resid_splits(int H, int M, int K) {
 
 // Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16, max(H, 2048) columns; b (hi, lo)
 // bf16, I columns (a and b: row-major for the skinny kernels, fragment-major for gemm_kernel, rows
-// rounded up to MT); q (hi, lo) bf16 [M][2048]; for M <= SMALL_M the raw Q/K/V sums; the split-K partials of
+// rounded up to MT); q (hi, lo) bf16 [M][2048]; for M <= small_m(H) the raw Q/K/V sums; the split-K partials of
 // the residual products; the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
   size_t x, ah, al, bh, bl, qh, ql, raw, part, apart, keys, bad, bytes;
@@ -1525,9 +1527,10 @@ static Layout layout(int H, int I, int M) {
   L.bl = take(MA * I * 2);
   L.qh = take((size_t)M * HQ * D * 2);
   L.ql = take((size_t)M * HQ * D * 2);
-  L.raw = take(M <= SMALL_M ? (size_t)M * (HQ + 2 * HKV) * D * 4 : 0);
+  const bool small = M <= small_m(H);
+  L.raw = take(small ? (size_t)M * (HQ + 2 * HKV) * D * 4 : 0);
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
-  const int sp = M <= SMALL_M ? 3 : (so > sd ? so : sd);
+  const int sp = small ? 3 : (so > sd ? so : sd);
   L.part = take(sp > 1 ? (size_t)sp * M * H * 4 : 0);
   L.apart = take(attn_part_slots(M) * 2 * attn_part_rows(M) * APS * 4);
   L.keys = take(8);
@@ -1595,10 +1598,11 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   MKP_LAUNCH(keys_init_kernel, dim3(1), dim3(64), 0, st, wk.keys, 1, wk.bad);
   const AttnPlan ap = attn_plan(M, position);
   if ((size_t)ap.wgs > attn_part_slots(M)) return hipErrorInvalidValue;  // cannot happen (see attn_plan)
-  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, M > SMALL_M ? 1 : 0, M, 0, position, kv, wk.bad,
+  const bool small = M <= small_m(H);
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, small ? 0 : 1, M, 0, position, kv, wk.bad,
                      wk.apart, ap.chunk, attn_part_rows(M)};
   const dim3 attn_grid(ap.wgs);
-  if (M <= SMALL_M) {
+  if (small) {
     // Short prompts: the products are weight-bandwidth bound, so they run on the skinny kernels (16
     // weight rows per workgroup, 256 to 384 workgroups), the O and down products split over K into
     // partials that the next norm adds to the residual in a fixed order.
@@ -1645,7 +1649,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   // Longer prompts: 128 x 128 tiles with the epilogues fused; the residual products split over K
   // into partials when their tile grid is small (the norm after them adds the partials).
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
-  for (int l = 0; M > SMALL_M && l < dims.num_layers; ++l) {
+  for (int l = 0; !small && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
     const dim3 rows((M + 3) / 4);
     MKP_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab,
@@ -1678,7 +1682,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H; gd.part = sd > 1 ? wk.part : nullptr;
     if ((e = launch_gemm<EPI_RESID>(dim3(H / NT, mtiles, sd), gd, st)) != hipSuccess) return e;
   }
-  if (M > SMALL_M && sd > 1)  // the last layer's down partials into the residual
+  if (!small && sd > 1)  // the last layer's down partials into the residual
     MKP_LAUNCH(bnorm_kernel<H>, dim3((M + 3) / 4), dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part,
                sd, nullptr, nullptr, nullptr, A, M);
   // the last row's logits and greedy token
