@@ -902,12 +902,27 @@ __global__ void __launch_bounds__(256) logits_argmax_kernel(float* logits, int v
   float* row = logits + (size_t)b * vocab;
   const bool failed = *bad != 0;
   u64 k = 0;
-  for (int i = 0; i < 16; ++i) {
-    const int v = blockIdx.x * 4096 + i * 256 + tid;
+  // 16 logits per thread as four 16-byte loads issued together (vocab is a multiple of 16)
+  float4 x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int v = blockIdx.x * 4096 + i * 1024 + 4 * tid;
+    x[i] = v < vocab ? *reinterpret_cast<const float4*>(row + v) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int v = blockIdx.x * 4096 + i * 1024 + 4 * tid;
     if (v < vocab) {
-      const u64 kv = argmax_key(row[v], v);
-      k = k > kv ? k : kv;
-      if (failed) row[v] = __builtin_nanf("");
+      const float e[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u64 kv = argmax_key(e[q], v + q);
+        k = k > kv ? k : kv;
+      }
+      if (failed) {
+        const float n = __builtin_nanf("");
+        *reinterpret_cast<float4*>(row + v) = make_float4(n, n, n, n);
+      }
     }
   }
 #pragma unroll
