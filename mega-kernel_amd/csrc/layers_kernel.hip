@@ -93,7 +93,10 @@ __device__ __forceinline__ size_t frag_off(int m, int k, int K) {
 }
 static size_t frag_rows(int M) { return (size_t)(M + MT - 1) / MT * MT; }
 
-enum Epi { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2 };
+// EPI_QKV_PART / EPI_SILU_PART: the QKV / gate-up products split over K on small grids, each K range's
+// raw sums into part[blockIdx.z][M][N] (N = 4096 / 2 I, a tile's columns as in EPI_QKV / EPI_SILU);
+// qkv_post_kernel / silu_post_kernel add the ranges in order and finish the epilogue.
+enum Epi { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_QKV_PART = 3, EPI_SILU_PART = 4 };
 
 struct GemmArgs {
   const uint16_t* ah;  // fragment-major, K columns
@@ -128,11 +131,11 @@ struct GemmArgs {
 // first element of weight row r (0..127) of N-tile t
 template <int EPI>
 __device__ __forceinline__ const uint16_t* weight_row(const GemmArgs& g, int t, int r) {
-  if constexpr (EPI == EPI_QKV) {
+  if constexpr (EPI == EPI_QKV || EPI == EPI_QKV_PART) {
     if (t < HQ) return g.w0 + (size_t)(t * D + r) * g.K;
     if (t < HQ + HKV) return g.w1 + (size_t)((t - HQ) * D + r) * g.K;
     return g.w2 + (size_t)((t - HQ - HKV) * D + r) * g.K;
-  } else if constexpr (EPI == EPI_SILU) {  // gate rows then up rows of intermediates [64 t, 64 t + 64)
+  } else if constexpr (EPI == EPI_SILU || EPI == EPI_SILU_PART) {  // gate rows then up rows of intermediates [64 t, 64 t + 64)
     return r < NT / 2 ? g.w0 + (size_t)(t * (NT / 2) + r) * g.K : g.w1 + (size_t)(t * (NT / 2) + r - NT / 2) * g.K;
   } else {
     return g.w0 + (size_t)(t * NT + r) * g.K;
@@ -282,7 +285,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
     }
   }
 
-  if constexpr (EPI == EPI_RESID) {
+  if constexpr (EPI == EPI_RESID || EPI == EPI_QKV_PART || EPI == EPI_SILU_PART) {
     // x += C (or C into this K range's partial), each element owned by one lane
     auto each = [&](auto&& f) {
 #pragma unroll
@@ -1226,11 +1229,12 @@ __device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_
   return p;
 }
 
-// The raw Q/K/V sums of M consecutive prompt tokens of one sequence (fp32 [M][4096]; row m at
-// position pos0 + m): per-head RMSNorm + RoPE on q and k (one wave per row and head, lane l holding
+// The raw Q/K/V sums of M consecutive prompt tokens of one sequence (fp32 [M][4096], or S such arrays
+// of K-range sums added in order; row m at position pos0 + m): per-head RMSNorm + RoPE on q and k
+// (one wave per row and head, lane l holding
 // dims l and l + 64, the RoPE pair), q kept as a bf16 hi/lo pair [M][2048], k and v rounded to bf16
 // into the cache [L][8][max_seq][128].
-__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, int pos0, const uint16_t* q_norm,
+__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int S, int M, int pos0, const uint16_t* q_norm,
                                                        const uint16_t* k_norm, const uint16_t* cos_tab,
                                                        const uint16_t* sin_tab, uint16_t* qh, uint16_t* ql,
                                                        uint16_t* k_cache, uint16_t* v_cache, int layer, KvMap kv,
@@ -1240,8 +1244,14 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, 
   if (item >= M * (HQ + 2 * HKV)) return;
   const int b = item / (HQ + 2 * HKV), hd = item % (HQ + 2 * HKV);
   const int pos = pos0 + b;
+  // the sums of S K ranges (EPI_QKV_PART), added in order
+  const size_t rstride = (size_t)M * (HQ + 2 * HKV) * D;
   const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
   float u0 = r[lane], u1 = r[lane + 64];
+  for (int q = 1; q < S; ++q) {
+    u0 += r[q * rstride + lane];
+    u1 += r[q * rstride + lane + 64];
+  }
   const int page = hd >= HQ && kv.bt ? kv_page(kv, pos, lane == 0 ? bad : nullptr) : 0;
   auto cache_row = [&](uint16_t* cache, int kvh) { return cache + kv_row(kv, layer, kvh, pos, page); };
   if (hd >= HQ + HKV) {  // v
@@ -1270,6 +1280,41 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int M, 
     dst[lane] = f32_to_bf16(o0);
     dst[lane + 64] = f32_to_bf16(o1);
   }
+}
+
+// silu(gate) * up of M rows from the S K-range sums of EPI_SILU_PART (part[S][M][2 I]: tile t's
+// columns 128 t .. +63 the gate and 128 t + 64 .. +127 the up sums of intermediates 64 t .. +63),
+// added in order, into the down product's A operand (bf16 hi/lo, fragment-major, I columns), as
+// the EPI_SILU epilogue writes it. One thread per row and 8 intermediates.
+__global__ void __launch_bounds__(256) silu_post_kernel(const float* part, int S, int M, int I, uint16_t* bh,
+                                                        uint16_t* bl) {
+  const int nc = I / 8, idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * nc) return;
+  const int m = idx / nc, i0 = 8 * (idx % nc);
+  const size_t stride = (size_t)M * 2 * I;
+  const float* pg = part + (size_t)m * 2 * I + 128 * (i0 >> 6) + (i0 & 63);
+  float gt[8], up[8];
+  auto ld8 = [](const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  };
+  ld8(pg, gt);
+  ld8(pg + 64, up);
+  for (int q = 1; q < S; ++q) {
+    float g2[8], u2[8];
+    ld8(pg + q * stride, g2);
+    ld8(pg + q * stride + 64, u2);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { gt[k] += g2[k]; up[k] += u2[k]; }
+  }
+  float mv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mv[k] = gt[k] / (1.f + expf(-gt[k])) * up[k];  // silu(gate) * up (/root/reference/megakernel.cu:659-665)
+  uint4 hi, lo;
+  split8(mv, hi, lo);
+  const size_t o = frag_off(m, i0, I);
+  *reinterpret_cast<uint4*>(bh + o) = hi;
+  *reinterpret_cast<uint4*>(bl + o) = lo;
 }
 
 // Split-K attention of one sequence and K/V head over keys [KS s, KS s + KS) of [0, position]: the
@@ -1493,6 +1538,7 @@ struct Work {
   uint16_t *ah, *al, *bh, *bl, *qh, *ql;
   float* raw;   // short prompts: Q/K/V row sums [M][4096]
   float* part;  // split-K partials of the O and down products [splits][M][H]
+  float* qpart; // split-K partials of the QKV or gate/up product on small grids [splits][M][4096 or 2 I]
   float* apart; // the attention's key-range chunk partials (attn_plan)
   u64* keys;
   int32_t* bad;
@@ -1522,12 +1568,30 @@ static int resid_splits(int H, int M, int K) {
   return sp;
 }
 
+// K splits of the QKV or gate/up product (`tiles` 128 x 128 tiles, K = H) for M > small_m(H): on a
+// grid of at most 128 tiles, as many as keep it within 256 workgroups (one per CU, on gemm_kernel's
+// deeper pipeline), at most 8, each K range a whole number of 64-wide steps; qkv_post_kernel /
+// silu_post_kernel then add the ranges and do the epilogue the tiles would have fused.
+static int small_grid_splits(int tiles, int K) {
+  if (tiles > 128) return 1;
+  int sp = 256 / tiles;
+  sp = sp < 8 ? sp : 8;
+  while ((K / KT) % sp != 0) --sp;
+  return sp;
+}
+static int qkv_splits(int H, int M) {
+  return M <= small_m(H) ? 1 : small_grid_splits((HQ + 2 * HKV) * D / NT * ((M + MT - 1) / MT), H);
+}
+static int silu_splits(int H, int I, int M) {
+  return M <= small_m(H) ? 1 : small_grid_splits(I / (NT / 2) * ((M + MT - 1) / MT), H);
+}
+
 // Workspace layout for M rows: x fp32 [M][H]; a (hi, lo) bf16, max(H, 2048) columns; b (hi, lo)
 // bf16, I columns (a and b: row-major for the skinny kernels, fragment-major for gemm_kernel, rows
 // rounded up to MT); q (hi, lo) bf16 [M][2048]; for M <= small_m(H) the raw Q/K/V sums; the split-K partials of
 // the residual products; the argmax keys. Offsets in bytes, each 256-byte aligned.
 struct Layout {
-  size_t x, ah, al, bh, bl, qh, ql, raw, part, apart, keys, bad, bytes;
+  size_t x, ah, al, bh, bl, qh, ql, raw, part, qpart, apart, keys, bad, bytes;
 };
 static Layout layout(int H, int I, int M) {
   const size_t A = H > HQ * D ? H : HQ * D;
@@ -1547,6 +1611,10 @@ static Layout layout(int H, int I, int M) {
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
   const int sp = small ? 3 : (so > sd ? so : sd);
   L.part = take(sp > 1 ? (size_t)sp * M * H * 4 : 0);
+  const int sq = qkv_splits(H, M), su = silu_splits(H, I, M);
+  size_t qp = sq > 1 ? (size_t)sq * M * (HQ + 2 * HKV) * D : 0;
+  if (su > 1 && (size_t)su * M * 2 * I > qp) qp = (size_t)su * M * 2 * I;
+  L.qpart = take(qp * 4);
   L.apart = take(attn_part_slots(M) * 2 * attn_part_rows(M) * APS * 4);
   L.keys = take(8);
   L.bad = take(4);
@@ -1565,6 +1633,7 @@ static Work carve(void* base, const Layout& L) {
   w.ql = reinterpret_cast<uint16_t*>(p + L.ql);
   w.raw = reinterpret_cast<float*>(p + L.raw);
   w.part = reinterpret_cast<float*>(p + L.part);
+  w.qpart = reinterpret_cast<float*>(p + L.qpart);
   w.apart = reinterpret_cast<float*>(p + L.apart);
   w.keys = reinterpret_cast<u64*>(p + L.keys);
   w.bad = reinterpret_cast<int32_t*>(p + L.bad);
@@ -1634,7 +1703,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
       q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = wk.raw;
       if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
-      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, M, position,
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, 1, M, position,
                  (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
                  k_cache, v_cache, l, kv, wk.bad);
       AttnArgs at = at0;
@@ -1664,6 +1733,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   // Longer prompts: 128 x 128 tiles with the epilogues fused; the residual products split over K
   // into partials when their tile grid is small (the norm after them adds the partials).
   const int so = resid_splits(H, M, HQ * D), sd = resid_splits(H, M, I);
+  const int sq = qkv_splits(H, M), su = silu_splits(H, I, M);
   for (int l = 0; !small && l < dims.num_layers; ++l) {
     const mk_layer_weights& lw = layers[l];
     const dim3 rows((M + 3) / 4);
@@ -1676,7 +1746,16 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     g.q_norm = (const uint16_t*)lw.q_norm_weight; g.k_norm = (const uint16_t*)lw.k_norm_weight;
     g.cos_tab = cos_tab; g.sin_tab = sin_tab; g.qh = wk.qh; g.ql = wk.ql; g.k_cache = k_cache; g.v_cache = v_cache;
     g.layer = l; g.position = position; g.kv = kv; g.bad = wk.bad;
-    if ((e = launch_gemm<EPI_QKV>(dim3(g.N / NT, mtiles), g, st)) != hipSuccess) return e;
+    if (sq > 1) {
+      GemmArgs gq = g;
+      gq.part = wk.qpart;
+      if ((e = launch_gemm<EPI_QKV_PART>(dim3(g.N / NT, mtiles, sq), gq, st)) != hipSuccess) return e;
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.qpart, sq, M, position,
+                 (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
+                 k_cache, v_cache, l, kv, wk.bad);
+    } else if ((e = launch_gemm<EPI_QKV>(dim3(g.N / NT, mtiles), g, st)) != hipSuccess) {
+      return e;
+    }
     AttnArgs at = at0;
     at.layer = l;
     MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
@@ -1691,7 +1770,14 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     gu.ah = wk.ah; gu.al = wk.al; gu.M = M; gu.N = 2 * I; gu.K = H;
     gu.w0 = (const uint16_t*)lw.gate_proj_weight; gu.w1 = (const uint16_t*)lw.up_proj_weight;
     gu.bh = wk.bh; gu.bl = wk.bl;
-    if ((e = launch_gemm<EPI_SILU>(dim3(I / (NT / 2), mtiles), gu, st)) != hipSuccess) return e;
+    if (su > 1) {
+      GemmArgs gp = gu;
+      gp.part = wk.qpart;
+      if ((e = launch_gemm<EPI_SILU_PART>(dim3(I / (NT / 2), mtiles, su), gp, st)) != hipSuccess) return e;
+      MKP_LAUNCH(silu_post_kernel, dim3((M * (I / 8) + 255) / 256), dim3(256), 0, st, wk.qpart, su, M, I, wk.bh, wk.bl);
+    } else if ((e = launch_gemm<EPI_SILU>(dim3(I / (NT / 2), mtiles), gu, st)) != hipSuccess) {
+      return e;
+    }
     GemmArgs gd{};
     gd.ah = wk.bh; gd.al = wk.bl; gd.M = M; gd.N = H; gd.K = I;
     gd.w0 = (const uint16_t*)lw.down_proj_weight; gd.x = wk.x; gd.ldx = H; gd.part = sd > 1 ? wk.part : nullptr;
