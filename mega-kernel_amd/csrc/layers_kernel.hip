@@ -1545,10 +1545,11 @@ struct Work {
 };
 
 // Prompts of at most small_m(H) tokens run their products on the skinny kernels (weights as the
-// MFMA A operand, the tokens as up to 8 column blocks); longer ones on 128 x 128 tiles. Measured on
-// MI355X (same box, ms per prefill, skinny / tiles): 0.6B 40 tokens 1.93 / 2.45, 48 2.08 / 2.44, 64
-// 2.38 / 2.46; 1.7B 48 tokens 3.73 / 4.01, 64 4.36 / 3.97.
-static int small_m(int H) { return H <= 1024 ? 64 : 48; }
+// MFMA A operand, the tokens as up to 4 column blocks); longer ones on 128 x 128 tiles (QKV and
+// gate/up split over K on small grids). Measured on MI355X (same box, ms per prefill, skinny /
+// tiles): 0.6B 24 tokens 1.51 / 1.81, 32 1.65 / 1.87, 33 1.84 / 1.87, 40 1.93 / 1.91, 64 2.39 / 2.01;
+// 1.7B 24 tokens 2.61 / 2.87, 32 2.94 / 2.93, 33 3.29 / 2.94, 48 3.74 / 3.01.
+static int small_m(int H) { (void)H; return 32; }
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 

@@ -63,17 +63,18 @@ def _check_cache(got, want, upto, tag):
     assert rel.max().item() <= 2 ** -8
 
 
-@pytest.mark.parametrize("shape_fixture, P", [("mini", 1), ("mini", 24), ("mini", 64), ("mini", 65), ("mini", 100),
-                                              ("mini", 300), ("mini17", 48), ("mini17", 64), ("mini17", 200), ("mini_4k", 1000),
+@pytest.mark.parametrize("shape_fixture, P", [("mini", 1), ("mini", 24), ("mini", 32), ("mini", 33), ("mini", 64),
+                                              ("mini", 65), ("mini", 100), ("mini", 300), ("mini17", 32),
+                                              ("mini17", 64), ("mini17", 200), ("mini_4k", 1000),
                                               ("mini_4k", 3000), ("mini17_2k", 1500)])
 def test_prefill_matches_oracle(shape_fixture, P, request):
     """Prefill from an empty cache against ``restate.prefill`` on the same prompt: the last token's
     logits and greedy token, every K/V row written, and nothing written past the prompt. P = 1 has
-    one key; P <= 64 at the 0.6B width and P <= 48 at the 1.7B width run the skinny products (64: all
-    8 column blocks), P = 65 (and 64 at 1.7B) the 128-row tiles (rows past the prompt dead, the
-    residual products split over K, 4 K steps in flight) and two attention query blocks, the second
-    with one row; P = 300 spans 5 query blocks of the attention (key-range chunks) and 3 row tiles
-    of the products. From 8 row tiles the residual products are placed row tile by row tile on the
+    one key; P <= 32 runs the skinny products (32: all 4 column blocks), P = 33 and 64 one 128-row
+    tile (rows past the prompt dead; QKV and gate/up split over K into raw sums that the post kernels
+    finish, the residual products split over K, several K steps in flight), P = 65 two attention
+    query blocks, the second with one row; P = 300 spans 5 query blocks of the attention (key-range
+    chunks) and 3 row tiles of the products. From 8 row tiles the residual products are placed row tile by row tile on the
     XCDs: P = 1000 (8 row tiles, 4-way K split), P = 3000 at the 0.6B width (24 row tiles, 192
     tiles: no split, one step in flight) and P = 1500 at the 1.7B width (12 row tiles of 16 column
     tiles: no split)."""
