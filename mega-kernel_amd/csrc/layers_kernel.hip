@@ -93,6 +93,32 @@ __device__ __forceinline__ size_t frag_off(int m, int k, int K) {
 }
 static size_t frag_rows(int M) { return (size_t)(M + MT - 1) / MT * MT; }
 
+// Activation operand of the skinny products in fragment order ("skinny fragments", used by the
+// batched decode): for column block cb (sequences 8 cb .. 8 cb + 7) and K block kb (32 inputs), one
+// 1 KB fragment holding, at lane l, MFMA column li = l % 16 (sequence 8 cb + li / 2, bf16 hi part for
+// even li, lo for odd) and inputs 32 kb + 8 (l / 16) .. + 8. A wave then loads a whole B operand as
+// 1 KB of consecutive bytes. In row order (B rows of ldx elements, hi and lo in two arrays) each lane
+// of such a load reads 16 bytes of a different row, and the vector cache takes one access per lane:
+// at 64 sequences that was the skinny products' bound (rocprof at 64 sequences: ~64 L1 accesses per
+// load instruction, TA address stalls). Rows past the batch are never written; their columns of the
+// products are never read.
+// Fragment order: with 2 or 4 column blocks (CB, skf_blocks) K-block major (the CB fragments of one
+// K block adjacent), with 8 column-block major (the K blocks of one column block adjacent). Every
+// workgroup of a product reads the same fragments at about the same time; measured on MI355X at
+// context 256 (layer by layer, per step), 16 / 32 / 64 sequences: column-block major 1744 / 2412 /
+// 2411 us, K-block major 1513 / 1994 / 2596, row order 1544 / 1979 / 2863.
+__host__ __device__ inline int skf_blocks(int B) { return B <= 8 ? 1 : B <= 16 ? 2 : B <= 32 ? 4 : 8; }
+__host__ __device__ inline size_t skf_frag(int cb, int kb, int CB, int K) {
+  return CB == 8 ? (size_t)cb * (K >> 5) + kb : (size_t)kb * CB + cb;
+}
+__host__ __device__ inline size_t skf_off(int b, int k, int part, int B, int K) {
+  const int cb = b >> 3, li = 2 * (b & 7) + part, kb = k >> 5, lg = (k & 31) >> 3;
+  return ((skf_frag(cb, kb, skf_blocks(B), K) * 64 + lg * 16 + li) << 3) + (k & 7);
+}
+// Elements of the skinny fragments of B rows: whole column blocks of the kernel that reads them (1,
+// 2, 4 or 8 blocks of 8 rows), hi and lo.
+__host__ __device__ inline size_t skf_elems(int B, int K) { return (size_t)skf_blocks(B) * 8 * K * 2; }
+
 // EPI_QKV_PART / EPI_SILU_PART: the QKV / gate-up products split over K on small grids, each K range's
 // raw sums into part[blockIdx.z][M][N] (N = 4096 / 2 I, a tile's columns as in EPI_QKV / EPI_SILU);
 // qkv_post_kernel / silu_post_kernel add the ranges in order and finish the epilogue.
@@ -433,9 +459,8 @@ struct AttnArgs {
   const uint16_t* ql;
   const uint16_t* k_cache;
   const uint16_t* v_cache;
-  uint16_t* oh;  // output rows [M][ldo], or with `frag` fragment-major with 16 * 128 columns
-  uint16_t* ol;
-  int ldo;
+  uint16_t* oh;  // output: frag 1 the GEMM's fragment order (frag_off, 16 * 128 columns; hi in oh, lo
+  uint16_t* ol;  // in ol), 2 the skinny products' fragments (skf_off, hi and lo both in oh)
   int frag;
   int M, layer, position;
   KvMap kv;
@@ -448,6 +473,12 @@ struct AttnArgs {
   int chunk, qr;
 };
 constexpr int APS = D + 4;  // floats per partial row: acc[128], m, l, pad (16-byte aligned rows)
+
+// Where the 8 output values of row m from column k (k % 8 == 0), part 0 (hi) or 1 (lo), go.
+__device__ __forceinline__ uint16_t* attn_out(const AttnArgs& a, int m, int k, int part) {
+  if (a.frag == 2) return a.oh + skf_off(m, k, part, a.M, HQ * D);
+  return (part ? a.ol : a.oh) + frag_off(m, k, HQ * D);
+}
 
 // Key blocks that query block qb attends to: keys [0, position + min(M, (qb + 1) QB)).
 __host__ __device__ inline int attn_nkb(int qb, int M, int position) {
@@ -718,8 +749,7 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
       const int c = lane + 64 * r, part = c >> 8, row = (c >> 4) & 15, ch = c & 15;
       const int m = q0 + wq + row;
       const uint4 v = *reinterpret_cast<const uint4*>(&sm.o[w][part][row][8 * ch]);
-      const size_t o = a.frag ? frag_off(m, h * D + 8 * ch, HQ * D) : (size_t)m * a.ldo + h * D + 8 * ch;
-      if (m < a.M) *reinterpret_cast<uint4*>((part ? a.ol : a.oh) + o) = v;
+      if (m < a.M) *reinterpret_cast<uint4*>(attn_out(a, m, h * D + 8 * ch, part)) = v;
     }
   }
 }
@@ -780,9 +810,8 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
   uint4 hi, lo;
   split8(o, hi, lo);
   const int h = 2 * kvh + hh;
-  const size_t off = a.frag ? frag_off(m, h * D + 8 * ch, HQ * D) : (size_t)m * a.ldo + h * D + 8 * ch;
-  *reinterpret_cast<uint4*>(a.oh + off) = hi;
-  *reinterpret_cast<uint4*>(a.ol + off) = lo;
+  *reinterpret_cast<uint4*>(attn_out(a, m, h * D + 8 * ch, 0)) = hi;
+  *reinterpret_cast<uint4*>(attn_out(a, m, h * D + 8 * ch, 1)) = lo;
 }
 
 // Chunk plan of the attention over a prompt of M tokens at `position`: chunk = ceil(U / 32) key
@@ -968,9 +997,7 @@ constexpr int KS = 64;  // keys per attention split (one round of 4 keys per 16-
 enum SkEpi { SK_RAW = 0, SK_PART = 1, SK_SILU = 2 };
 
 struct SkArgs {
-  const uint16_t* xh;  // activations [B][ldx], bf16 hi/lo
-  const uint16_t* xl;
-  int ldx;
+  const uint16_t* xh;  // activations as skinny fragments (skf_off: K inputs, hi and lo) of B rows
   int B, N, K;
   // SK_RAW: rows [0, n1) of w0, [n1, n2) of w1, [n2, N) of w2 (Q, K, V); SK_PART: w0; SK_SILU: w0 gate, w1 up
   const uint16_t* w0;
@@ -978,46 +1005,20 @@ struct SkArgs {
   const uint16_t* w2;
   int n1, n2;
   float* out;    // SK_RAW: [B][N]; SK_PART: [gridDim.y][B][N]
-  uint16_t* mh;  // SK_SILU: silu(gate) * up, bf16 hi/lo [B][ldm]
-  uint16_t* ml;
+  uint16_t* mh;  // SK_SILU: silu(gate) * up as skinny fragments of ldm inputs (the down product's operand)
   int ldm;
 };
 
-// Activation operand of the skinny products in fragment order ("skinny fragments", used by the
-// batched decode): for column block cb (sequences 8 cb .. 8 cb + 7) and K block kb (32 inputs), one
-// 1 KB fragment holding, at lane l, MFMA column li = l % 16 (sequence 8 cb + li / 2, bf16 hi part for
-// even li, lo for odd) and inputs 32 kb + 8 (l / 16) .. + 8. A wave then loads a whole B operand as
-// 1 KB of consecutive bytes. In row order (B rows of ldx elements, hi and lo in two arrays) each lane
-// of such a load reads 16 bytes of a different row, and the vector cache takes one access per lane:
-// at 64 sequences that was the skinny products' bound (rocprof at 64 sequences: ~64 L1 accesses per
-// load instruction, TA address stalls). Rows past the batch are never written; their columns of the
-// products are never read.
-// Fragment order: with 2 or 4 column blocks (CB, skf_blocks) K-block major (the CB fragments of one
-// K block adjacent), with 8 column-block major (the K blocks of one column block adjacent). Every
-// workgroup of a product reads the same fragments at about the same time; measured on MI355X at
-// context 256 (layer by layer, per step), 16 / 32 / 64 sequences: column-block major 1744 / 2412 /
-// 2411 us, K-block major 1513 / 1994 / 2596, row order 1544 / 1979 / 2863.
-__host__ __device__ inline int skf_blocks(int B) { return B <= 8 ? 1 : B <= 16 ? 2 : B <= 32 ? 4 : 8; }
-__host__ __device__ inline size_t skf_frag(int cb, int kb, int CB, int K) {
-  return CB == 8 ? (size_t)cb * (K >> 5) + kb : (size_t)kb * CB + cb;
-}
-__host__ __device__ inline size_t skf_off(int b, int k, int part, int B, int K) {
-  const int cb = b >> 3, li = 2 * (b & 7) + part, kb = k >> 5, lg = (k & 31) >> 3;
-  return ((skf_frag(cb, kb, skf_blocks(B), K) * 64 + lg * 16 + li) << 3) + (k & 7);
-}
-// Elements of the skinny fragments of B rows: whole column blocks of the kernel that reads them (1,
-// 2, 4 or 8 blocks of 8 rows), hi and lo.
-__host__ __device__ inline size_t skf_elems(int B, int K) { return (size_t)skf_blocks(B) * 8 * K * 2; }
 
 // A workgroup takes 16 weight rows (rows 16 bx ..). SK_RAW / SK_PART: its K range [by K / gy, ...)
-// split over the 4 waves; SK_SILU: 16 intermediates, gate rows on waves 0-1 and up rows on waves
-// 2-3, each pair splitting K in two. Each wave's K range is a multiple of 256 (checked on the host).
+// split over the 4 waves; SK_SILU: 8 intermediates, their 8 gate rows and 8 up rows in one 16-row
+// tile, K split over the 4 waves. Each wave's K range is a multiple of 256 (checked on the host).
 // The B operand holds CB column blocks of 8 rows of activations (a decode batch, or up to 64 prompt
-// tokens): column li of block cb is row 8 cb + li / 2, hi (even li) or lo (odd li). The weight
-// fragments of a K chunk stay in registers across the column blocks; the next block's activation
-// fragments are loaded while the current block is multiplied.
-// With FRAG the activations are skinny fragments (skf_off) in xh, of the batch's CB column blocks.
-template <int EPI, int CB, bool FRAG = false>
+// tokens): column li of block cb is row 8 cb + li / 2, hi (even li) or lo (odd li), read as skinny
+// fragments (skf_off) of the CB column blocks. The weight fragments of a K chunk stay in registers
+// across the column blocks; the next block's activation fragments are loaded while the current
+// block is multiplied.
+template <int EPI, int CB>
 __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   constexpr int NC = 8 * CB;
   __shared__ float red[4][16][NC + 1];
@@ -1042,22 +1043,11 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
     ke = kb + kw;
   }
   const int sb = li >> 1;
-  const uint16_t* xs[CB];
-  bool live[CB];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int b = 8 * cb + sb;
-    live[cb] = b < g.B;
-    xs[cb] = (li & 1 ? g.xl : g.xh) + (size_t)(live[cb] ? b : 0) * g.ldx + 8 * lg;
-  }
   f32x4 c[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) c[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint4* xf = reinterpret_cast<const uint4*>(g.xh) + lane;  // FRAG: this lane's 16 bytes of fragment 0
-  auto ld_act = [&](int cb, int k) {
-    if constexpr (FRAG) return xf[skf_frag(cb, k >> 5, CB, g.K) * 64];
-    else return live[cb] ? *reinterpret_cast<const uint4*>(xs[cb] + k) : make_uint4(0, 0, 0, 0);
-  };
+  const uint4* xf = reinterpret_cast<const uint4*>(g.xh) + lane;  // this lane's 16 bytes of fragment 0
+  auto ld_act = [&](int cb, int k) { return xf[skf_frag(cb, k >> 5, CB, g.K) * 64]; };
   for (int k0 = kb; k0 < ke; k0 += 256) {
     uint4 wa[8], xb[8];
 #pragma unroll
@@ -1096,14 +1086,9 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
       const float up = ((red[0][r + 8][b] + red[1][r + 8][b]) + red[2][r + 8][b]) + red[3][r + 8][b];
       const float m = gt / (1.f + expf(-gt)) * up;
       const uint16_t hi = f32_to_bf16(m), lo = f32_to_bf16(m - bf16_to_f32(hi));
-      const int it = 8 * blockIdx.x + r;
-      if constexpr (FRAG) {  // the down product's skinny fragments (g.ldm inputs)
-        g.mh[skf_off(b, it, 0, g.B, g.ldm)] = hi;
-        g.mh[skf_off(b, it, 1, g.B, g.ldm)] = lo;
-      } else {
-        g.mh[(size_t)b * g.ldm + it] = hi;
-        g.ml[(size_t)b * g.ldm + it] = lo;
-      }
+      const int it = 8 * blockIdx.x + r;  // into the down product's skinny fragments (g.ldm inputs)
+      g.mh[skf_off(b, it, 0, g.B, g.ldm)] = hi;
+      g.mh[skf_off(b, it, 1, g.B, g.ldm)] = lo;
     } else {
       const float v = ((red[0][r][b] + red[1][r][b]) + red[2][r][b]) + red[3][r][b];
       g.out[((size_t)blockIdx.y * g.B + b) * g.N + n0 + r] = v;
@@ -1113,14 +1098,11 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
 
 
 // The skinny product for up to 8 * cb activation rows (cb: 1, 2, 4 or 8 column blocks).
-static hipError_t launch_skinny(int epi, int cb, dim3 grid, const SkArgs& a, hipStream_t st, bool frag = false) {
-#define MK_SK(E, C, F) hipLaunchKernelGGL((skinny_kernel<E, C, F>), grid, dim3(256), 0, st, a)
-#define MK_SK_CB(E, F) \
-  if (cb == 1) MK_SK(E, 1, F); else if (cb == 2) MK_SK(E, 2, F); else if (cb == 4) MK_SK(E, 4, F); else MK_SK(E, 8, F)
-#define MK_SK_E(F) \
-  if (epi == SK_RAW) { MK_SK_CB(SK_RAW, F); } else if (epi == SK_PART) { MK_SK_CB(SK_PART, F); } else { MK_SK_CB(SK_SILU, F); }
-  if (frag) { MK_SK_E(true); } else { MK_SK_E(false); }
-#undef MK_SK_E
+static hipError_t launch_skinny(int epi, int cb, dim3 grid, const SkArgs& a, hipStream_t st) {
+#define MK_SK(E, C) hipLaunchKernelGGL((skinny_kernel<E, C>), grid, dim3(256), 0, st, a)
+#define MK_SK_CB(E) \
+  if (cb == 1) MK_SK(E, 1); else if (cb == 2) MK_SK(E, 2); else if (cb == 4) MK_SK(E, 4); else MK_SK(E, 8)
+  if (epi == SK_RAW) { MK_SK_CB(SK_RAW); } else if (epi == SK_PART) { MK_SK_CB(SK_PART); } else { MK_SK_CB(SK_SILU); }
 #undef MK_SK_CB
 #undef MK_SK
   return hipGetLastError();
@@ -1129,8 +1111,7 @@ static int column_blocks(int rows) { return rows <= 8 ? 1 : rows <= 16 ? 2 : row
 
 // Rows b < B of the residual: with `tokens`, x[b] = embed[tokens[b]] (a token outside [0, vocab)
 // reads row 0 and sets *bad); with `part`, x[b] += sum over s < S of part[s][b] (in order); then,
-// with `w`, RMSNorm into the bf16 hi/lo pair: [B][lda], or with FRAG the fragment-major layout of
-// H columns that gemm_kernel reads. One wave per row.
+// with `w`, RMSNorm into the bf16 hi/lo pair in the layout LAYOUT names. One wave per row.
 // LAYOUT 0: row order ah/al [B][lda]; 1: the GEMM's fragment order (frag_off, H columns); 2: skinny
 // fragments (skf_off, H inputs, hi and lo both in ah).
 template <int H, int LAYOUT = 0>
@@ -1549,7 +1530,7 @@ struct Work {
 // gate/up split over K on small grids). Measured on MI355X (same box, ms per prefill, skinny /
 // tiles): 0.6B 24 tokens 1.51 / 1.81, 32 1.65 / 1.87, 33 1.84 / 1.87, 40 1.93 / 1.91, 64 2.39 / 2.01;
 // 1.7B 24 tokens 2.61 / 2.87, 32 2.94 / 2.93, 33 3.29 / 2.94, 48 3.74 / 3.01.
-static int small_m(int H) { (void)H; return 32; }
+static int small_m(int H) { return H <= 1024 ? 64 : 32; }
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -1684,7 +1665,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
   const AttnPlan ap = attn_plan(M, position);
   if ((size_t)ap.wgs > attn_part_slots(M)) return hipErrorInvalidValue;  // cannot happen (see attn_plan)
   const bool small = M <= small_m(H);
-  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, A, small ? 0 : 1, M, 0, position, kv, wk.bad,
+  const AttnArgs at0{wk.qh, wk.ql, k_cache, v_cache, wk.ah, wk.al, small ? 2 : 1, M, 0, position, kv, wk.bad,
                      wk.apart, ap.chunk, attn_part_rows(M)};
   const dim3 attn_grid(ap.wgs);
   if (small) {
@@ -1695,12 +1676,18 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     const int cb = column_blocks(M);
     auto skinny = [&](int epi, dim3 grid, const SkArgs& a) { return launch_skinny(epi, cb, grid, a, st); };
     const dim3 rows((M + 3) / 4);
+    // norms into the products' skinny fragments (hi and lo in ah)
+    auto norm = [&](const int32_t* tk, int S, const uint16_t* w) {
+      hipLaunchKernelGGL((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, wk.x, tk, embed, dims.vocab, wk.bad, wk.part, S,
+                         w, wk.ah, nullptr, 0, M);
+      return hipGetLastError();
+    };
     for (int l = 0; l < dims.num_layers; ++l) {
       const mk_layer_weights& lw = layers[l];
-      MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, l == 0 ? tokens : nullptr, embed, dims.vocab, wk.bad,
-                 wk.part, l == 0 ? 0 : BP::SD, (const uint16_t*)lw.norm_weight, wk.ah, wk.al, A, M);
+      if ((e = norm(l == 0 ? tokens : nullptr, l == 0 ? 0 : BP::SD, (const uint16_t*)lw.norm_weight)) != hipSuccess)
+        return e;
       SkArgs q{};
-      q.xh = wk.ah; q.xl = wk.al; q.ldx = A; q.B = M; q.N = (HQ + 2 * HKV) * D; q.K = H;
+      q.xh = wk.ah; q.B = M; q.N = (HQ + 2 * HKV) * D; q.K = H;
       q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
       q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = wk.raw;
       if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
@@ -1712,18 +1699,17 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       MKP_LAUNCH(attn_kernel, attn_grid, dim3(512), 0, st, at);
       if (ap.merge) MKP_LAUNCH(attn_merge_kernel, dim3(ap.merge), dim3(256), 0, st, at);
       SkArgs o{};
-      o.xh = wk.ah; o.xl = wk.al; o.ldx = A; o.B = M; o.N = H; o.K = HQ * D;
+      o.xh = wk.ah; o.B = M; o.N = H; o.K = HQ * D;
       o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = wk.part;
       if ((e = skinny(SK_PART, dim3(H / 16, BP::SO), o)) != hipSuccess) return e;
-      MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SO,
-                 (const uint16_t*)lw.post_attn_norm_weight, wk.ah, wk.al, A, M);
+      if ((e = norm(nullptr, BP::SO, (const uint16_t*)lw.post_attn_norm_weight)) != hipSuccess) return e;
       SkArgs u{};
-      u.xh = wk.ah; u.xl = wk.al; u.ldx = A; u.B = M; u.N = I; u.K = H;
+      u.xh = wk.ah; u.B = M; u.N = I; u.K = H;
       u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight;
-      u.mh = wk.bh; u.ml = wk.bl; u.ldm = I;
+      u.mh = wk.bh; u.ldm = I;
       if ((e = skinny(SK_SILU, dim3(I / 8, 1), u)) != hipSuccess) return e;
       SkArgs dn{};
-      dn.xh = wk.bh; dn.xl = wk.bl; dn.ldx = I; dn.B = M; dn.N = H; dn.K = I;
+      dn.xh = wk.bh; dn.B = M; dn.N = H; dn.K = I;
       dn.w0 = (const uint16_t*)lw.down_proj_weight; dn.out = wk.part;
       if ((e = skinny(SK_PART, dim3(H / 16, BP::SD), dn)) != hipSuccess) return e;
     }
@@ -1934,24 +1920,24 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     q.xh = af; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
     q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
     q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = raw;
-    if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_RAW, cb, dim3(q.N / 16, 1), q, st)) != hipSuccess) return e;
     MKB_LAUNCH(battn_partial_kernel, dim3(S < gx ? S : gx, HKV, B), dim3(256), 0, st, raw, positions, tokens,
                dims.vocab, (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, k_cache,
                v_cache, L, l, max_seq, apart, S, bad);
     MKB_LAUNCH(battn_merge_kernel, dim3(B, HQ), dim3(D), 0, st, apart, S, positions, max_seq, af, nullptr, 0);
     SkArgs o{};
     o.xh = af; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
-    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, so), o, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, so), o, st)) != hipSuccess) return e;
     MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, so,
                (const uint16_t*)lw.post_attn_norm_weight, af, nullptr, 0, B);
     SkArgs u{};
     u.xh = af; u.B = B; u.N = I; u.K = H;
     u.w0 = (const uint16_t*)lw.gate_proj_weight; u.w1 = (const uint16_t*)lw.up_proj_weight; u.mh = bf; u.ldm = I;
-    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 8, 1), u, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_SILU, cb, dim3(I / 8, 1), u, st)) != hipSuccess) return e;
     SkArgs dn{};
     dn.xh = bf; dn.B = B; dn.N = H; dn.K = I; dn.w0 = (const uint16_t*)lw.down_proj_weight;
     dn.out = part;
-    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, sd), dn, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, sd), dn, st)) != hipSuccess) return e;
   }
   // the last layer's down partials and the final norm, then the tied LM head as one more skinny
   // product (vocabulary rows x the B normalised rows: each table byte read once, on the matrix
@@ -1967,7 +1953,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     SkArgs lmh{};
     lmh.xh = af; lmh.B = B; lmh.N = dims.vocab; lmh.K = H;
     lmh.w0 = lm_head; lmh.n1 = dims.vocab; lmh.n2 = dims.vocab; lmh.out = logits;
-    if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st, true)) != hipSuccess) return e;
+    if ((e = launch_skinny(SK_RAW, cb, dim3(dims.vocab / 16, 1), lmh, st)) != hipSuccess) return e;
   } else {
     // beyond one column block the skinny product re-reads every row's activations per 16 table
     // rows; a 128-row tile of the table reads them once per 128 (the B rows are one row tile)

@@ -70,7 +70,8 @@ def _check_cache(got, want, upto, tag):
 def test_prefill_matches_oracle(shape_fixture, P, request):
     """Prefill from an empty cache against ``restate.prefill`` on the same prompt: the last token's
     logits and greedy token, every K/V row written, and nothing written past the prompt. P = 1 has
-    one key; P <= 32 runs the skinny products (32: all 4 column blocks), P = 33 and 64 one 128-row
+    one key; P <= 64 at the 0.6B width and P <= 32 at 1.7B run the skinny products on activations in
+    skinny fragment order (32: 4 column blocks, 33 and 64: 8), P = 65 and the 1.7B P = 64 one 128-row
     tile (rows past the prompt dead; QKV and gate/up split over K into raw sums that the post kernels
     finish, the residual products split over K, several K steps in flight), P = 65 two attention
     query blocks, the second with one row; P = 300 spans 5 query blocks of the attention (key-range
