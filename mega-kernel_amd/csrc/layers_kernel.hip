@@ -19,8 +19,12 @@
 //               x += m . Wd^T                          (gemm, EPI_RESID)
 //   logits of the last row = RMSNorm(x) . E^T, greedy token (lm_head_kernel, fused argmax)
 // When the residual products' tile grid is small (below 192 tiles) they are split over K into
-// partials that the next norm adds in a fixed order. Prompts of at most small_m(H) tokens run the
-// products on the skinny kernels of the batched decode instead (weights as the MFMA A operand).
+// partials that the next norm adds in a fixed order; on grids of at most 128 tiles QKV and gate/up
+// are split over K too, into raw sums that qkv_post_kernel / silu_post_kernel finish. The attention
+// takes one query block per workgroup, or key-range chunks of the blocks merged by
+// attn_merge_kernel where the blocks' key chains are uneven against the grid. Prompts of at most
+// small_m(H) tokens run the products on the skinny kernels of the batched decode instead (weights
+// as the MFMA A operand, activations in its skinny fragment order).
 //
 // Numerics are the decode kernel's (the reference kernel's fp32 design, /root/reference/
 // megakernel.cu): fp32 residual and accumulation, fp32 RMSNorm, exact softmax, new K/V rounded to
