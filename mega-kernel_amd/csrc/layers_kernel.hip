@@ -283,35 +283,39 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
       step(ac);
     }
   } else {
-    // the K range is a multiple of PF steps (host); step i + PF's loads go out as step i starts
+    // The K range is a multiple of PF steps (host). Step i + PF's loads go out as step i starts, the
+    // last PF steps issue none. The scheduling barriers keep each step's loads in issue order: the
+    // waits before a step then cover that step's loads alone (left free, the scheduler may issue a
+    // later step's loads first, and the wait for the earlier ones then drains the whole pipeline).
     AStep aq[PF];
     WStep wq[PF];
-    const int klast = ke - KT;
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
-      const int k = min(kb + p * KT, klast);
-      load_w(k, wq[p]);
-      load_a(k, aq[p]);
+      load_w(kb + p * KT, wq[p]);
+      load_a(kb + p * KT, aq[p]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    for (int k0 = kb; k0 < ke; k0 += PF * KT) {
+    for (int k0 = kb; k0 < ke - PF * KT; k0 += PF * KT) {
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
         __syncthreads();  // every wave is done with the previous step's weight tile
         store_w(wq[p]);
         __syncthreads();
-        AStep ac;
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int bm = 0; bm < 2; ++bm) {
-            ac[s][bm][0] = aq[p][s][bm][0];
-            ac[s][bm][1] = aq[p][s][bm][1];
-          }
-        const int kn = min(k0 + (p + PF) * KT, klast);
+        // step i + PF's weights into the registers just stored, its A fragments into the ones the
+        // MFMAs just read (no copies: a register copy of a pending load would wait for it)
+        const int kn = k0 + (p + PF) * KT;
         load_w(kn, wq[p]);
+        step(aq[p]);
         load_a(kn, aq[p]);
-        step(ac);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      __syncthreads();
+      store_w(wq[p]);
+      __syncthreads();
+      step(aq[p]);
     }
   }
 
