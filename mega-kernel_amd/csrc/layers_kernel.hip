@@ -179,13 +179,12 @@ struct GemmSmem {
   };
 };
 
-// PF: K steps of operands in flight. 1: the next step's loads are issued as a step's MFMAs start
-// (two workgroups per CU hide each other's load latency). PF > 1 for grids of at most one workgroup
-// per CU (short prompts), where a lone workgroup otherwise waits out most of each load round trip:
-// PF steps are loaded ahead in registers (a clamped re-load of the last step past the end, so that
-// every step issues the same loads and each wait covers exactly its own step).
+// PF: K steps of operands in flight, loaded ahead in registers. 1: the next step's loads are issued
+// as a step's MFMAs start (two workgroups per CU hide each other's load latency). 4: grids of at
+// most one workgroup per CU (short prompts), where a lone workgroup otherwise waits out most of each
+// load round trip. 2: either; the register budget of two workgroups per CU (256 per lane) holds it.
 template <int EPI, int PF = 1>
-__global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
+__global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) GemmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int tn = blockIdx.x, tm = blockIdx.y;
@@ -1630,21 +1629,16 @@ static Work carve(void* base, const Layout& L) {
   return w;
 }
 
-// K steps in flight (gemm_kernel's PF) of a launch: up to GEMM_PF_MAX when the grid holds at most
-// GEMM_PF_WGS workgroups (one per CU), the largest power of two that divides the steps.
-#ifndef MKP_GEMM_PF_MAX
-#define MKP_GEMM_PF_MAX 4
-#endif
-#ifndef MKP_GEMM_PF_WGS
-#define MKP_GEMM_PF_WGS 256
-#endif
-constexpr int GEMM_PF_MAX = MKP_GEMM_PF_MAX, GEMM_PF_WGS = MKP_GEMM_PF_WGS;
+// K steps in flight (gemm_kernel's PF) of a launch. Grids of at most one workgroup per CU: 4, else 2
+// (whichever divides the steps). Grids of two or more workgroups per CU: 2, at two workgroups per CU.
+// In between (1 to 2 workgroups per CU): 1. Measured on MI355X, per launch, 1 -> 2 steps in flight:
+// 0.6B prompt 3,584 QKV (896 workgroups) 80.5 -> 73.3 us, gate/up (1,344) 97.5 -> 96.2 us; prompt
+// 2,048 QKV (512) 42.9 -> 40.9 us, gate/up (768) 58.4 -> 54.6 us; 1.7B prompt 1,500 gate/up (1,152)
+// 161.9 -> 156.8 us; but 1.7B prompt 512 gate/up (384) 62.5 -> 66.0 us.
 static int gemm_pf(dim3 grid, int K) {
-  const int steps = K / (int)grid.z / KT;
-  if ((int)(grid.x * grid.y * grid.z) > GEMM_PF_WGS) return 1;
-  for (int pf = GEMM_PF_MAX; pf > 1; pf /= 2)
-    if (steps % pf == 0) return pf;
-  return 1;
+  const int steps = K / (int)grid.z / KT, wgs = (int)(grid.x * grid.y * grid.z);
+  if (wgs <= 256) return steps % 4 == 0 ? 4 : steps % 2 == 0 ? 2 : 1;
+  return wgs >= 512 && steps % 2 == 0 ? 2 : 1;
 }
 template <int EPI>
 static hipError_t launch_gemm(dim3 grid, const GemmArgs& g, hipStream_t st) {
