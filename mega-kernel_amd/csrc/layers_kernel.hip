@@ -1023,8 +1023,8 @@ struct SkArgs {
 // The B operand holds CB column blocks of 8 rows of activations (a decode batch, or up to 64 prompt
 // tokens): column li of block cb is row 8 cb + li / 2, hi (even li) or lo (odd li), read as skinny
 // fragments (skf_off) of the CB column blocks. The weight fragments of a K chunk stay in registers
-// across the column blocks; the next block's activation fragments are loaded while the current
-// block is multiplied.
+// across the column blocks; up to 4 blocks' activation fragments are in flight while a block is
+// multiplied.
 template <int EPI, int CB>
 __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   constexpr int NC = 8 * CB;
@@ -1055,26 +1055,28 @@ __global__ void __launch_bounds__(256) skinny_kernel(const SkArgs g) {
   for (int cb = 0; cb < CB; ++cb) c[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint4* xf = reinterpret_cast<const uint4*>(g.xh) + lane;  // this lane's 16 bytes of fragment 0
   auto ld_act = [&](int cb, int k) { return xf[skf_frag(cb, k >> 5, CB, g.K) * 64]; };
+  // R column blocks' activation fragments in flight: block cb + R's loads go into the registers
+  // block cb's MFMAs have just read (no copies: a register copy of a pending load would wait for it)
+  constexpr int R = CB < 4 ? CB : 4;
   for (int k0 = kb; k0 < ke; k0 += 256) {
-    uint4 wa[8], xb[8];
+    uint4 wa[8], xq[R][8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      wa[u] = ld_stream(reinterpret_cast<const uint4*>(wrow + k0 + 32 * u + 8 * lg));
-      xb[u] = ld_act(0, k0 + 32 * u);
+    for (int u = 0; u < 8; ++u) wa[u] = ld_stream(reinterpret_cast<const uint4*>(wrow + k0 + 32 * u + 8 * lg));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) xq[r][u] = ld_act(r, k0 + 32 * u);
+      __builtin_amdgcn_sched_barrier(0);  // the blocks' loads in block order: each wait covers one block
     }
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      uint4 xn[8];
-      if (cb + 1 < CB) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) xn[u] = ld_act(cb + 1, k0 + 32 * u);
+      for (int u = 0; u < 8; ++u) c[cb] = mfma(wa[u], xq[cb % R][u], c[cb]);
+      if (cb + R < CB) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) xq[cb % R][u] = ld_act(cb + R, k0 + 32 * u);
       }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) c[cb] = mfma(wa[u], xb[u], c[cb]);
-      if (cb + 1 < CB) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) xb[u] = xn[u];
-      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // C[row 4 lg + j][column li]: activation row 8 cb + li / 2 is the sum of its hi and lo columns
