@@ -575,7 +575,10 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     f32x4 acc[8];
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float mrun = -INFINITY, lrun = 0.f;  // running max and sum of query qrow (replicated on its 4 lanes)
+    // running max (of the raw scores) and sum of query qrow, replicated on its 4 lanes; a weight is
+    // exp(ATT_SCALE (s - m)) = exp2(s C - m C)
+    float mrun = -INFINITY, lrun = 0.f;
+    constexpr float C = ATT_SCALE * 1.4426950408889634f;
 
     // K chunks and V rows of a block, loaded into registers ahead of use. Keys past `last` load key
     // `last` again (finite data; the causal mask gives them probability 0): every lane issues the
@@ -584,7 +587,13 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
     struct Blk {
       uint4 k0, k1, v0, v1;
     };
+    // Contiguous cache: the (layer, head) rows as a uniform base plus a 32-bit byte offset (one
+    // multiply-add per load). Paged: the row through the staged table.
+    const size_t hbase = ((size_t)a.layer * HKV + kvh) * a.kv.max_seq * D;
     auto ld = [&](const uint16_t* base, int kp, int e) __attribute__((always_inline)) {
+      if (!a.kv.bt)
+        return ld_global16(reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base + hbase) +
+                                                          2u * (uint32_t)(kp * D + e)));
       return ld_global16(reinterpret_cast<const uint4*>(base + key_row(kp) + e));  // a value, not a copy
     };
     auto load_block = [&](Blk& b, int kb) __attribute__((always_inline)) {
@@ -630,56 +639,50 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) st[mb] = mfma(fk[mb], fq[1][s], st[mb]);
       }
-      // causal mask (only on blocks that reach past the wave's first query) and scale; block
-      // maximum of this lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip)
-      float bmax = -INFINITY;
-      if (kp0 + KB - 1 <= a.position + q0 + wq) {
+      // causal mask (only on blocks that reach past the wave's first query); block maximum of this
+      // lane's query over its 4 lanes (gfx950 lane swaps, no LDS round trip), on the raw scores
+      if (kp0 + KB - 1 > a.position + q0 + wq) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            st[mb][j] *= ATT_SCALE;
-            bmax = fmaxf(bmax, st[mb][j]);
-          }
-      } else {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int kp = kp0 + 16 * mb + 4 * lg + j;
-            const float sv = kp <= qpos ? st[mb][j] * ATT_SCALE : -INFINITY;
-            st[mb][j] = sv;
-            bmax = fmaxf(bmax, sv);
-          }
+          for (int j = 0; j < 4; ++j)
+            if (kp0 + 16 * mb + 4 * lg + j > qpos) st[mb][j] = -INFINITY;
       }
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bmax = fmaxf(bmax, st[mb][j]);
       bmax = xmax32(xmax16(bmax));
       // mnew is finite once the query has seen a key: from the first block on (key 0) without
       // chunks; a chunk that starts past some of its block's queries leaves those at -inf, and
-      // then msafe keeps their weights exp(-inf) = 0 instead of NaN
+      // then mc = 0 keeps their weights exp2(-inf) = 0 instead of NaN
       const float mnew = fmaxf(mrun, bmax);
-      const float msafe = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = __expf(mrun - msafe);
+      const float mc = mnew == -INFINITY ? 0.f : mnew * C;
+      const float alpha = __builtin_amdgcn_exp2f(mrun * C - mc);  // exactly 1 when the max holds
       float psum = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p = __expf(st[mb][j] - msafe);
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[mb][j], C, -mc));
           st[mb][j] = p;
           psum += p;
         }
       psum = xsum32(xsum16(psum));
       lrun = lrun * alpha + psum;
       mrun = mnew;
-      // rescale the output rows: row 4g + j of the accumulator is query 4g + j, whose alpha sits
-      // in lane 4g + j (and its copies)
-      float ar[4];
+      // rescale the output rows (skipped when no query of the wave has a new maximum): row 4g + j
+      // of the accumulator is query 4g + j, whose alpha sits in lane 4g + j (and its copies)
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+        float ar[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
+        for (int j = 0; j < 4; ++j) ar[j] = __shfl(alpha, 4 * lg + j);
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+        for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
+          for (int j = 0; j < 4; ++j) acc[nb][j] *= ar[j];
+      }
       // O += P . V over two 32-key steps
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -722,15 +725,15 @@ __global__ void __launch_bounds__(512) attn_kernel(const AttnArgs a) {
       __syncthreads();  // block kb consumed by every wave; block kb + 1 staged
     }
     if (partial) {
-      // this chunk's unnormalised rows and their (m, l) into the workgroup's slot, staged per wave in
-      // LDS as the slot's rows (APS floats; the tiles are free after the loop's last barrier) and
-      // stored as 16-byte chunks; rows past qr (queries past a short prompt) are not kept
+      // this chunk's unnormalised rows and their (m ATT_SCALE, l) into the workgroup's slot, staged
+      // per wave in LDS as the slot's rows (APS floats; the tiles are free after the loop's last
+      // barrier) and stored as 16-byte chunks; rows past qr (queries past a short prompt) are not kept
       float* stg = reinterpret_cast<float*>(&sm) + w * 16 * APS;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) stg[(4 * lg + j) * APS + 16 * nb + li] = acc[nb][j];
-      if (lg == 0) *reinterpret_cast<float2*>(stg + li * APS + D) = make_float2(mrun, lrun);
+      if (lg == 0) *reinterpret_cast<float2*>(stg + li * APS + D) = make_float2(mrun * ATT_SCALE, lrun);
       float* P = a.part + (((size_t)blockIdx.x * 2 + (w >> 2)) * a.qr + wq) * APS;
       const int nch = (min(16, a.qr - wq) * APS) / 4;  // 16-byte chunks of this wave's kept rows
       for (int k = lane; k < nch; k += 64)
