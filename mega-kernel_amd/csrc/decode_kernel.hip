@@ -2067,4 +2067,4 @@ extern "C" int mk_grid_size(void) {
   return device_state(&st) == hipSuccess ? NWG : -1;
 }
 
-extern "C" const char* mk_version(void) { return "megakernel_amd 0.23 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, gate/up rows early on split-free workgroups, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure; prefill GEMMs on fragment-major activations, 4 K steps in flight on small grids, prefill attention in key-range chunks)"; }
+extern "C" const char* mk_version(void) { return "megakernel_amd 0.24 (gfx950; 32-bit LL exchanges, 8 math waves, phase-ahead weight prefetch split across hops, gate/up rows early on split-free workgroups, max-first split merge, early LM-head rows, plain launch, device-side token loop, paged cache, per-stream workspaces, in-band failure; prefill GEMMs on fragment-major activations with K steps in flight in issue order, prefill attention in key-range chunks, skinny products with 4 activation blocks in flight)"; }
