@@ -170,8 +170,8 @@ hipError_t mk_prefill_paged(const mk_model_dims* dims, const int32_t* tokens, in
  * Batched decode: `batch` (1..64) independent sequences advance by one token each in one call.
  * Two engines: up to 16 sequences of the Qwen3-0.6B shape run as one persistent kernel (256
  * workgroups exchanging data through epoch-tagged words, the batch as the columns of the matrix-core
- * tiles), 17-32 as two such launches (16 and the rest); other batches run layer by layer (a few
- * kernels per layer). mk_set_batch_engine chooses.
+ * tiles), 17-24 as two such launches (16 and the rest; 17-32 with the persistent engine forced);
+ * other batches run layer by layer (a few kernels per layer). mk_set_batch_engine chooses.
  * Sequence b decodes tokens[b] at positions[b] (both int32 device arrays of `batch` entries, so a
  * device-side loop can advance them): it writes its K/V rows at positions[b] of its own cache and
  * attends over [0, positions[b]]. k_cache/v_cache are bf16 [batch][num_layers][8][max_seq_len][128]
@@ -262,8 +262,9 @@ hipError_t mk_status(uint32_t* status);
 
 /* Engine of mk_decode_batch for the calling process: 0 automatic (the persistent kernel where it
  * applies: the Qwen3-0.6B shape, 1..16 sequences -- one MFMA column block up to 8, two from 9 on --, at
- * most 32 layers, a device with 256 CUs; 17..32 sequences as two launches of it), 1 always
- * the layer-by-layer engine, 2 the persistent kernel where it applies. Both give each sequence
+ * most 32 layers, a device with 256 CUs; 17..24 sequences as two launches of it), 1 always
+ * the layer-by-layer engine, 2 the persistent kernel where it applies (17..32 sequences as two
+ * launches). Both give each sequence
  * mk_decode's numerics. hipErrorInvalidValue for another value. No reference counterpart. */
 hipError_t mk_set_batch_engine(int engine);
 

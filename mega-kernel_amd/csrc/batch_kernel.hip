@@ -1158,6 +1158,7 @@ bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len) {
          dims->num_layers < 255 && batch >= 1 && batch <= BMAX && max_seq_len >= 1 && device_ok(batch <= 8 ? 1 : 2);
 }
 size_t mkb_workspace_bytes() { return mkb::WS_BYTES; }
+int mkb_engine() { return mkb::g_engine.load(); }
 void mkb_set_drain(bool on) { mkb::g_drain.store(on); }
 
 hipError_t mkb_decode_batch(const mk_model_dims* dims, int batch, const int32_t* tokens, const int32_t* positions,

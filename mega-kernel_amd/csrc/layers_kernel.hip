@@ -2008,12 +2008,14 @@ extern "C" hipError_t mk_decode_batch(const mk_model_dims* dims, int batch, cons
                             cos_table, sin_table, k_cache, v_cache, max_seq_len, logits, out_tokens, workspace,
                             stream);
   }
-  // 17-32 sequences where the persistent kernel applies to their halves: two persistent launches,
-  // MKB_MAX sequences and the rest, one after the other on the stream (each sequence's cache, token,
-  // position, logits and greedy token are its own slices, so the halves are independent calls).
-  // Measured on MI355X at context 256 (0.6B): 32 sequences 1.87 ms per step layer by layer, two
-  // launches of 16 ~1.70 ms.
-  if (batch > MKB_MAX && batch <= 2 * MKB_MAX && mkb_applies(dims, MKB_MAX, max_seq_len) &&
+  // 17-24 sequences (17-32 with the persistent engine forced) where the persistent kernel applies
+  // to their parts: two persistent launches, MKB_MAX sequences and the rest, one after the other on
+  // the stream (each sequence's cache, token, position, logits and greedy token are its own slices,
+  // so the parts are independent calls). Measured on MI355X (0.6B, ms per step, two launches /
+  // layer by layer), context 256: 17 1.41 / 1.48, 20 1.45 / 1.50, 24 1.49 / 1.52, 28 1.65 / 1.58,
+  // 32 1.70 / 1.61; context 1,500: 24 2.10 / 2.19, 28 2.34 / 2.37, 32 2.48 / 2.47.
+  const int two_max = mkb_engine() == 2 ? 2 * MKB_MAX : MKB_MAX + 8;
+  if (batch > MKB_MAX && batch <= two_max && mkb_applies(dims, MKB_MAX, max_seq_len) &&
       mkb_applies(dims, batch - MKB_MAX, max_seq_len)) {
     if (workspace_bytes < mkb_workspace_bytes()) return hipErrorInvalidValue;
     const size_t seq_cache = (size_t)dims->num_layers * HKV * max_seq_len * D;  // elements per sequence

@@ -16,6 +16,8 @@ constexpr int MKB_MAX = 16;
 bool mkb_applies(const mk_model_dims* dims, int batch, int max_seq_len);
 // Workspace bytes the persistent kernel needs (exchange words, tickets, greedy keys).
 size_t mkb_workspace_bytes();
+// The engine selection (mk_set_batch_engine): 0 automatic, 1 layer by layer, 2 persistent kernel.
+int mkb_engine();
 // Host drain request (mk_request_drain / mk_reset): later launches give up at once.
 void mkb_set_drain(bool on);
 // Launches zero fill, the persistent kernel and the finish kernel on `stream`; arguments as

@@ -451,7 +451,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "batched decode of B <= 64 sequences (int32 tokens [B], positions [B], caches [B, L, 8, max_seq, 128]); "
         "returns (fp32 logits [B, V], int32 greedy tokens [B] on device)");
   m.def("set_batch_engine", &set_batch_engine,
-        "engine of decode_batch: 0 automatic (the persistent kernel for <= 16 sequences of the 0.6B shape, two launches of it for 17-32), "
+        "engine of decode_batch: 0 automatic (the persistent kernel for <= 16 sequences of the 0.6B shape, two launches of it for 17-24), "
         "1 layer by layer, 2 persistent where it applies");
   m.def("status", &status,
         "device status (0 = healthy; bit 0 timeout, 1 placement, 2 token, 3 page, 4 drain requested); synchronizes");
