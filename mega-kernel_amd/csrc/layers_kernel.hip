@@ -1967,7 +1967,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     GemmArgs gl{};
     gl.ah = ah; gl.al = al; gl.M = B; gl.N = dims.vocab; gl.K = H;
     gl.w0 = lm_head; gl.part = logits;  // logits[b][v], no residual
-    MKB_LAUNCH(gemm_kernel<EPI_RESID>, dim3(dims.vocab / NT, 1, 1), dim3(256), 0, st, gl);
+    if ((e = launch_gemm<EPI_RESID>(dim3(dims.vocab / NT, 1, 1), gl, st)) != hipSuccess) return e;
   }
   MKB_LAUNCH(logits_argmax_kernel, dim3((dims.vocab + 4095) / 4096, B), dim3(256), 0, st, logits, dims.vocab, keys, bad);
   if (out_tokens) MKB_LAUNCH(keys_to_tokens_kernel, dim3(1), dim3(64), 0, st, keys, B, bad, out_tokens);
