@@ -182,9 +182,10 @@ struct GemmSmem {
 // PF: K steps of operands in flight, loaded ahead in registers. 1: the next step's loads are issued
 // as a step's MFMAs start (two workgroups per CU hide each other's load latency). 4: grids of at
 // most one workgroup per CU (short prompts), where a lone workgroup otherwise waits out most of each
-// load round trip. 2: either; the register budget of two workgroups per CU (256 per lane) holds it.
+// load round trip. 2: either. PF 1 and 2 are held to the register budget of two workgroups per CU
+// (256 per lane).
 template <int EPI, int PF = 1>
-__global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmArgs g) {
+__global__ void __launch_bounds__(256, PF == 4 ? 1 : 2) gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) GemmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int tn = blockIdx.x, tm = blockIdx.y;
@@ -244,6 +245,10 @@ __global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmAr
     for (int bn = 0; bn < 8; ++bn) acc[bm][bn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kspan = g.K / gridDim.z, kb = blockIdx.z * kspan, ke = kb + kspan;  // a multiple of KT
+  // a wave whose 32 rows all lie past M (a short last row tile: the batched decode's LM head takes 64
+  // or fewer rows) still loads its fragments and stages its part of the weight tile -- the same loads
+  // in every wave keep the waits exact -- but skips the MFMAs
+  const bool act = m0 + 32 * wave < g.M;
   auto step = [&](const AStep& ac) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < KT / 32; ++s) {
@@ -279,7 +284,7 @@ __global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmAr
         load_w(k0 + KT, rw);
         load_a(k0 + KT, an);
       }
-      step(ac);
+      if (act) step(ac);
     }
   } else {
     // The K range is a multiple of PF steps (host). Step i + PF's loads go out as step i starts, the
@@ -304,7 +309,7 @@ __global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmAr
         // MFMAs just read (no copies: a register copy of a pending load would wait for it)
         const int kn = k0 + (p + PF) * KT;
         load_w(kn, wq[p]);
-        step(aq[p]);
+        if (act) step(aq[p]);
         load_a(kn, aq[p]);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -314,7 +319,7 @@ __global__ void __launch_bounds__(256, PF == 2 ? 2 : 1) gemm_kernel(const GemmAr
       __syncthreads();
       store_w(wq[p]);
       __syncthreads();
-      step(aq[p]);
+      if (act) step(aq[p]);
     }
   }
 
