@@ -1688,10 +1688,10 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
     typedef BatchPlan<H, I> BP;
     const int cb = column_blocks(M);
     auto skinny = [&](int epi, dim3 grid, const SkArgs& a) { return launch_skinny(epi, cb, grid, a, st); };
-    const dim3 rows((M + 3) / 4);
+    const dim3 rows(M), nthr(64);  // one row per single-wave workgroup: the rows spread over M CUs
     // norms into the products' skinny fragments (hi and lo in ah)
     auto norm = [&](const int32_t* tk, int S, const uint16_t* w) {
-      hipLaunchKernelGGL((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, wk.x, tk, embed, dims.vocab, wk.bad, wk.part, S,
+      hipLaunchKernelGGL((bnorm_kernel<H, 2>), rows, nthr, 0, st, wk.x, tk, embed, dims.vocab, wk.bad, wk.part, S,
                          w, wk.ah, nullptr, 0, M);
       return hipGetLastError();
     };
@@ -1727,7 +1727,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       if ((e = skinny(SK_PART, dim3(H / 16, BP::SD), dn)) != hipSuccess) return e;
     }
     // the last layer's down partials into the residual (no norm: the LM head normalises its row)
-    MKP_LAUNCH(bnorm_kernel<H>, rows, dim3(256), 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SD,
+    MKP_LAUNCH(bnorm_kernel<H>, rows, nthr, 0, st, wk.x, nullptr, embed, dims.vocab, wk.bad, wk.part, BP::SD,
                nullptr, nullptr, nullptr, A, M);
   }
   // Longer prompts: 128 x 128 tiles with the epilogues fused; the residual products split over K
@@ -1927,12 +1927,12 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   // attention workgroups per sequence and K/V head (each loops over its splits): about 1024 in all,
   // 16 at most (the grid cannot follow the device-side positions, so it must not be mostly idle)
   const int gx = B <= 8 ? 16 : B <= 16 ? 8 : B <= 32 ? 4 : 2;
-  const dim3 rows((B + 3) / 4);
+  const dim3 rows(B), nthr(64);  // norms: one row per single-wave workgroup
   const int so = BP::SO, sd = BP::SD;
   for (int l = 0; l < L; ++l) {
     const mk_layer_weights& lw = layers[l];
     // x (embedding, or + the previous layer's down partials) -> input norm, as skinny fragments
-    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, l == 0 ? tokens : nullptr, embed, dims.vocab, bad,
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, nthr, 0, st, x, l == 0 ? tokens : nullptr, embed, dims.vocab, bad,
                part, l == 0 ? 0 : sd, (const uint16_t*)lw.norm_weight, af, nullptr, 0, B);
     SkArgs q{};
     q.xh = af; q.B = B; q.N = (HQ + 2 * HKV) * D; q.K = H;
@@ -1946,7 +1946,7 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
     SkArgs o{};
     o.xh = af; o.B = B; o.N = H; o.K = HQ * D; o.w0 = (const uint16_t*)lw.o_proj_weight; o.out = part;
     if ((e = launch_skinny(SK_PART, cb, dim3(H / 16, so), o, st)) != hipSuccess) return e;
-    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, so,
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, nthr, 0, st, x, nullptr, embed, dims.vocab, bad, part, so,
                (const uint16_t*)lw.post_attn_norm_weight, af, nullptr, 0, B);
     SkArgs u{};
     u.xh = af; u.B = B; u.N = I; u.K = H;
@@ -1962,10 +1962,10 @@ static hipError_t run_batch(const mk_model_dims& dims, int B, const int32_t* tok
   // cores) and the greedy keys
   const bool lm_tiles = B > 8 && dims.vocab % NT == 0;
   if (lm_tiles)
-    MKB_LAUNCH((bnorm_kernel<H, 1>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
+    MKB_LAUNCH((bnorm_kernel<H, 1>), rows, nthr, 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
                final_norm, ah, al, A, B);
   else
-    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, dim3(256), 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
+    MKB_LAUNCH((bnorm_kernel<H, 2>), rows, nthr, 0, st, x, nullptr, embed, dims.vocab, bad, part, sd,
                final_norm, af, nullptr, 0, B);
   if (!lm_tiles) {
     SkArgs lmh{};
