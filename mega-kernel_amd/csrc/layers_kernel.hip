@@ -1229,55 +1229,57 @@ __device__ __forceinline__ int seq_pos(const int32_t* positions, int b, int max_
 }
 
 // The raw Q/K/V sums of M consecutive prompt tokens of one sequence (fp32 [M][4096], or S such arrays
-// of K-range sums added in order; row m at position pos0 + m): per-head RMSNorm + RoPE on q and k
-// (one wave per row and head, lane l holding
-// dims l and l + 64, the RoPE pair), q kept as a bf16 hi/lo pair [M][2048], k and v rounded to bf16
-// into the cache [L][8][max_seq][128].
-__global__ void __launch_bounds__(256) qkv_post_kernel(const float* raw, int S, int M, int pos0, const uint16_t* q_norm,
+// of K-range sums added in order; row m at position pos0 + m): per-head RMSNorm + RoPE on q and k,
+// q kept as a bf16 hi/lo pair [M][2048], k and v rounded to bf16 into the cache [L][8][max_seq][128].
+__global__ void __launch_bounds__(64) qkv_post_kernel(const float* raw, int S, int M, int pos0, const uint16_t* q_norm,
                                                        const uint16_t* k_norm, const uint16_t* cos_tab,
                                                        const uint16_t* sin_tab, uint16_t* qh, uint16_t* ql,
                                                        uint16_t* k_cache, uint16_t* v_cache, int layer, KvMap kv,
                                                        int32_t* bad) {
-  const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= M * (HQ + 2 * HKV)) return;
+  // one item (row b, head hd) per 16-lane group, lane t holding dims 8 t .. +7 (head_norm_rope's
+  // layout): 16-byte loads and stores
+  const int t = threadIdx.x & 15;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 4);  // single-wave workgroups: the items spread over the CUs
+  if (item >= M * (HQ + 2 * HKV)) return;  // uniform in the 16-lane group
   const int b = item / (HQ + 2 * HKV), hd = item % (HQ + 2 * HKV);
   const int pos = pos0 + b;
   // the sums of S K ranges (EPI_QKV_PART), added in order
   const size_t rstride = (size_t)M * (HQ + 2 * HKV) * D;
-  const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D;
-  float u0 = r[lane], u1 = r[lane + 64];
-  for (int q = 1; q < S; ++q) {
-    u0 += r[q * rstride + lane];
-    u1 += r[q * rstride + lane + 64];
+  const float* r = raw + (size_t)b * (HQ + 2 * HKV) * D + hd * D + 8 * t;
+  float v[8];
+  {
+    const float4 x0 = *reinterpret_cast<const float4*>(r), x1 = *reinterpret_cast<const float4*>(r + 4);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
   }
-  const int page = hd >= HQ && kv.bt ? kv_page(kv, pos, lane == 0 ? bad : nullptr) : 0;
-  auto cache_row = [&](uint16_t* cache, int kvh) { return cache + kv_row(kv, layer, kvh, pos, page); };
+  for (int q = 1; q < S; ++q) {
+    const float4 x0 = *reinterpret_cast<const float4*>(r + q * rstride);
+    const float4 x1 = *reinterpret_cast<const float4*>(r + q * rstride + 4);
+    v[0] += x0.x; v[1] += x0.y; v[2] += x0.z; v[3] += x0.w; v[4] += x1.x; v[5] += x1.y; v[6] += x1.z; v[7] += x1.w;
+  }
+  const int page = hd >= HQ && kv.bt ? kv_page(kv, pos, t == 0 ? bad : nullptr) : 0;
+  auto pack = [&]() {
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
+  };
   if (hd >= HQ + HKV) {  // v
-    if (page < 0) return;
-    uint16_t* dst = cache_row(v_cache, hd - HQ - HKV);
-    dst[lane] = f32_to_bf16(u0);
-    dst[lane + 64] = f32_to_bf16(u1);
+    if (page >= 0)
+      *reinterpret_cast<uint4*>(v_cache + kv_row(kv, layer, hd - HQ - HKV, pos, page) + 8 * t) = pack();
     return;
   }
-  const float rs = rsqrtf(wave_sum(u0 * u0 + u1 * u1) / (float)D + EPS);
-  const uint16_t* nw = hd < HQ ? q_norm : k_norm;
-  u0 *= rs * bf16_to_f32(nw[lane]);
-  u1 *= rs * bf16_to_f32(nw[lane + 64]);
-  const float cs = bf16_to_f32(cos_tab[(size_t)pos * D + lane]), sn = bf16_to_f32(sin_tab[(size_t)pos * D + lane]);
-  const float o0 = u0 * cs - u1 * sn, o1 = u1 * cs + u0 * sn;
+  // per-head RMSNorm and rotate-half RoPE (/root/reference/megakernel.cu:490-630, 548-555)
+  float wn[8], cs[8], sn[8];
+  unpack8(*reinterpret_cast<const uint4*>((hd < HQ ? q_norm : k_norm) + 8 * t), wn);
+  unpack8(*reinterpret_cast<const uint4*>(cos_tab + (size_t)pos * D + 8 * (t & 7)), cs);
+  unpack8(*reinterpret_cast<const uint4*>(sin_tab + (size_t)pos * D + 8 * (t & 7)), sn);
+  head_norm_rope(v, wn, cs, sn, t);
   if (hd < HQ) {
-    uint16_t* h = qh + (size_t)b * HQ * D + hd * D;
-    uint16_t* l = ql + (size_t)b * HQ * D + hd * D;
-    const uint16_t h0 = f32_to_bf16(o0), h1 = f32_to_bf16(o1);
-    h[lane] = h0;
-    h[lane + 64] = h1;
-    l[lane] = f32_to_bf16(o0 - bf16_to_f32(h0));
-    l[lane + 64] = f32_to_bf16(o1 - bf16_to_f32(h1));
+    uint4 hi, lo;
+    split8(v, hi, lo);
+    const size_t o = (size_t)b * HQ * D + hd * D + 8 * t;
+    *reinterpret_cast<uint4*>(qh + o) = hi;
+    *reinterpret_cast<uint4*>(ql + o) = lo;
   } else if (page >= 0) {
-    uint16_t* dst = cache_row(k_cache, hd - HQ);
-    dst[lane] = f32_to_bf16(o0);
-    dst[lane + 64] = f32_to_bf16(o1);
+    *reinterpret_cast<uint4*>(k_cache + kv_row(kv, layer, hd - HQ, pos, page) + 8 * t) = pack();
   }
 }
 
@@ -1704,7 +1706,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       q.w0 = (const uint16_t*)lw.q_weight; q.w1 = (const uint16_t*)lw.k_weight; q.w2 = (const uint16_t*)lw.v_weight;
       q.n1 = HQ * D; q.n2 = (HQ + HKV) * D; q.out = wk.raw;
       if ((e = skinny(SK_RAW, dim3(q.N / 16, 1), q)) != hipSuccess) return e;
-      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.raw, 1, M, position,
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(64), 0, st, wk.raw, 1, M, position,
                  (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
                  k_cache, v_cache, l, kv, wk.bad);
       AttnArgs at = at0;
@@ -1755,7 +1757,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       GemmArgs gq = g;
       gq.part = wk.qpart;
       if ((e = launch_gemm<EPI_QKV_PART>(dim3(g.N / NT, mtiles, sq), gq, st)) != hipSuccess) return e;
-      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(256), 0, st, wk.qpart, sq, M, position,
+      MKP_LAUNCH(qkv_post_kernel, dim3((M * (HQ + 2 * HKV) + 3) / 4), dim3(64), 0, st, wk.qpart, sq, M, position,
                  (const uint16_t*)lw.q_norm_weight, (const uint16_t*)lw.k_norm_weight, cos_tab, sin_tab, wk.qh, wk.ql,
                  k_cache, v_cache, l, kv, wk.bad);
     } else if ((e = launch_gemm<EPI_QKV>(dim3(g.N / NT, mtiles), g, st)) != hipSuccess) {
