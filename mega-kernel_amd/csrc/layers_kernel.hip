@@ -1287,9 +1287,9 @@ __global__ void __launch_bounds__(64) qkv_post_kernel(const float* raw, int S, i
 // columns 128 t .. +63 the gate and 128 t + 64 .. +127 the up sums of intermediates 64 t .. +63),
 // added in order, into the down product's A operand (bf16 hi/lo, fragment-major, I columns), as
 // the EPI_SILU epilogue writes it. One thread per row and 8 intermediates.
-__global__ void __launch_bounds__(256) silu_post_kernel(const float* part, int S, int M, int I, uint16_t* bh,
+__global__ void __launch_bounds__(64) silu_post_kernel(const float* part, int S, int M, int I, uint16_t* bh,
                                                         uint16_t* bl) {
-  const int nc = I / 8, idx = blockIdx.x * 256 + threadIdx.x;
+  const int nc = I / 8, idx = blockIdx.x * 64 + threadIdx.x;  // single-wave workgroups: spread over the CUs
   if (idx >= M * nc) return;
   const int m = idx / nc, i0 = 8 * (idx % nc);
   const size_t stride = (size_t)M * 2 * I;
@@ -1781,7 +1781,7 @@ static hipError_t run(const mk_model_dims& dims, const int32_t* tokens, int M, i
       GemmArgs gp = gu;
       gp.part = wk.qpart;
       if ((e = launch_gemm<EPI_SILU_PART>(dim3(I / (NT / 2), mtiles, su), gp, st)) != hipSuccess) return e;
-      MKP_LAUNCH(silu_post_kernel, dim3((M * (I / 8) + 255) / 256), dim3(256), 0, st, wk.qpart, su, M, I, wk.bh, wk.bl);
+      MKP_LAUNCH(silu_post_kernel, dim3((M * (I / 8) + 63) / 64), dim3(64), 0, st, wk.qpart, su, M, I, wk.bh, wk.bl);
     } else if ((e = launch_gemm<EPI_SILU>(dim3(I / (NT / 2), mtiles), gu, st)) != hipSuccess) {
       return e;
     }
